@@ -1,0 +1,58 @@
+// Host-side context: device, stream, scratch workspace, allocation stats and per-kernel
+// timestamps.  Internal to liblocalfold.so (the C ABI in include/localfold.h wraps it).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/localfold.h"
+
+struct lf_context {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  // scratch workspace: one grow-only device buffer carved per call
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  // caller allocations through lf_malloc
+  size_t user_bytes = 0, peak_bytes = 0, alloc_count = 0;
+  std::vector<std::pair<void*, size_t>> user_allocs;
+  // profiling
+  bool profile = false;
+  struct Rec {
+    std::string label;
+    hipEvent_t start, stop;
+  };
+  std::vector<Rec> recs;
+};
+
+namespace lf {
+
+int set_error(int code, const std::string& msg);
+int check_hip(hipError_t e, const char* what);
+
+// Carves `n` buffers from the context workspace (256-byte aligned), growing it if needed.
+// Growing synchronises the stream first, so earlier kernels finish with the old buffer.
+int workspace(lf_context* ctx, const size_t* sizes, void** out, int n);
+
+// Brackets a kernel launch with events when profiling is on.
+struct LaunchScope {
+  lf_context* ctx;
+  int idx = -1;
+  LaunchScope(lf_context* c, const char* label);
+  ~LaunchScope();
+};
+
+}  // namespace lf
+
+#define LF_TRY(expr)            \
+  do {                          \
+    int _rc = (expr);           \
+    if (_rc != LF_OK) return _rc; \
+  } while (0)
+
+#define LF_REQUIRE(cond, msg)                                     \
+  do {                                                            \
+    if (!(cond)) return ::lf::set_error(LF_ERR_INVALID, (msg));   \
+  } while (0)

@@ -1,0 +1,25 @@
+// Host-side helpers shared by the op launchers: weight-record validation and the
+// conversion of an lf_weight into the kernels' logical K x N view.
+#pragma once
+#include <string>
+
+#include "lf_common.h"
+#include "lf_context.h"
+
+namespace lf {
+
+// Validates `w` as a logical [K x N] matrix (K inputs, N outputs) and builds its view.
+// `col_off`/`col_stride` select a strided subset of the stored output columns (AF3's
+// interleaved a/b split); the stored output count must cover them.
+int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off = 0,
+              int col_stride = 1);
+
+inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == LF_BF16; }
+inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }
+
+int tri_mult(lf_context* ctx, const lf_tri_mult_args& a);
+int attention(lf_context* ctx, const lf_attention_args& a);
+int transition(lf_context* ctx, const lf_transition_args& a);
+int outer_product_mean(lf_context* ctx, const lf_opm_args& a);
+
+}  // namespace lf

@@ -1,0 +1,197 @@
+"""Python host over the C ABI, with torch as the device-memory plumbing.
+
+torch supplies device tensors and the stream; every computation goes through
+liblocalfold.so.  The op helpers mirror the reference classes' inputs
+(`webgpu/kernels/triangle/types.js`, `webgpu/kernels/attention.js:15-57`,
+`webgpu/kernels/transition.js:445-460`, `webgpu/kernels/outer-product-mean.js:38-70`):
+numpy weight dicts keyed by the reference's names, uploaded once into DeviceWeights.
+
+A weight value is either a numpy array (float32 values) or a record dict
+{dtype: "float32"|"float16"|"bfloat16"|"int8"|"int5", shape, data, scales?, zeros?,
+ block | channel_axis} (the codec records of shared/weights/dtype.js).
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import capi
+from .capi import check
+
+_DTYPE_CODE = {"float32": capi.LF_F32, "float16": capi.LF_F16, "bfloat16": capi.LF_BF16,
+               "int8": capi.LF_INT8, "int5": capi.LF_INT5}
+_TORCH_ACT = {torch.float32: capi.LF_F32, torch.float16: capi.LF_F16, torch.bfloat16: capi.LF_BF16}
+
+
+def act_code(t: torch.Tensor) -> int:
+    if t.dtype not in _TORCH_ACT:
+        raise TypeError(f"activation dtype {t.dtype} is not float32/float16/bfloat16")
+    return _TORCH_ACT[t.dtype]
+
+
+def ptr(t) -> int:
+    return None if t is None else t.data_ptr()
+
+
+class Context:
+    """An lf_context bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0):
+        self.lib = capi.load()
+        if not torch.cuda.is_available():
+            raise capi.LocalfoldError("no GPU: liblocalfold needs a HIP device (there is no CPU fallback)")
+        self.device = torch.device("cuda", device)
+        torch.cuda.set_device(self.device)
+        h = self.lib.lf_context_create(device)
+        if not h:
+            raise capi.LocalfoldError(self.lib.lf_last_error().decode())
+        self.handle = C.c_void_p(h)
+        self.bind_stream()
+
+    def bind_stream(self, stream=None):
+        s = stream or torch.cuda.current_stream(self.device)
+        check(self.lib.lf_context_set_stream(self.handle, C.c_void_p(s.cuda_stream)))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.lf_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        check(self.lib.lf_synchronize(self.handle))
+
+    def profile(self, enable: bool = True):
+        check(self.lib.lf_profile_enable(self.handle, int(enable)))
+
+    def read_profile(self, max_records: int = 4096):
+        buf = (capi.lf_kernel_timing * max_records)()
+        n = self.lib.lf_profile_read(self.handle, buf, max_records)
+        if n < 0:
+            check(-n)
+        return [(buf[i].label.decode(), float(buf[i].ms)) for i in range(n)]
+
+    def memory_stats(self):
+        cur, peak, cnt = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        check(self.lib.lf_memory_stats(self.handle, C.byref(cur), C.byref(peak), C.byref(cnt)))
+        return {"currentBytes": cur.value, "peakBytes": peak.value, "allocationCount": cnt.value}
+
+
+class DeviceWeights:
+    """Uploads weight records / vectors and keeps the tensors alive while structs point at them."""
+
+    def __init__(self, device):
+        self.device = device
+        self.keep = []
+
+    def vec(self, x):
+        if x is None:
+            return None
+        t = torch.as_tensor(np.ascontiguousarray(np.asarray(x, np.float32)).reshape(-1)).to(self.device)
+        self.keep.append(t)
+        return t.data_ptr()
+
+    def _tensor(self, arr, dtype=None):
+        a = np.ascontiguousarray(arr)
+        t = torch.from_numpy(a.view(np.uint8).copy() if dtype is None else a).to(self.device)
+        self.keep.append(t)
+        return t.data_ptr()
+
+    def weight(self, value, layout: int, dtype_override: str = None) -> capi.lf_weight:
+        """lf_weight for a numpy array (float32) or a codec record, in the given stored layout."""
+        rec = value if isinstance(value, dict) else {"dtype": "float32", "data": np.asarray(value, np.float32),
+                                                     "shape": list(np.shape(value))}
+        if dtype_override and rec["dtype"] == "float32":
+            rec = dict(rec, dtype=dtype_override)
+        shape = list(rec["shape"])
+        if len(shape) != 2:
+            raise ValueError(f"weights must be 2-D, got shape {shape}")
+        w = capi.lf_weight()
+        w.dtype = _DTYPE_CODE[rec["dtype"]]
+        w.layout = layout
+        w.rows, w.cols = shape
+        dt = rec["dtype"]
+        if dt == "float32":
+            w.data = self._tensor(np.asarray(rec["data"], np.float32))
+        elif dt == "float16":
+            w.data = self._tensor(np.asarray(rec["data"], np.float32).astype(np.float16))
+        elif dt == "bfloat16":
+            t = torch.as_tensor(np.asarray(rec["data"], np.float32)).to(torch.bfloat16).to(self.device)
+            self.keep.append(t)
+            w.data = t.data_ptr()
+        else:
+            w.data = self._tensor(np.asarray(rec["data"]))
+            w.scales = self._tensor(np.asarray(rec["scales"], np.float16))
+            if rec.get("zeros") is not None:
+                w.zeros = self._tensor(np.asarray(rec["zeros"], np.float16))
+            if "channel_axis" in rec:
+                out_axis = 1 if layout == capi.LF_IN_OUT else 0
+                if rec["channel_axis"] != out_axis:
+                    raise ValueError("per-channel quantisation must be along the output axis")
+                w.group = 0
+            else:
+                w.group = int(rec["block"])
+        return w
+
+
+# ---------------------------------------------------------------------------------------
+# Triangle multiplication
+# ---------------------------------------------------------------------------------------
+
+def tri_mult_weights(dw: DeviceWeights, w: dict, dialect: int = capi.LF_AF2) -> capi.lf_tri_mult_weights:
+    """Struct for the reference's weight names.
+
+    AF2: the sixteen (out,in) tensors of `webgpu/kernels/triangle/types.js:28-43`.
+    AF3: leftNormInputScale/Offset, projection, gate, centerNormScale/Offset,
+    outputProjection, gatingLinear (all (in,out), `cpu/af3/trunk/pairformer.js:213-300`).
+    """
+    s = capi.lf_tri_mult_weights()
+    if dialect == capi.LF_AF2:
+        s.ln_in_scale, s.ln_in_offset = dw.vec(w["layerNormInWeight"]), dw.vec(w["layerNormInBias"])
+        s.ap = dw.weight(w["linearAPWeight"], capi.LF_OUT_IN)
+        s.ag = dw.weight(w["linearAGWeight"], capi.LF_OUT_IN)
+        s.bp = dw.weight(w["linearBPWeight"], capi.LF_OUT_IN)
+        s.bg = dw.weight(w["linearBGWeight"], capi.LF_OUT_IN)
+        s.ap_bias, s.ag_bias = dw.vec(w["linearAPBias"]), dw.vec(w["linearAGBias"])
+        s.bp_bias, s.bg_bias = dw.vec(w["linearBPBias"]), dw.vec(w["linearBGBias"])
+        s.ln_out_scale, s.ln_out_offset = dw.vec(w["layerNormOutWeight"]), dw.vec(w["layerNormOutBias"])
+        s.wz = dw.weight(w["linearZWeight"], capi.LF_OUT_IN)
+        s.wz_bias = dw.vec(w["linearZBias"])
+        s.wg = dw.weight(w["linearGWeight"], capi.LF_OUT_IN)
+        s.wg_bias = dw.vec(w["linearGBias"])
+    else:
+        s.ln_in_scale, s.ln_in_offset = dw.vec(w["leftNormInputScale"]), dw.vec(w["leftNormInputOffset"])
+        s.ap = dw.weight(w["projection"], capi.LF_IN_OUT)
+        s.ag = dw.weight(w["gate"], capi.LF_IN_OUT)
+        s.ln_out_scale, s.ln_out_offset = dw.vec(w["centerNormScale"]), dw.vec(w["centerNormOffset"])
+        s.wz = dw.weight(w["outputProjection"], capi.LF_IN_OUT)
+        s.wg = dw.weight(w["gatingLinear"], capi.LF_IN_OUT)
+    return s
+
+
+def tri_mult(ctx: Context, z: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf_tri_mult_weights,
+             direction: str = "outgoing", dialect: int = capi.LF_AF2, out: torch.Tensor = None,
+             accumulate: bool = False, epsilon: float = 1e-5, divide_by_length: bool = False) -> torch.Tensor:
+    n, n2, cz = z.shape
+    if n != n2 or tuple(mask.shape) != (n, n) or mask.dtype != torch.float32:
+        raise ValueError("z must be [N, N, cZ] and mask [N, N] float32")
+    if out is None:
+        out = torch.empty_like(z)
+    a = capi.lf_tri_mult_args()
+    a.direction = capi.LF_OUTGOING if direction == "outgoing" else capi.LF_INCOMING
+    a.dialect = dialect
+    a.divide_by_length = int(divide_by_length)
+    a.length, a.c_z = n, cz
+    a.c_hidden = wstruct.wz.cols if wstruct.wz.layout == capi.LF_OUT_IN else wstruct.wz.rows
+    a.act_dtype = act_code(z)
+    a.z, a.mask, a.out = ptr(z), ptr(mask), ptr(out)
+    a.accumulate = int(accumulate)
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_tri_mult(ctx.handle, C.byref(a)))
+    return out

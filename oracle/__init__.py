@@ -1,0 +1,45 @@
+"""CPU oracle for the Evoformer / Pairformer pair-stack path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in `localfold_amd/` imports, links or runs this
+package: only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` use it, and only as the checker (or the timed CPU baseline), never as the
+thing measured or shipped.
+
+It restates, in numpy, the reference's CPU path for the hot path:
+
+* `webgpu/kernels/triangle/cpu-reference.js`  - AF2 triangle multiplication
+* `cpu/af3/trunk/pairformer.js`               - AF3 layer norm, linear, transition,
+                                                triangle multiplication, grid and single
+                                                attention, pairformer block
+* `cpu/af3/trunk/msa.js`                      - AF3 outer-product-mean
+* AF2-only semantics the reference states only as WGSL (`webgpu/kernels/attention.js`,
+  `transition.js`, `outer-product-mean.js`, `webgpu/af2/evoformer/block.js`)
+* the weight codecs of `shared/weights/dtype.js` and the quantisers of
+  `tools/quantize_af3.py` / `tools/quantize_model.py`
+* the deterministic generator of `webgpu/testing/deterministic-input.js`
+
+Arithmetic follows the reference's JS: every intermediate is computed in float64 (JS
+numbers) and stored as float32 (`Float32Array`) at the same points the reference stores
+it.  Each function cites the reference file:line it follows.
+
+Pinning status (what checks each function, in tests/test_oracle.py):
+
+* tri_mult_af2 outgoing   - the four committed fixtures (OpenFold + three AlphaFold captures)
+* tri_mult_af2 incoming   - transpose identity against outgoing on the same fixtures,
+                            plus a brute-force einsum on tiny inputs
+* tri_mult_af3            - reduction to tri_mult_af2 with interleaved weights / no biases
+                            (closed form), and the transposed identity
+* layer_norm / linear     - closed forms (row independence, transposed weights, scale)
+* attention (all modes)   - brute-force per-element softmax loops on tiny inputs;
+                            invariants: one unmasked key -> that value row; transpose
+                            identity; zero bias -> plain attention
+* outer_product_mean      - S=1 closed form and the count identity
+* transitions             - closed forms (ReLU split, SwiGLU blocked split, swish(1))
+* codecs                  - the reference's own int5 boundary cases
+                            (`test/int5-tensor.test.js`), quantise->decode round trips
+* generator               - integer restatement (counter form), checked against a direct
+                            sequential loop
+* evoformer / pairformer block order - composition of the pinned ops (parity of the
+                            composition itself is pinned only by that construction:
+                            the reference's block fixtures are absent from its checkout)
+"""

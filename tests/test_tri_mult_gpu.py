@@ -1,0 +1,123 @@
+"""Triangle multiplication on the GPU through the C ABI, against the oracle and the
+reference's committed fixtures (test/triangle-multiplication-outgoing.gpu.test.js:31-69,
+test/evoformer-triangle-incoming.gpu.test.js:36-85)."""
+import numpy as np
+import pytest
+
+from oracle import ops, prng
+from tests import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(ctx, z, mask, w, direction="outgoing", dialect=0, act=None, accumulate=False, divide=False):
+    import torch
+    from localfold_amd import device as D
+    act = act or torch.float32
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.tri_mult_weights(dw, w, dialect)
+    zt = torch.as_tensor(z).to(ctx.device).to(act)
+    mt = torch.as_tensor(np.asarray(mask, np.float32)).to(ctx.device)
+    out = D.tri_mult(ctx, zt, mt, ws, direction, dialect, accumulate=accumulate, divide_by_length=divide)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), zt.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", H.FIXTURES)
+def test_fixture_outgoing(ctx, name):
+    f = H.load_fixture(name)
+    out, _ = _run(ctx, f["z"], f["mask"], f["weights"])
+    m = H.metrics(out, f["expected"])
+    print(name, m)
+    # the reference's f16 bounds on the same fixtures (mean < 1e-3, max < 1e-2)
+    assert m["meanAbsoluteError"] < 1e-3 and m["maxAbsoluteError"] < 1e-2, m
+
+
+@pytest.mark.parametrize("name", H.FIXTURES)
+def test_fixture_incoming_vs_oracle(ctx, name):
+    f = H.load_fixture(name)
+    out, _ = _run(ctx, f["z"], f["mask"], f["weights"], "incoming")
+    ref = ops.tri_mult_af2(f["z"], f["mask"], f["weights"], "incoming", f["meta"]["epsilon"])
+    m = H.metrics(out, ref)
+    assert m["meanAbsoluteError"] < 1e-3 and m["maxAbsoluteError"] < 1e-2, m
+
+
+@pytest.mark.parametrize("n,cz,ch,seed", [(3, 4, 5, 42), (37, 64, 32, 5), (64, 128, 128, 7), (130, 128, 128, 11)])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_deterministic_input(ctx, n, cz, ch, seed, direction):
+    inp = prng.deterministic_triangle_input(n, cz, ch, seed)
+    out, _ = _run(ctx, inp["z"], inp["mask"], inp["weights"], direction)
+    ref = ops.tri_mult_af2(inp["z"], inp["mask"], inp["weights"], direction)
+    H.assert_close(out, ref, label=f"{n}/{cz}/{ch}/{direction}")
+
+
+@pytest.mark.parametrize("dtype,per_channel", [("float16", False), ("int8", False), ("int5", False),
+                                               ("int8", True), ("int5", True)])
+@pytest.mark.parametrize("act", ["float32", "bfloat16", "float16"])
+def test_quantised_weights_and_activation_dtypes(ctx, dtype, per_channel, act):
+    import torch
+    inp = prng.deterministic_triangle_input(48, 128, 128, 3)
+    rec, dec = H.quantise_weights(inp["weights"], H.TRI_MATS, dtype, per_channel, 0)
+    tdt = getattr(torch, act)
+    for direction in ("outgoing", "incoming"):
+        out, zin = _run(ctx, inp["z"], inp["mask"], rec, direction, act=tdt)
+        ref = ops.tri_mult_af2(zin, inp["mask"], dec, direction)
+        # the update is stored in the activation dtype: add its rounding to the bound
+        H.assert_close(out, ref, max_abs=2e-2, label=f"{dtype}/{per_channel}/{act}/{direction}")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("divide", [False, True])
+def test_af3_dialect(ctx, direction, divide):
+    n, c = 40, 128
+    w = H.af3_tri_weights(c, 21)
+    s = prng.Stream(77)
+    z = s.normal(n * n * c).reshape(n, n, c)
+    mask = np.ones((n, n), np.float32)
+    mask[-4:, :] = 0
+    mask[:, -4:] = 0
+    out, _ = _run(ctx, z, mask, w, direction, dialect=1, divide=divide)
+    ref = ops.tri_mult_af3(z, mask, w, direction, divide_by_length=divide)
+    H.assert_close(out, ref, label=f"af3/{direction}/{divide}")
+
+
+def test_accumulate_in_place(ctx):
+    import torch
+    from localfold_amd import device as D
+    inp = prng.deterministic_triangle_input(33, 128, 128, 9)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.tri_mult_weights(dw, inp["weights"])
+    z = torch.as_tensor(inp["z"]).to(ctx.device)
+    m = torch.as_tensor(inp["mask"]).to(ctx.device)
+    D.tri_mult(ctx, z, m, ws, "outgoing", out=z, accumulate=True)
+    torch.cuda.synchronize()
+    ref = inp["z"].astype(np.float64) + ops.tri_mult_af2(inp["z"], inp["mask"], inp["weights"], "outgoing")
+    H.assert_close(z.cpu().numpy(), ref)
+
+
+def test_config2_full_size(ctx):
+    """BASELINE config 2 at full size: N=384, int5 per-output-channel weights, bf16 pair,
+    last 16 residues masked; outgoing then incoming, each against the oracle."""
+    import torch
+    c2 = H.config2_inputs()
+    out1, zin = _run(ctx, c2["z"], c2["mask"], c2["rec_out"], "outgoing", act=torch.bfloat16)
+    ref1 = ops.tri_mult_af2(zin, c2["mask"], c2["dec_out"], "outgoing")
+    H.assert_close(out1, ref1, label="config2/outgoing")
+    out2, zin2 = _run(ctx, c2["z"], c2["mask"], c2["rec_in"], "incoming", act=torch.bfloat16)
+    ref2 = ops.tri_mult_af2(zin2, c2["mask"], c2["dec_in"], "incoming")
+    H.assert_close(out2, ref2, label="config2/incoming")
+    # masked rows of a and b are zero: the contraction of a fully masked row/column is zero,
+    # so those pairs' update is the gated output bias path only - identical across k.
+    assert np.isfinite(out1).all() and np.isfinite(out2).all()
+
+
+def test_invalid_shapes_rejected(ctx):
+    import torch
+    from localfold_amd import capi, device as D
+    inp = prng.deterministic_triangle_input(4, 8, 8, 1)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.tri_mult_weights(dw, inp["weights"])
+    z = torch.zeros(4, 4, 9, device=ctx.device)       # cZ 9 against weights of 8
+    m = torch.ones(4, 4, device=ctx.device)
+    with pytest.raises(capi.LocalfoldError, match="inputs"):
+        D.tri_mult(ctx, z, m, ws)
