@@ -1,0 +1,176 @@
+"""Benchmark: BASELINE config 2 - standalone triangle multiplicative update, outgoing then
+incoming, N_res = 384, c_z = c_hidden = 128, bf16 pair, int5 weights with per-output-channel
+fp16 scales/zeros, last 16 residues masked.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step = z1 = z0 + tri_out(z0); z2 = z1 + tri_in(z1) through the C ABI (lf_tri_mult, six
+kernels).  Inputs are resident in HBM before the timed region.  Prints ONE JSON line.
+Per-kernel durations come from the library's own hipEvents on the launch stream, in a
+separate profiled pass after the timed steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+N, CZ, CH, MASKED = 384, 128, 128, 16
+PEAK_F16_TFLOPS = 2500.0    # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic(n=N, cz=CZ, ch=CH, act_bytes=2):
+    """Per-direction flops and minimum HBM bytes of each kernel (formulas in DESIGN.md)."""
+    p = n * n
+    return {
+        "project": {"flops": 2 * p * cz * ch * 4, "bytes": p * cz * act_bytes + 2 * p * ch * 2},
+        "contract": {"flops": 2 * n * n * n * ch, "bytes": 2 * p * ch * 2 + p * ch * 2},
+        "output": {"flops": 2 * p * (ch * cz + cz * cz), "bytes": p * ch * 2 + 2 * p * cz * act_bytes},
+    }
+
+
+def cpu_baseline(c2, budget_s=30.0):
+    """The oracle (numpy, float64 compute / float32 storage) on the same workload, host cores."""
+    from oracle import codec, ops
+    dec = lambda w: {k: (codec.decode(v) if isinstance(v, dict) and "dtype" in v else v) for k, v in w.items()}
+    dec_out, dec_in = dec(c2["rec_out"]), dec(c2["rec_in"])
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    z = c2["z"]
+    t0 = time.perf_counter()
+    z1 = z + ops.tri_mult_af2(z, c2["mask"], dec_out, "outgoing")
+    t1 = time.perf_counter()
+    sample = "one full step (outgoing + incoming) at N=384"
+    if (t1 - t0) * 2 < budget_s:
+        ops.tri_mult_af2(z1, c2["mask"], dec_in, "incoming")
+        secs = time.perf_counter() - t0
+    else:
+        secs = (t1 - t0) * 2
+        sample = "outgoing at N=384, doubled for the step"
+    flops = sum(v["flops"] for v in algorithmic().values()) * 2
+    return {"value": round(flops / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": sample + f"; numpy oracle, {secs:.1f} s per step", "ms_per_step": round(secs * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the pair stack's row "
+              "sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from localfold_amd import capi, device as D
+    from localfold_amd import synthetic
+
+    ctx = D.Context(0)
+    dev = ctx.device
+    log("generating config-2 inputs ...")
+    c2 = synthetic.config2_inputs(N, CZ, seed=2, masked_tail=MASKED)
+    dw = D.DeviceWeights(dev)
+    w_out = D.tri_mult_weights(dw, c2["rec_out"])
+    w_in = D.tri_mult_weights(dw, c2["rec_in"])
+    z0 = torch.as_tensor(c2["z"]).to(dev).to(torch.bfloat16)
+    mask = torch.as_tensor(c2["mask"]).to(dev)
+    z1 = torch.empty_like(z0)
+    z2 = torch.empty_like(z0)
+
+    def step():
+        D.tri_mult(ctx, z0, mask, w_out, "outgoing", out=z1, accumulate=True)
+        D.tri_mult(ctx, z1, mask, w_in, "incoming", out=z2, accumulate=True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = start.elapsed_time(stop) / args.steps
+
+    # per-kernel durations: library hipEvents on the launch stream
+    ctx.profile(True)
+    prof_steps = 10
+    for _ in range(prof_steps):
+        step()
+    recs = ctx.read_profile()
+    ctx.profile(False)
+    per = {}
+    for label, t in recs:
+        per.setdefault(label, []).append(t)
+    kern = {k: round(float(np.mean(v)), 4) for k, v in per.items()}
+
+    alg = algorithmic()
+    flops_step = sum(v["flops"] for v in alg.values()) * 2
+    tflops = flops_step / (ms * 1e-3) / 1e12
+    # dominant kernel (largest summed time over both directions)
+    kinds = {}
+    for label, t in kern.items():
+        kinds.setdefault(label.split(".")[1], []).append(t)
+    dom = max(kinds, key=lambda k: sum(kinds[k]))
+    dom_ms = float(np.mean(kinds[dom]))
+    a = alg[dom]
+    ai = a["flops"] / a["bytes"]
+    if ai >= PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        roof = {"bound": "mfma", "achieved": round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2),
+                "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(a["bytes"] / (dom_ms * 1e-3) / 1e9, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["kernel"] = f"tri_*.{dom}"
+    roof["ms_per_launch"] = round(dom_ms, 4)
+    roof["mfma_tflops"] = round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2)
+    roof["traffic"] = None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle ...")
+        cpu = cpu_baseline(c2)
+
+    out = {
+        "metric": "Evoformer block ms at N_res=384/512 + triangle-op TFLOP/s as % of MFMA peak",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: triangle multiplicative update outgoing then incoming, "
+                               "N_res=384, c_z=128, c_hidden=128, bf16 pair, int5 per-output-channel weights, "
+                               "last 16 residues masked",
+                   "N_res": N, "c_z": CZ, "c_hidden": CH, "pair_storage": "bf16", "weights": "int5/per-channel fp16",
+                   "mfma": "f16 operands, f32 accumulation", "parallelism": "single GPU"},
+        "pct_of_mfma_peak": round(100 * tflops / PEAK_F16_TFLOPS, 2),
+        "algorithmic_gflop_per_step": round(flops_step / 1e9, 2),
+        "kernels_ms": kern,
+        "wall_s": round(wall, 3),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

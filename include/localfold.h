@@ -64,7 +64,8 @@ typedef struct {
 /* Replaces the WebGPU device of webgpu/node.js:51-81 / webgpu/runtime/device.js:98. */
 lf_context* lf_context_create(int device_ordinal);
 void lf_context_destroy(lf_context* ctx);
-/* Use an existing hipStream_t (e.g. torch's current stream); NULL selects the context's own. */
+/* Enqueue on an existing hipStream_t (e.g. torch's current stream); NULL is the HIP null stream.
+ * A new context starts on a non-blocking stream of its own. */
 int lf_context_set_stream(lf_context* ctx, void* hip_stream);
 const char* lf_last_error(void);
 const char* lf_version(void);

@@ -134,6 +134,9 @@ lf_context* lf_context_create(int device_ordinal) {
   if (check_hip(hipSetDevice(device_ordinal), "hipSetDevice") != LF_OK) return nullptr;
   lf_context* ctx = new lf_context();
   ctx->device = device_ordinal;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_ordinal) == hipSuccess && cus > 0)
+    ctx->num_cus = cus;
   if (check_hip(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking), "hipStreamCreate") != LF_OK) {
     delete ctx;
     return nullptr;
@@ -158,7 +161,7 @@ void lf_context_destroy(lf_context* ctx) {
 
 int lf_context_set_stream(lf_context* ctx, void* hip_stream) {
   if (!ctx) return set_error(LF_ERR_INVALID, "context is NULL");
-  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+  ctx->stream = static_cast<hipStream_t>(hip_stream);
   return LF_OK;
 }
 

@@ -30,12 +30,12 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// Round-to-nearest-even float -> bf16 (NaN stays NaN).
+// Round-to-nearest-even float -> bf16 (gfx950's v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 h = (__bf16)f;
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
 }
 
 __device__ __forceinline__ float load_act(const void* p, int dt, size_t i) {
@@ -50,7 +50,11 @@ __device__ __forceinline__ void store_act(void* p, int dt, size_t i, float v) {
   else static_cast<uint16_t*>(p)[i] = f2bf(v);
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: ~1 ulp each)
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// 1/sqrt(x) with v_rsq_f32 (~1 ulp)
+__device__ __forceinline__ float rsqrt_(float x) { return __builtin_amdgcn_rsqf(x); }
 
 // A stored weight tensor seen as a logical matrix W[k][n], k < K, n < N.
 // flat stored index = k*ld_k + nphys*ld_n, nphys = col_off + n*col_stride.
@@ -102,50 +106,306 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// LayerNorm of one row of C <= 256 channels by one wave; writes f16 to dst[0..KPAD)
-// (zero past C).  Two-pass statistics (mean, then mean squared deviation) as
-// webgpu/kernels/triangle/cpu-reference.js:5-29, or E[x^2]-E[x]^2 when fast_var
-// (cpu/af3/trunk/pairformer.js:68-87).
-template <int KPAD>
-__device__ __forceinline__ void ln_row_to_lds(_Float16* dst, const void* src, int dt, size_t base, int C,
+// Compile-time activation storage: loads and stores are straight-line code, so a wave can
+// keep many of them in flight (a runtime dtype switch puts every load in its own basic
+// block and the compiler then waits for each one before the next).
+template <int ACT> struct Act;
+template <> struct Act<DT_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float ld(const T* p) { return *p; }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = v; }
+};
+template <> struct Act<DT_F16> {
+  typedef _Float16 T;
+  static __device__ __forceinline__ float ld(const T* p) { return (float)*p; }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = (_Float16)v; }
+};
+template <> struct Act<DT_BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float ld(const T* p) { return bf2f(*p); }
+  static __device__ __forceinline__ void st(T* p, float v) { *p = f2bf(v); }
+};
+
+// Sum over the 4 lanes of a quad (lanes 4q..4q+3) with two DPP quad permutes (VALU only).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
+  return v;
+}
+
+// A tile of 16 activation rows held in registers by one wave, 4 lanes per row: lane l owns
+// row l/4 and the CPL = KPAD/4 consecutive channels (l%4)*CPL.  A tile of row-major rows is
+// one contiguous block of memory, so the 16-byte loads of a wave are fully coalesced, and
+// a row's statistics need only a 4-lane (DPP) reduction.  The words are kept RAW until the
+// tile is normalised, so loads issued for the next tile stay in flight meanwhile.
+template <int ACT, int KPAD>
+struct RowTile {
+  typedef typename Act<ACT>::T T;
+  static constexpr int CPL = KPAD / 4;
+  static constexpr int VEC = 16 / (int)sizeof(T);   // elements per 16-byte load
+  static constexpr int NV = CPL / VEC;
+  static_assert(CPL % VEC == 0, "a lane's channels must be whole 16-byte vectors");
+  uint4 raw[NV];
+  __device__ __forceinline__ float get(int j) const {
+    const T* e = reinterpret_cast<const T*>(raw);
+    return Act<ACT>::ld(e + j);
+  }
+};
+
+// Row r = lane/4 reads src[(row0 + r) * C + c]; rows >= nvalid and channels >= C come from a
+// clamped (valid) address and are discarded when the tile is normalised.
+template <int ACT, int KPAD>
+__device__ __forceinline__ void tile_load(RowTile<ACT, KPAD>& t, const void* src, size_t row0, int nvalid, int C,
+                                          int lane) {
+  typedef RowTile<ACT, KPAD> RT;
+  typedef typename RT::T T;
+  const T* s = static_cast<const T*>(src);
+  const int r = lane >> 2, c0 = (lane & 3) * RT::CPL;
+  const size_t base = (row0 + (r < nvalid ? r : 0)) * (size_t)C;
+  if (C == KPAD) {
+#pragma unroll
+    for (int v = 0; v < RT::NV; ++v) t.raw[v] = *reinterpret_cast<const uint4*>(s + base + c0 + v * RT::VEC);
+  } else {
+    T* e = reinterpret_cast<T*>(t.raw);
+#pragma unroll
+    for (int j = 0; j < RT::CPL; ++j) {
+      const int c = c0 + j;
+      e[j] = s[base + (c < C ? c : 0)];
+    }
+  }
+}
+
+// LayerNorm of the tile's rows written as f16 to dst[r*lda + c], c < KPAD (zero past C and
+// for rows >= nvalid).  gamma/beta: KPAD floats (LDS), 1/0 past C.  Two-pass statistics
+// (mean, then mean squared deviation) as webgpu/kernels/triangle/cpu-reference.js:5-29, or
+// E[x^2]-E[x]^2 when fast_var (cpu/af3/trunk/pairformer.js:68-87).
+template <int ACT, int KPAD>
+__device__ __forceinline__ void tile_ln_store(const RowTile<ACT, KPAD>& t, _Float16* dst, int lda, int nvalid, int C,
                                               const float* gamma, const float* beta, float eps, bool fast_var,
                                               int lane) {
-  constexpr int PER = (KPAD + WAVE - 1) / WAVE;
-  float v[PER];
+  constexpr int CPL = RowTile<ACT, KPAD>::CPL;
+  const int r = lane >> 2, c0 = (lane & 3) * CPL;
+  const bool full = C == KPAD;
+  float x[CPL];
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = lane + j * WAVE;
-    v[j] = c < C ? load_act(src, dt, base + c) : 0.f;
-    s += v[j];
+  for (int j = 0; j < CPL; ++j) {
+    x[j] = (full || c0 + j < C) ? t.get(j) : 0.f;
+    s += x[j];
   }
-  s = wave_sum(s);
-  const float mean = s / (float)C;
+  const float invC = 1.0f / (float)C;
+  const float mean = quad_sum(s) * invC;
   float q = 0.f;
   if (fast_var) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) q += v[j] * v[j];
-    q = wave_sum(q);
-    q = q / (float)C - mean * mean;
+    for (int j = 0; j < CPL; ++j) q += x[j] * x[j];
+    q = quad_sum(q) * invC - mean * mean;
   } else {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int c = lane + j * WAVE;
-      const float d = c < C ? v[j] - mean : 0.f;
+    for (int j = 0; j < CPL; ++j) {
+      const float d = (full || c0 + j < C) ? x[j] - mean : 0.f;
       q += d * d;
     }
-    q = wave_sum(q) / (float)C;
+    q = quad_sum(q) * invC;
   }
-  const float inv = 1.0f / sqrtf(q + eps);
+  const float inv = rsqrt_(q + eps);
+  const bool ok = r < nvalid;
+  _Float16* d = dst + r * lda + c0;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = lane + j * WAVE;
-    if (c < KPAD) {
-      float o = 0.f;
-      if (c < C) o = (v[j] - mean) * inv * (gamma ? gamma[c] : 1.f) + (beta ? beta[c] : 0.f);
-      dst[c] = (_Float16)o;
+  for (int v = 0; v < CPL / 8; ++v) {
+    h8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = v * 8 + k;
+      o[k] = (_Float16)((ok && (full || c0 + j < C)) ? (x[j] - mean) * inv * gamma[c0 + j] + beta[c0 + j] : 0.f);
+    }
+    *reinterpret_cast<h8*>(d + v * 8) = o;
+  }
+}
+
+// LayerNorm, in place, of each of the 16 rows of an f16 LDS tile X[r*ld + c] over its first
+// C of KPAD columns (4 lanes per row, as tile_ln_store).  Rows >= nvalid become zero.
+template <int KPAD>
+__device__ __forceinline__ void lds_ln_inplace(_Float16* X, int ld, int nvalid, int C, const float* gamma,
+                                               const float* beta, float eps, bool fast_var, int lane) {
+  constexpr int CPL = KPAD / 4;
+  const int r = lane >> 2, c0 = (lane & 3) * CPL;
+  _Float16* row = X + r * ld + c0;
+  float x[CPL];
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < CPL / 8; ++v) {
+    const h8 h = *reinterpret_cast<const h8*>(row + v * 8);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x[v * 8 + k] = (c0 + v * 8 + k < C) ? (float)h[k] : 0.f;
+      s += x[v * 8 + k];
     }
   }
+  const float invC = 1.0f / (float)C;
+  const float mean = quad_sum(s) * invC;
+  float q = 0.f;
+  if (fast_var) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) q += x[j] * x[j];
+    q = quad_sum(q) * invC - mean * mean;
+  } else {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float d = c0 + j < C ? x[j] - mean : 0.f;
+      q += d * d;
+    }
+    q = quad_sum(q) * invC;
+  }
+  const float inv = rsqrt_(q + eps);
+  const bool ok = r < nvalid;
+#pragma unroll
+  for (int v = 0; v < CPL / 8; ++v) {
+    h8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = v * 8 + k;
+      o[k] = (_Float16)((ok && c0 + j < C) ? (x[j] - mean) * inv * gamma[c0 + j] + beta[c0 + j] : 0.f);
+    }
+    *reinterpret_cast<h8*>(row + v * 8) = o;
+  }
+}
+
+// ---- MFMA A-fragment row tiles ---------------------------------------------------------
+// For v_mfma_f32_16x16x32_f16 with K = 128 in four k-steps, lane l supplies row l%16 and
+// channels 32*j + 8*(l/16) .. +8 at k-step j.  A FragTile loads a 16-row activation tile
+// straight into that layout (one 16-byte load per k-step for 16-bit storage, two for f32),
+// so the LayerNorm'd rows never touch LDS: a row's 128 channels sit in lanes l, l^16,
+// l^32, l^48 and its statistics take two cross-lane shuffles for all 16 rows at once.
+template <int ACT>
+struct FragTile {
+  typedef typename Act<ACT>::T T;
+  static constexpr int NV = (int)sizeof(T) * 8 / 16;   // uint4 per 8 elements
+  uint4 raw[4][NV];
+  // element e (< 8) of k-step j, decoded with shifts (no address-taken locals)
+  __device__ __forceinline__ float get(int j, int e) const {
+    if constexpr (ACT == DT_F32) {
+      const uint4 q = raw[j][e >> 2];
+      const uint32_t w = (e & 3) == 0 ? q.x : (e & 3) == 1 ? q.y : (e & 3) == 2 ? q.z : q.w;
+      return __uint_as_float(w);
+    } else {
+      const uint4 q = raw[j][0];
+      const uint32_t w = (e >> 1) == 0 ? q.x : (e >> 1) == 1 ? q.y : (e >> 1) == 2 ? q.z : q.w;
+      const uint16_t hbits = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+      if constexpr (ACT == DT_BF16) return bf2f(hbits);
+      else return h2f(hbits);
+    }
+  }
+};
+
+// Row r16 = lane%16 of the tile reads src[(row0 + r16) * C + 32j + 8*(lane/16) + e]; rows
+// >= nvalid and channels >= C come from clamped addresses and are discarded later.
+template <int ACT>
+__device__ __forceinline__ void frag_load(FragTile<ACT>& t, const void* src, size_t row0, int nvalid, int C,
+                                          int lane) {
+  typedef typename FragTile<ACT>::T T;
+  const T* s = static_cast<const T*>(src);
+  const int r = lane & 15, g = lane >> 4;
+  const size_t base = (row0 + (r < nvalid ? r : 0)) * (size_t)C;
+  if (C == 128) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < FragTile<ACT>::NV; ++v)
+        t.raw[j][v] = *reinterpret_cast<const uint4*>(s + base + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      T* e = reinterpret_cast<T*>(t.raw[j]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int c = 32 * j + 8 * g + k;
+        e[k] = s[base + (c < C ? c : 0)];
+      }
+    }
+  }
+}
+
+// 8 floats -> the storage words of 8 activations (bit operations only, so the words stay
+// in registers).
+template <int ACT>
+__device__ __forceinline__ void pack8(const float (&v)[8], uint4 (&o)[FragTile<ACT>::NV]) {
+  if constexpr (ACT == DT_F32) {
+    o[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+    o[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]));
+  } else if constexpr (ACT == DT_BF16) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = (uint32_t)f2bf(v[2 * k]) | ((uint32_t)f2bf(v[2 * k + 1]) << 16);
+    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const h2 hh = h2{(_Float16)v[2 * k], (_Float16)v[2 * k + 1]};
+      w[k] = __builtin_bit_cast(uint32_t, hh);
+    }
+    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__device__ __forceinline__ float lanes4_sum(float v) {   // over lanes l, l^16, l^32, l^48
+  v += __shfl_xor(v, 16, WAVE);
+  v += __shfl_xor(v, 32, WAVE);
+  return v;
+}
+
+// LayerNorm of the 16 rows held as raw values x[j][e] (channel 32j + 8*(lane/16) + e) into
+// f16 A fragments.  gamma/beta: 128 floats (LDS).  Rows >= nvalid give zero fragments.
+__device__ __forceinline__ void frag_ln(const float (&x)[4][8], h8 (&a)[4], int nvalid, int C, const float* gamma,
+                                        const float* beta, float eps, bool fast_var, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[j][e];
+  const float invC = 1.0f / (float)C;
+  const float mean = lanes4_sum(s) * invC;
+  float q = 0.f;
+  if (fast_var) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += x[j][e] * x[j][e];
+    q = lanes4_sum(q) * invC - mean * mean;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (32 * j + 8 * g + e < C) ? x[j][e] - mean : 0.f;
+        q += d * d;
+      }
+    q = lanes4_sum(q) * invC;
+  }
+  const float inv = rsqrt_(q + eps);
+  const bool ok = r < nvalid;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 g0 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g);
+    const float4 g1 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g);
+    const float4 b1 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g + 4);
+    const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool valid = ok && (32 * j + 8 * g + e < C);
+      a[j][e] = (_Float16)(valid ? (x[j][e] - mean) * inv * gg[e] + bb[e] : 0.f);
+    }
+  }
+}
+
+// dst[i] = v[i] when v is non-null and i < n, else dflt; i < cap (block-cooperative).
+__device__ __forceinline__ void stage_vec(float* dst, const float* v, int n, float dflt, int cap, int tid,
+                                          int nthreads) {
+  for (int i = tid; i < cap; i += nthreads) dst[i] = (v && i < n) ? v[i] : dflt;
 }
 
 }  // namespace lf

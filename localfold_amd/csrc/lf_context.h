@@ -10,6 +10,7 @@
 
 struct lf_context {
   int device = 0;
+  int num_cus = 256;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   // scratch workspace: one grow-only device buffer carved per call

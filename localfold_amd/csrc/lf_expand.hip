@@ -1,0 +1,46 @@
+// Weight expansion: the codec records of an op (f32 / f16 / bf16 / int8 / int5, flat-group or
+// per-output-channel tables) decoded on the device into f16 E[n][k] tiles in the workspace,
+// once per op call.  The decode is the reference's readTensorRange arithmetic
+// (shared/weights/dtype.js:212-406): code*scale for int8, fma(code, scale, zero) for int5,
+// exact in float32 before the f16 rounding the MFMA operand needs.
+#include "lf_gemm.h"
+#include "lf_ops.h"
+
+namespace lf {
+
+__global__ __launch_bounds__(256) void expand_weights_kernel(ExpandBatch b) {
+  const int m = blockIdx.y;
+  if (m >= b.count) return;
+  const WView& v = b.v[m];
+  const int kp = b.kp[m];
+  const long total = (long)v.N * kp;
+  for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
+    const int n = (int)(e / kp), k = (int)(e - (long)n * kp);
+    b.dst[m][e] = (_Float16)wdecode(v, k, n);
+  }
+}
+
+int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label) {
+  for (int base = 0; base < count; base += 8) {
+    ExpandBatch b{};
+    b.count = std::min(8, count - base);
+    long most = 0;
+    for (int i = 0; i < b.count; ++i) {
+      const WView& v = views[base + i];
+      b.v[i] = v;
+      b.kp[i] = (v.K + 31) & ~31;
+      b.dst[i] = static_cast<_Float16*>(dst[base + i]);
+      out[base + i] = WExp{b.dst[i], b.kp[i], v.N};
+      most = std::max(most, (long)v.N * b.kp[i]);
+    }
+    LaunchScope ls(ctx, label);
+    dim3 grid((unsigned)std::min<long>((most + 255) / 256, 1024), b.count);
+    hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
+    LF_TRY(check_hip(hipGetLastError(), "expand_weights launch"));
+  }
+  return LF_OK;
+}
+
+size_t expanded_bytes(const WView& v) { return (size_t)v.N * ((v.K + 31) & ~31) * sizeof(_Float16); }
+
+}  // namespace lf

@@ -12,6 +12,35 @@
 
 namespace lf {
 
+// Expanded weights: one matrix decoded to f16 as E[n][k] (k contiguous, row pitch kp,
+// zero past K), written once per op call by expand_weights_kernel into the workspace;
+// the GEMM blocks copy their column chunks from it with 16-byte loads.
+struct WExp {
+  const _Float16* p;
+  int kp;   // row pitch = K rounded up to 32
+  int N;    // valid columns
+};
+
+struct ExpandBatch {
+  WView v[8];
+  _Float16* dst[8];
+  int kp[8];
+  int count;
+};
+
+// Ws[n][k] = E[n_base + n][k] for n < ncols, k < e.kp (zero past the valid columns).
+__device__ __forceinline__ void stage_expanded(_Float16* Ws, int ldw, const WExp& e, int ncols, int n_base, int tid,
+                                               int nthreads) {
+  const int segs = e.kp >> 3;
+  const int total = ncols * segs;
+  for (int i = tid; i < total; i += nthreads) {
+    const int n = i / segs, seg = i - n * segs;
+    h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (n_base + n < e.N) v = *reinterpret_cast<const h8*>(e.p + (size_t)(n_base + n) * e.kp + seg * 8);
+    *reinterpret_cast<h8*>(Ws + n * ldw + seg * 8) = v;
+  }
+}
+
 // Ws[n][k] = W[k][n_base + n] for n < ncols, k < kpad (zero outside the view).
 __device__ __forceinline__ void stage_weights(_Float16* Ws, int ldw, const WView& w, int ncols, int n_base,
                                               int kpad, int tid, int nthreads) {

@@ -3,7 +3,9 @@
 #pragma once
 #include <string>
 
-#include "lf_common.h"
+#include <algorithm>
+
+#include "lf_gemm.h"
 #include "lf_context.h"
 
 namespace lf {
@@ -13,6 +15,10 @@ namespace lf {
 // interleaved a/b split); the stored output count must cover them.
 int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off = 0,
               int col_stride = 1);
+
+// Decodes `count` weight views into f16 E[n][k] tiles at dst[i] (expanded_bytes(views[i]) each).
+int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label);
+size_t expanded_bytes(const WView& v);
 
 inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == LF_BF16; }
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }

@@ -1,15 +1,22 @@
 // Triangle multiplicative update (AF2 and AF3 dialects), three kernels per direction:
 //
-//  tri_project  LN(z) -> a, b = mask * (LN(z) Wp + bp) * sigmoid(LN(z) Wg + bg)
-//               one block = 64 pairs x all hidden channels; a/b stored channel-major
-//               [cH][N*N] f16 (the layout the contraction reads).
-//  tri_contract X[h] = s * A[h] B[h]^T per channel h, 128x128 output tiles on MFMA;
-//               outgoing reads a, b row-major, incoming reads them k-major
-//               (x_ij = sum_k a_kj b_ki).  X stored channel-major f16, pre-scaled by
-//               s = 2^-ceil(log2(N)/2) so a length-long sum stays inside f16's range.
-//  tri_output   LN_out(X) Wz + bz, gated by sigmoid(LN_in(z) Wg + bg), + z residual.
-//               LN_in(z) is recomputed from z rather than stored (one read of z instead
-//               of a write + read of the gate tensor).
+//  project  LN(z) -> a, b = mask * (LN(z) Wp + bp) * sigmoid(LN(z) Wg + bg), stored
+//           channel-major [cH][N*N] f16 (the layout the contraction reads).
+//  contract X[h] = s * A[h] B[h]^T per channel h, 128x128 output tiles on MFMA; outgoing
+//           reads a, b row-major, incoming reads them k-major (x_ij = sum_k a_kj b_ki).
+//           X is stored channel-major f16, pre-scaled by s = 2^-ceil(log2(N)/2) so a
+//           length-long sum stays inside f16's range.
+//  output   LN_out(X) Wz + bz, gated by sigmoid(LN_in(z) Wg + bg), + z residual.  LN_in(z)
+//           is recomputed from z rather than stored (one read of z instead of a write and
+//           a read of the gate tensor).
+//
+// For c_z, c_hidden <= 128 (every AF2/AF3 pair width) project and output run as
+// weight-resident persistent kernels: a block stages all of the op's f16 weights in LDS
+// once and each wave streams 16-row tiles with no block barrier, prefetching the next
+// tile's rows during the current tile's MFMA passes.  Wider channels use the chunked
+// kernels, which re-stage 32/64-column weight chunks per 64-row block.
+//
+// The activation dtype is a template parameter so every load is straight-line code.
 //
 // Semantics: webgpu/kernels/triangle/cpu-reference.js:55-99 (AF2 outgoing),
 // cpu/af3/trunk/pairformer.js:213-300 (AF3, both directions, interleaved split).
@@ -23,65 +30,85 @@ namespace lf {
 
 struct TriProjectParams {
   const void* z;
-  int zdt;
   const float* mask;
   const float *ln_s, *ln_o;
   float eps;
   int fast_var;
   int P, C, H;         // pairs, cZ, cHidden
-  WView wp[2], wg[2];  // [0] -> a, [1] -> b
+  WExp wp[2], wg[2];   // [0] -> a, [1] -> b
   const float *bp[2], *bg[2];
   _Float16* out[2];    // a, b: [H][P]
 };
 
+struct TriOutputParams {
+  const _Float16* X;   // [H][P]
+  const void* z;
+  void* out;
+  int accumulate;
+  const float *ln_in_s, *ln_in_o, *ln_out_s, *ln_out_o;
+  float eps, eps_x;    // eps_x: centre-norm epsilon on the stored (scaled) X
+  int fast_var;
+  int P, C, H;
+  WExp wz, wg;
+  const float *bz, *bg;
+};
+
+// ---------------------------------------------------------------------------------------
+// Chunked kernels (any c_z, c_hidden <= 256)
+// ---------------------------------------------------------------------------------------
+
 constexpr int PJ_ROWS = 64;     // pairs per block (4 waves x 16)
 constexpr int PJ_COLS = 32;     // hidden channels per chunk (32 projection + 32 gate columns)
 
-template <int KPAD>
+template <int ACT, int KPAD>
 __global__ __launch_bounds__(256) void tri_project_kernel(TriProjectParams p) {
   constexpr int LDA = KPAD + 8, LDW = KPAD + 8, LDO = PJ_ROWS + 8;
   __shared__ _Float16 As[PJ_ROWS * LDA];
   __shared__ _Float16 Ws[2 * PJ_COLS * LDW];
   __shared__ _Float16 Os[PJ_COLS * LDO];
+  __shared__ float Gs[2 * KPAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = blockIdx.x * PJ_ROWS;
   const int kloop = (p.C + 31) & ~31;
-
-  for (int r = 0; r < 16; ++r) {
-    const int row = wave * 16 + r, pair = p0 + row;
-    if (pair < p.P)
-      ln_row_to_lds<KPAD>(As + row * LDA, p.z, p.zdt, (size_t)pair * p.C, p.C, p.ln_s, p.ln_o, p.eps, p.fast_var, lane);
-    else
-      for (int c = lane; c < KPAD; c += 64) As[row * LDA + c] = (_Float16)0.f;
+  stage_vec(Gs, p.ln_s, p.C, 1.f, KPAD, tid, 256);
+  stage_vec(Gs + KPAD, p.ln_o, p.C, 0.f, KPAD, tid, 256);
+  __syncthreads();
+  {
+    const int row0 = p0 + wave * 16;
+    RowTile<ACT, KPAD> t;
+    tile_load(t, p.z, (size_t)row0, min(16, p.P - row0), p.C, lane);
+    tile_ln_store(t, As + wave * 16 * LDA, LDA, min(16, p.P - row0), p.C, Gs, Gs + KPAD, p.eps, p.fast_var, lane);
   }
-
   const int hchunks = (p.H + PJ_COLS - 1) / PJ_COLS;
   for (int chunk = 0; chunk < 2 * hchunks; ++chunk) {
     const int which = chunk / hchunks, h0 = (chunk % hchunks) * PJ_COLS;
+    const WExp wpe = which ? p.wp[1] : p.wp[0];
+    const WExp wge = which ? p.wg[1] : p.wg[0];
     __syncthreads();  // As ready / previous chunk done with Ws, Os
-    stage_weights(Ws, LDW, p.wp[which], PJ_COLS, h0, kloop, tid, 256);
-    stage_weights(Ws + PJ_COLS * LDW, LDW, p.wg[which], PJ_COLS, h0, kloop, tid, 256);
+    stage_expanded(Ws, LDW, wpe, PJ_COLS, h0, tid, 256);
+    stage_expanded(Ws + PJ_COLS * LDW, LDW, wge, PJ_COLS, h0, tid, 256);
     __syncthreads();
     f4 acc[1][4];
     zero_acc(acc);
     wave_tile_mfma<1, 4>(acc, As, LDA, wave * 16, Ws, LDW, kloop, lane);
+    const float* bpv = which ? p.bp[1] : p.bp[0];
+    const float* bgv = which ? p.bg[1] : p.bg[0];
     // tiles 0,1: projection columns h0 + 16t + lane%16; tiles 2,3: the gate of the same channel
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int hl = t * 16 + (lane & 15), h = h0 + hl;
-      const float bpv = (p.bp[which] && h < p.H) ? p.bp[which][h] : 0.f;
-      const float bgv = (p.bg[which] && h < p.H) ? p.bg[which][h] : 0.f;
+      const int hl = t * 16 + (lane & 15), h = h0 + hl, hc = h < p.H ? h : 0;
+      const float bpp = bpv ? bpv[hc] : 0.f;
+      const float bgg = bgv ? bgv[hc] : 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = wave * 16 + (lane >> 4) * 4 + i, pair = p0 + row;
-        const float m = pair < p.P ? p.mask[pair] : 0.f;
-        const float v = (acc[0][t][i] + bpv) * (m * sigmoidf_(acc[0][t + 2][i] + bgv));
-        Os[hl * LDO + row] = (_Float16)v;
+        const float m = p.mask[pair < p.P ? pair : 0];
+        const float v = (acc[0][t][i] + bpp) * (m * sigmoidf_(acc[0][t + 2][i] + bgg));
+        Os[hl * LDO + row] = (_Float16)(pair < p.P ? v : 0.f);
       }
     }
     __syncthreads();
-    // coalesced channel-major store: 32 channels x 64 consecutive pairs
-    _Float16* dst = p.out[which];
+    _Float16* dst = which ? p.out[1] : p.out[0];
     if (p0 + PJ_ROWS <= p.P && (p.P & 7) == 0) {
       const int hl = tid >> 3, seg = tid & 7;
       if (h0 + hl < p.H)
@@ -91,6 +118,72 @@ __global__ __launch_bounds__(256) void tri_project_kernel(TriProjectParams p) {
       for (int e = tid; e < PJ_COLS * PJ_ROWS; e += 256) {
         const int hl = e / PJ_ROWS, row = e % PJ_ROWS;
         if (h0 + hl < p.H && p0 + row < p.P) dst[(size_t)(h0 + hl) * p.P + p0 + row] = Os[hl * LDO + row];
+      }
+    }
+  }
+}
+
+constexpr int OT_ROWS = 64, OT_COLS = 64;
+
+template <int ACT, int KZ, int KH>
+__global__ __launch_bounds__(256) void tri_output_kernel(TriOutputParams p) {
+  typedef typename Act<ACT>::T T;
+  constexpr int LDX = KH + 8, LDZ = KZ + 8;
+  __shared__ _Float16 Xs[OT_ROWS * LDX];
+  __shared__ _Float16 Zs[OT_ROWS * LDZ];
+  __shared__ _Float16 Wzs[OT_COLS * LDX];
+  __shared__ _Float16 Wgs[OT_COLS * LDZ];
+  __shared__ float Gs[2 * KZ + 2 * KH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int p0 = blockIdx.x * OT_ROWS;
+  const int kh = (p.H + 31) & ~31, kz = (p.C + 31) & ~31;
+
+  // X tile, transposed into Xs[pair][h]
+  for (int e = tid; e < KH * OT_ROWS; e += 256) {
+    const int h = e / OT_ROWS, r = e % OT_ROWS;
+    const size_t src = (size_t)(h < p.H ? h : 0) * p.P + (p0 + r < p.P ? p0 + r : 0);
+    const _Float16 v = p.X[src];
+    Xs[r * LDX + h] = (h < p.H && p0 + r < p.P) ? v : (_Float16)0.f;
+  }
+  stage_vec(Gs, p.ln_in_s, p.C, 1.f, KZ, tid, 256);
+  stage_vec(Gs + KZ, p.ln_in_o, p.C, 0.f, KZ, tid, 256);
+  stage_vec(Gs + 2 * KZ, p.ln_out_s, p.H, 1.f, KH, tid, 256);
+  stage_vec(Gs + 2 * KZ + KH, p.ln_out_o, p.H, 0.f, KH, tid, 256);
+  __syncthreads();
+  // centre LN over h (in place, scaled-X epsilon) and LN_in of z rows
+  {
+    const int row0 = p0 + wave * 16, nvalid = min(16, p.P - row0);
+    lds_ln_inplace<KH>(Xs + wave * 16 * LDX, LDX, nvalid, p.H, Gs + 2 * KZ, Gs + 2 * KZ + KH, p.eps_x, p.fast_var,
+                       lane);
+    RowTile<ACT, KZ> t;
+    tile_load(t, p.z, (size_t)row0, nvalid, p.C, lane);
+    tile_ln_store(t, Zs + wave * 16 * LDZ, LDZ, nvalid, p.C, Gs, Gs + KZ, p.eps, p.fast_var, lane);
+  }
+  const T* zin = static_cast<const T*>(p.z);
+  T* out = static_cast<T*>(p.out);
+  for (int c0 = 0; c0 < p.C; c0 += OT_COLS) {
+    __syncthreads();
+    stage_expanded(Wzs, LDX, p.wz, OT_COLS, c0, tid, 256);
+    stage_expanded(Wgs, LDZ, p.wg, OT_COLS, c0, tid, 256);
+    __syncthreads();
+    f4 az[1][4], ag[1][4];
+    zero_acc(az);
+    zero_acc(ag);
+    wave_tile_mfma<1, 4>(az, Xs, LDX, wave * 16, Wzs, LDX, kh, lane);
+    wave_tile_mfma<1, 4>(ag, Zs, LDZ, wave * 16, Wgs, LDZ, kz, lane);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int c = c0 + t * 16 + (lane & 15);
+      if (c >= p.C) continue;
+      const float bz = p.bz ? p.bz[c] : 0.f, bg = p.bg ? p.bg[c] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pair = p0 + wave * 16 + (lane >> 4) * 4 + i;
+        if (pair >= p.P) continue;
+        const size_t idx = (size_t)pair * p.C + c;
+        float v = (az[0][t][i] + bz) * sigmoidf_(ag[0][t][i] + bg);
+        if (p.accumulate) v += Act<ACT>::ld(zin + idx);
+        Act<ACT>::st(out + idx, v);
       }
     }
   }
@@ -128,9 +221,10 @@ __device__ __forceinline__ void ct_load(_Float16* S, const _Float16* src, int N,
     }
   } else {
     if (VEC) {
+      // lane -> k, so the eight 2-byte LDS stores of a wave hit 64 consecutive k (no bank conflicts)
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        const int e = tid + it * 256, k = e >> 4, seg = e & 15;
+        const int k = tid & 63, seg = (tid >> 6) + it * 4;
         const int gk = k0 + k, gm = m0 + seg * 8;
         h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
         if (gk < N && gm < N) v = *reinterpret_cast<const h8*>(src + (size_t)gk * N + gm);
@@ -190,113 +284,296 @@ __global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) 
       }
 }
 
-struct TriOutputParams {
-  const _Float16* X;   // [H][P]
-  const void* z;
-  int zdt;
-  void* out;
-  int accumulate;
-  const float *ln_in_s, *ln_in_o, *ln_out_s, *ln_out_o;
-  float eps, eps_x;    // eps_x: centre-norm epsilon on the stored (scaled) X
-  int fast_var;
-  int P, C, H;
-  WView wz, wg;
-  const float *bz, *bg;
-};
+// ---------------------------------------------------------------------------------------
+// Weight-resident persistent kernels (c_z <= 128 and c_hidden <= 128)
+// ---------------------------------------------------------------------------------------
 
-constexpr int OT_ROWS = 64, OT_COLS = 64;
+constexpr int RS_LD = 136;  // 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
 
-template <int KZ, int KH>
-__global__ __launch_bounds__(256) void tri_output_kernel(TriOutputParams p) {
-  constexpr int LDX = KH + 8, LDZ = KZ + 8;
-  __shared__ _Float16 Xs[OT_ROWS * LDX];
-  __shared__ _Float16 Zs[OT_ROWS * LDZ];
-  __shared__ _Float16 Wzs[OT_COLS * LDX];
-  __shared__ _Float16 Wgs[OT_COLS * LDZ];
+__device__ __forceinline__ void stage_resident(_Float16* W, const WExp& e, int tid, int nthreads) {
+  const int segs = e.kp >> 3;
+  for (int i = tid; i < 128 * 16; i += nthreads) {
+    const int n = i >> 4, seg = i & 15;
+    h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (n < e.N && seg < segs) v = *reinterpret_cast<const h8*>(e.p + (size_t)n * e.kp + seg * 8);
+    *reinterpret_cast<h8*>(W + n * RS_LD + seg * 8) = v;
+  }
+}
+
+// Weights of the a/b projections ([h][k] f16, padded rows) and a block of 8 waves; each
+// wave LayerNorms its 16-row tiles straight into MFMA A fragments (FragTile), so LDS holds
+// weights only.
+constexpr int PR_WAVES = 8;
+
+template <int ACT>
+__global__ __launch_bounds__(512) void tri_project_resident_kernel(TriProjectParams p) {
+  __shared__ _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate, b-proj, b-gate as [h][k]
+  __shared__ float Bs[4 * 128];              // the four bias vectors
+  __shared__ float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int p0 = blockIdx.x * OT_ROWS;
-  const int kh = (p.H + 31) & ~31, kz = (p.C + 31) & ~31;
-
-  // X tile, transposed into Xs[pair][h]
-  for (int e = tid; e < KH * OT_ROWS; e += 256) {
-    const int h = e / OT_ROWS, r = e % OT_ROWS;
-    _Float16 v = (_Float16)0.f;
-    if (h < p.H && p0 + r < p.P) v = p.X[(size_t)h * p.P + p0 + r];
-    Xs[r * LDX + h] = v;
-  }
+  stage_resident(Ws, p.wp[0], tid, 512);
+  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, 512);
+  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, 512);
+  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, 512);
+  stage_vec(Bs, p.bp[0], p.H, 0.f, 128, tid, 512);
+  stage_vec(Bs + 128, p.bg[0], p.H, 0.f, 128, tid, 512);
+  stage_vec(Bs + 256, p.bp[1], p.H, 0.f, 128, tid, 512);
+  stage_vec(Bs + 384, p.bg[1], p.H, 0.f, 128, tid, 512);
+  stage_vec(Gs, p.ln_s, p.C, 1.f, 128, tid, 512);
+  stage_vec(Gs + 128, p.ln_o, p.C, 0.f, 128, tid, 512);
   __syncthreads();
-  // centre LN over h (in place), and LN_in of z rows
-  for (int r = 0; r < 16; ++r) {
-    const int row = wave * 16 + r, pair = p0 + row;
-    _Float16* xr = Xs + row * LDX;
-    constexpr int PER = (KH + 63) / 64;
-    float v[PER], s = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int c = lane + j * 64;
-      v[j] = (c < p.H) ? (float)xr[c] : 0.f;
-      s += v[j];
-    }
-    s = wave_sum(s);
-    const float mean = s / (float)p.H;
-    float q = 0.f;
-    if (p.fast_var) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) q += v[j] * v[j];
-      q = wave_sum(q) / (float)p.H - mean * mean;
-    } else {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int c = lane + j * 64;
-        const float d = c < p.H ? v[j] - mean : 0.f;
-        q += d * d;
-      }
-      q = wave_sum(q) / (float)p.H;
-    }
-    const float inv = 1.0f / sqrtf(q + p.eps_x);
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int c = lane + j * 64;
-      if (c < KH) {
-        float o = 0.f;
-        if (c < p.H && pair < p.P)
-          o = (v[j] - mean) * inv * (p.ln_out_s ? p.ln_out_s[c] : 1.f) + (p.ln_out_o ? p.ln_out_o[c] : 0.f);
-        xr[c] = (_Float16)o;
-      }
-    }
-    if (pair < p.P)
-      ln_row_to_lds<KZ>(Zs + row * LDZ, p.z, p.zdt, (size_t)pair * p.C, p.C, p.ln_in_s, p.ln_in_o, p.eps, p.fast_var,
-                        lane);
-    else
-      for (int c = lane; c < KZ; c += 64) Zs[row * LDZ + c] = (_Float16)0.f;
-  }
 
-  for (int c0 = 0; c0 < p.C; c0 += OT_COLS) {
-    __syncthreads();
-    stage_weights(Wzs, LDX, p.wz, OT_COLS, c0, kh, tid, 256);
-    stage_weights(Wgs, LDZ, p.wg, OT_COLS, c0, kz, tid, 256);
-    __syncthreads();
-    f4 az[1][4], ag[1][4];
-    zero_acc(az);
-    zero_acc(ag);
-    wave_tile_mfma<1, 4>(az, Xs, LDX, wave * 16, Wzs, LDX, kh, lane);
-    wave_tile_mfma<1, 4>(ag, Zs, LDZ, wave * 16, Wgs, LDZ, kz, lane);
+  const int r16 = lane & 15, g = lane >> 4, q4 = g * 4, kq = g * 8;
+  const int ntiles = (p.P + 15) >> 4, stride = gridDim.x * PR_WAVES;
+  const bool vec_store = (p.P & 3) == 0;
+  // Loads for tile t+1 (rows and mask) are issued before tile t's stores: gfx9 counts loads
+  // and stores on one in-order counter, so a wait on anything issued after a store would
+  // also wait for the store.
+  FragTile<ACT> t;
+  float mnext[4];
+  auto prefetch = [&](int tl) {
+    const int r0 = tl * 16, nv = min(16, p.P - r0);
+    frag_load(t, p.z, (size_t)r0, nv, p.C, lane);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int c = c0 + t * 16 + (lane & 15);
-      if (c >= p.C) continue;
-      const float bz = p.bz ? p.bz[c] : 0.f, bg = p.bg ? p.bg[c] : 0.f;
+    for (int i = 0; i < 4; ++i) mnext[i] = p.mask[r0 + (q4 + i < nv ? q4 + i : 0)];
+  };
+  int tile = blockIdx.x * PR_WAVES + wave;
+  if (tile < ntiles) prefetch(tile);
+  for (; tile < ntiles; tile += stride) {
+    const int row0 = tile * 16, nvalid = min(16, p.P - row0);
+    h8 a[4];
+    {
+      float x[4][8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pair = p0 + wave * 16 + (lane >> 4) * 4 + i;
-        if (pair >= p.P) continue;
-        const size_t idx = (size_t)pair * p.C + c;
-        float v = (az[0][t][i] + bz) * sigmoidf_(ag[0][t][i] + bg);
-        if (p.accumulate) v += load_act(p.z, p.zdt, idx);
-        store_act(p.out, p.zdt, idx, v);
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + kq + e < p.C) ? t.get(j, e) : 0.f;
+      frag_ln(x, a, nvalid, p.C, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    }
+    float m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = q4 + i < nvalid ? mnext[i] : 0.f;
+    const int next = tile + stride;
+    if (next < ntiles) prefetch(next);
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+      const int which = pass >> 1, hh = (pass & 1) * 64;
+      const _Float16* Wp = Ws + (which * 2) * 128 * RS_LD;
+      const _Float16* Wg = Wp + 128 * RS_LD;
+      f4 acc[8];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const h8 bp = *reinterpret_cast<const h8*>(Wp + (hh + t4 * 16 + r16) * RS_LD + kq);
+        const h8 bg = *reinterpret_cast<const h8*>(Wg + (hh + t4 * 16 + r16) * RS_LD + kq);
+        acc[t4] = mfma16(a[0], bp, f4{0.f, 0.f, 0.f, 0.f});
+        acc[4 + t4] = mfma16(a[0], bg, f4{0.f, 0.f, 0.f, 0.f});
+      }
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        __builtin_amdgcn_sched_barrier(0);   // keep one k-step's fragments live at a time
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const h8 bp = *reinterpret_cast<const h8*>(Wp + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+          const h8 bg = *reinterpret_cast<const h8*>(Wg + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+          acc[t4] = mfma16(a[j], bp, acc[t4]);
+          acc[4 + t4] = mfma16(a[j], bg, acc[4 + t4]);
+        }
+      }
+      _Float16* dst = which ? p.out[1] : p.out[0];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int h = hh + t4 * 16 + r16;
+        if (h >= p.H) continue;
+        const float bpp = Bs[which * 256 + h], bgg = Bs[which * 256 + 128 + h];
+        h4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (_Float16)((acc[t4][i] + bpp) * (m[i] * sigmoidf_(acc[4 + t4][i] + bgg)));
+        _Float16* d = dst + (size_t)h * p.P + row0 + q4;
+        if (vec_store && q4 + 4 <= nvalid) {
+          *reinterpret_cast<h4*>(d) = o;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (q4 + i < nvalid) d[i] = o[i];
+        }
       }
     }
   }
+}
+
+constexpr int OR_WAVES = 8;
+constexpr int OR_SCR = 16 * 132;   // floats of per-wave scratch: X^T tile (f16) then the f32 update
+
+template <int ACT>
+__global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParams p) {
+  typedef typename Act<ACT>::T T;
+  __shared__ _Float16 Wz[128 * RS_LD];   // [c][h]
+  __shared__ _Float16 Wg[128 * RS_LD];   // [c][k]
+  __shared__ float Scr[OR_WAVES * OR_SCR];
+  __shared__ float Vs[6 * 128];           // bz, bg, centre-norm scale/offset, LN_in scale/offset
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  stage_resident(Wz, p.wz, tid, 512);
+  stage_resident(Wg, p.wg, tid, 512);
+  stage_vec(Vs, p.bz, p.C, 0.f, 128, tid, 512);
+  stage_vec(Vs + 128, p.bg, p.C, 0.f, 128, tid, 512);
+  stage_vec(Vs + 256, p.ln_out_s, p.H, 1.f, 128, tid, 512);
+  stage_vec(Vs + 384, p.ln_out_o, p.H, 0.f, 128, tid, 512);
+  stage_vec(Vs + 512, p.ln_in_s, p.C, 1.f, 128, tid, 512);
+  stage_vec(Vs + 640, p.ln_in_o, p.C, 0.f, 128, tid, 512);
+  __syncthreads();
+
+  const int r16 = lane & 15, g = lane >> 4, q4 = g * 4, kq = g * 8;
+  const int ntiles = (p.P + 15) >> 4, stride = gridDim.x * OR_WAVES;
+  _Float16* Xw = reinterpret_cast<_Float16*>(Scr + wave * OR_SCR);   // [16][RS_LD] f16
+  float* Ow = Scr + wave * OR_SCR;                                    // [16][132] f32
+  const bool vec_x = (p.P & 7) == 0;
+  const T* zin = static_cast<const T*>(p.z);
+  T* out = static_cast<T*>(p.out);
+  // No cross-tile prefetch here: holding the next tile's X and z words across the two GEMMs
+  // pushes this kernel past 256 VGPRs (spills); two waves per SIMD hide the loads instead.
+  FragTile<ACT> t;
+  for (int tile = blockIdx.x * OR_WAVES + wave; tile < ntiles; tile += stride) {
+    const int row0 = tile * 16, nvalid = min(16, p.P - row0);
+    // X tile [h][16 rows] -> Xw[row][h]; z rows into A-fragment layout
+    frag_load(t, p.z, (size_t)row0, nvalid, p.C, lane);
+    if (vec_x && nvalid == 16) {
+      h8 xv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+        xv[j] = *reinterpret_cast<const h8*>(p.X + (size_t)(h < p.H ? h : 0) * p.P + row0 + seg * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) Xw[(seg * 8 + jj) * RS_LD + h] = h < p.H ? xv[j][jj] : (_Float16)0.f;
+      }
+    } else {
+#pragma unroll 1
+      for (int idx = lane; idx < 128 * 16; idx += 64) {
+        const int h = idx >> 4, r = idx & 15;
+        const _Float16 v = p.X[(size_t)(h < p.H ? h : 0) * p.P + row0 + (r < nvalid ? r : 0)];
+        Xw[r * RS_LD + h] = (h < p.H && r < nvalid) ? v : (_Float16)0.f;
+      }
+    }
+    // centre LN over h into A fragments (scaled-X epsilon); LN_in(z) into A fragments
+    h8 ax[4], az[4];
+    {
+      float x[4][8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h8 v = *reinterpret_cast<const h8*>(Xw + r16 * RS_LD + 32 * j + kq);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][e] = (float)v[e];
+      }
+      frag_ln(x, ax, nvalid, p.H, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + kq + e < p.C) ? t.get(j, e) : 0.f;
+      frag_ln(x, az, nvalid, p.C, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+    }
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      const int c0 = pass * 64;
+      f4 accz[4], accg[4];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        accz[t4] = mfma16(ax[0], *reinterpret_cast<const h8*>(Wz + (c0 + t4 * 16 + r16) * RS_LD + kq),
+                          f4{0.f, 0.f, 0.f, 0.f});
+        accg[t4] = mfma16(az[0], *reinterpret_cast<const h8*>(Wg + (c0 + t4 * 16 + r16) * RS_LD + kq),
+                          f4{0.f, 0.f, 0.f, 0.f});
+      }
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        __builtin_amdgcn_sched_barrier(0);   // keep one k-step's fragments live at a time
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          accz[t4] = mfma16(ax[j], *reinterpret_cast<const h8*>(Wz + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq),
+                            accz[t4]);
+          accg[t4] = mfma16(az[j], *reinterpret_cast<const h8*>(Wg + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq),
+                            accg[t4]);
+        }
+      }
+      // stage the gated update as f32 [row][c] (Xw is dead: its fragments are in registers)
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int c = c0 + t4 * 16 + r16;
+        const float bz = Vs[c], bg = Vs[128 + c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ow[(q4 + i) * 132 + c] = (accz[t4][i] + bz) * sigmoidf_(accg[t4][i] + bg);
+      }
+    }
+    // lane: row r16, channels 32j + 8g .. +8; the residual rows are re-read (L2-resident: this
+    // wave loaded them one tile ago) instead of being held in registers across the GEMMs.
+    FragTile<ACT> zraw;
+    if (p.accumulate) frag_load(zraw, p.z, (size_t)row0, nvalid, p.C, lane);
+    if (r16 < nvalid) {
+      T* orow = out + (size_t)(row0 + r16) * p.C;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 u0 = *reinterpret_cast<const float4*>(Ow + r16 * 132 + 32 * j + kq);
+        const float4 u1 = *reinterpret_cast<const float4*>(Ow + r16 * 132 + 32 * j + kq + 4);
+        const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        if (p.C == 128) {
+          float w8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) w8[e] = p.accumulate ? u[e] + zraw.get(j, e) : u[e];
+          uint4 o[FragTile<ACT>::NV];
+          pack8<ACT>(w8, o);
+#pragma unroll
+          for (int v = 0; v < FragTile<ACT>::NV; ++v)
+            *reinterpret_cast<uint4*>(orow + 32 * j + kq + v * (16 / (int)sizeof(T))) = o[v];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int c = 32 * j + kq + e;
+            if (c < p.C) Act<ACT>::st(orow + c, p.accumulate ? u[e] + Act<ACT>::ld(zin + (size_t)(row0 + r16) * p.C + c) : u[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int ACT>
+static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool resident, int kz) {
+  const int P = pp.P;
+  if (resident) {
+    const int tiles = (P + 15) / 16;
+    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + PR_WAVES - 1) / PR_WAVES)));
+    hipLaunchKernelGGL(tri_project_resident_kernel<ACT>, g, dim3(512), 0, ctx->stream, pp);
+    return;
+  }
+  dim3 grid((P + PJ_ROWS - 1) / PJ_ROWS);
+  if (kz == 64) hipLaunchKernelGGL((tri_project_kernel<ACT, 64>), grid, dim3(256), 0, ctx->stream, pp);
+  else if (kz == 128) hipLaunchKernelGGL((tri_project_kernel<ACT, 128>), grid, dim3(256), 0, ctx->stream, pp);
+  else hipLaunchKernelGGL((tri_project_kernel<ACT, 256>), grid, dim3(256), 0, ctx->stream, pp);
+}
+
+template <int ACT>
+static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resident, int kz, int kh) {
+  const int P = op.P;
+  if (resident) {
+    const int tiles = (P + 15) / 16;
+    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + OR_WAVES - 1) / OR_WAVES)));
+    hipLaunchKernelGGL(tri_output_resident_kernel<ACT>, g, dim3(512), 0, ctx->stream, op);
+    return;
+  }
+  dim3 grid((P + OT_ROWS - 1) / OT_ROWS);
+#define LF_TO(KZ_, KH_) \
+  if (kz == KZ_ && kh == KH_) hipLaunchKernelGGL((tri_output_kernel<ACT, KZ_, KH_>), grid, dim3(256), 0, ctx->stream, op)
+  LF_TO(64, 64);
+  else LF_TO(64, 128);
+  else LF_TO(64, 256);
+  else LF_TO(128, 64);
+  else LF_TO(128, 128);
+  else LF_TO(128, 256);
+  else LF_TO(256, 64);
+  else LF_TO(256, 128);
+  else LF_TO(256, 256);
+#undef LF_TO
 }
 
 static int kpad_of(int c) { return c <= 64 ? 64 : (c <= 128 ? 128 : 256); }
@@ -316,8 +593,8 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   const int P = N * N;
 
   TriProjectParams pp{};
+  WView views[6];  // a-proj, a-gate, b-proj, b-gate, output, gate
   pp.z = a.z;
-  pp.zdt = a.act_dtype;
   pp.mask = a.mask;
   pp.ln_s = w.ln_in_scale;
   pp.ln_o = w.ln_in_offset;
@@ -329,10 +606,10 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   if (a.dialect == LF_AF2) {
     LF_REQUIRE(w.ln_in_scale && w.ln_in_offset && w.ln_out_scale && w.ln_out_offset,
                "tri_mult: AF2 layer norms need scale and offset");
-    LF_TRY(make_view(w.ap, C, H, "linearAPWeight", &pp.wp[0]));
-    LF_TRY(make_view(w.ag, C, H, "linearAGWeight", &pp.wg[0]));
-    LF_TRY(make_view(w.bp, C, H, "linearBPWeight", &pp.wp[1]));
-    LF_TRY(make_view(w.bg, C, H, "linearBGWeight", &pp.wg[1]));
+    LF_TRY(make_view(w.ap, C, H, "linearAPWeight", &views[0]));
+    LF_TRY(make_view(w.ag, C, H, "linearAGWeight", &views[1]));
+    LF_TRY(make_view(w.bp, C, H, "linearBPWeight", &views[2]));
+    LF_TRY(make_view(w.bg, C, H, "linearBGWeight", &views[3]));
     pp.bp[0] = w.ap_bias;
     pp.bg[0] = w.ag_bias;
     pp.bp[1] = w.bp_bias;
@@ -340,30 +617,40 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
     pp.fast_var = 0;
   } else {
     LF_REQUIRE(H == C, "tri_mult: AF3 dialect needs c_hidden == c_z");
-    LF_TRY(make_view(w.ap, C, C, "projection(a)", &pp.wp[0], 0, 2));
-    LF_TRY(make_view(w.ap, C, C, "projection(b)", &pp.wp[1], 1, 2));
-    LF_TRY(make_view(w.ag, C, C, "gate(a)", &pp.wg[0], 0, 2));
-    LF_TRY(make_view(w.ag, C, C, "gate(b)", &pp.wg[1], 1, 2));
+    LF_TRY(make_view(w.ap, C, C, "projection(a)", &views[0], 0, 2));
+    LF_TRY(make_view(w.ag, C, C, "gate(a)", &views[1], 0, 2));
+    LF_TRY(make_view(w.ap, C, C, "projection(b)", &views[2], 1, 2));
+    LF_TRY(make_view(w.ag, C, C, "gate(b)", &views[3], 1, 2));
     pp.fast_var = 1;
   }
-  LF_TRY(make_view(w.wz, H, C, "linearZWeight", &op.wz));
-  LF_TRY(make_view(w.wg, C, C, "linearGWeight", &op.wg));
+  LF_TRY(make_view(w.wz, H, C, "linearZWeight", &views[4]));
+  LF_TRY(make_view(w.wg, C, C, "linearGWeight", &views[5]));
 
   const size_t plane = (size_t)H * P * sizeof(_Float16);
-  size_t sizes[3] = {plane, plane, plane};
-  void* bufs[3];
-  LF_TRY(workspace(ctx, sizes, bufs, 3));
+  size_t sizes[9] = {plane, plane, plane};
+  for (int i = 0; i < 6; ++i) sizes[3 + i] = expanded_bytes(views[i]);
+  void* bufs[9];
+  LF_TRY(workspace(ctx, sizes, bufs, 9));
   pp.out[0] = static_cast<_Float16*>(bufs[0]);
   pp.out[1] = static_cast<_Float16*>(bufs[1]);
   _Float16* X = static_cast<_Float16*>(bufs[2]);
+  WExp ex[6];
+  LF_TRY(expand_weights(ctx, views, 6, bufs + 3, ex,
+                        a.direction == LF_OUTGOING ? "tri_out.expand" : "tri_in.expand"));
+  pp.wp[0] = ex[0];
+  pp.wg[0] = ex[1];
+  pp.wp[1] = ex[2];
+  pp.wg[1] = ex[3];
+  op.wz = ex[4];
+  op.wg = ex[5];
 
   const int kz = kpad_of(C), kh = kpad_of(H);
+  const bool resident = C <= 128 && H <= 128 && N >= 16;
   {
     LaunchScope ls(ctx, a.direction == LF_OUTGOING ? "tri_out.project" : "tri_in.project");
-    dim3 grid((P + PJ_ROWS - 1) / PJ_ROWS);
-    if (kz == 64) hipLaunchKernelGGL(tri_project_kernel<64>, grid, dim3(256), 0, ctx->stream, pp);
-    else if (kz == 128) hipLaunchKernelGGL(tri_project_kernel<128>, grid, dim3(256), 0, ctx->stream, pp);
-    else hipLaunchKernelGGL(tri_project_kernel<256>, grid, dim3(256), 0, ctx->stream, pp);
+    if (a.act_dtype == LF_F32) launch_project<DT_F32>(ctx, pp, resident, kz);
+    else if (a.act_dtype == LF_F16) launch_project<DT_F16>(ctx, pp, resident, kz);
+    else launch_project<DT_BF16>(ctx, pp, resident, kz);
   }
   LF_TRY(check_hip(hipGetLastError(), "tri_project launch"));
 
@@ -395,7 +682,6 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   const double c = (a.dialect == LF_AF3 && a.divide_by_length ? 1.0 / N : 1.0) / scale;
   op.X = X;
   op.z = a.z;
-  op.zdt = a.act_dtype;
   op.out = a.out;
   op.accumulate = a.accumulate;
   op.ln_in_s = w.ln_in_scale;
@@ -412,19 +698,9 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   op.bg = a.dialect == LF_AF2 ? w.wg_bias : nullptr;
   {
     LaunchScope ls(ctx, outgoing ? "tri_out.output" : "tri_in.output");
-    dim3 grid((P + OT_ROWS - 1) / OT_ROWS);
-#define LF_TO(KZ_, KH_) \
-  if (kz == KZ_ && kh == KH_) hipLaunchKernelGGL((tri_output_kernel<KZ_, KH_>), grid, dim3(256), 0, ctx->stream, op)
-    LF_TO(64, 64);
-    else LF_TO(64, 128);
-    else LF_TO(64, 256);
-    else LF_TO(128, 64);
-    else LF_TO(128, 128);
-    else LF_TO(128, 256);
-    else LF_TO(256, 64);
-    else LF_TO(256, 128);
-    else LF_TO(256, 256);
-#undef LF_TO
+    if (a.act_dtype == LF_F32) launch_output<DT_F32>(ctx, op, resident, kz, kh);
+    else if (a.act_dtype == LF_F16) launch_output<DT_F16>(ctx, op, resident, kz, kh);
+    else launch_output<DT_BF16>(ctx, op, resident, kz, kh);
   }
   return check_hip(hipGetLastError(), "tri_output launch");
 }

@@ -65,58 +65,3 @@ def pairformer_block_af3(pair, single, pair_mask, seq_mask, w, swap_transposed_b
     single = _add(single, ops.transition_af3(single, w["singleTransition"], eps=eps))
     assert logits.shape == (heads, n, n)
     return pair, single
-
-
-def synthetic_pairformer_weights(c_z, c_s, heads_pair, heads_single, dim_single, seed=3, factor=4):
-    """Random-init AF3 pairformer block weights (N(0, 1/fan_in) masters, LN scale ~1).
-
-    The reference has no AF3 synthetic generator; this uses the same `generator(seed)`
-    stream with Box-Muller normals (oracle.prng.Stream.normal).
-    """
-    from .prng import Stream
-    s = Stream(seed)
-
-    def lin(i, o):
-        return s.normal(i * o, 1.0 / np.sqrt(i)).reshape(i, o)
-
-    def ln(c):
-        return s.values(c, 0.2, 1), s.values(c, 0.1)
-
-    def tri():
-        sc, of = ln(c_z)
-        cs, co = ln(c_z)
-        return {"leftNormInputScale": sc, "leftNormInputOffset": of,
-                "projection": lin(c_z, 2 * c_z), "gate": lin(c_z, 2 * c_z),
-                "centerNormScale": cs, "centerNormOffset": co,
-                "outputProjection": lin(c_z, c_z), "gatingLinear": lin(c_z, c_z)}
-
-    def grid(heads, dim):
-        sc, of = ln(c_z)
-        w = heads * dim
-        return {"heads": heads, "dimension": dim, "actNormScale": sc, "actNormOffset": of,
-                "pairBiasProjection": lin(c_z, heads),
-                "qProjection": lin(c_z, w).T.copy(), "kProjection": lin(c_z, w).T.copy(),
-                "vProjection": lin(c_z, w), "gatingQuery": lin(c_z, w).T.copy(),
-                "outputProjection": lin(w, c_z)}
-
-    def trans(c):
-        sc, of = ln(c)
-        return {"inputLayerNormScale": sc, "inputLayerNormOffset": of,
-                "transition1": lin(c, 2 * factor * c), "transition2": lin(factor * c, c)}
-
-    w = {"triangleMultiplicationOutgoing": tri(), "triangleMultiplicationIncoming": tri(),
-         "pairAttention1": grid(heads_pair, c_z // heads_pair),
-         "pairAttention2": grid(heads_pair, c_z // heads_pair),
-         "pairTransition": trans(c_z)}
-    sc, of = ln(c_z)
-    w["singlePairLogitsNormScale"], w["singlePairLogitsNormOffset"] = sc, of
-    w["singlePairLogitsProjection"] = lin(c_z, heads_single)
-    sc, of = ln(c_s)
-    hw = heads_single * dim_single
-    w["singleAttention"] = {"heads": heads_single, "dimension": dim_single,
-                            "layerNormScale": sc, "layerNormOffset": of,
-                            "qProjection": lin(c_s, hw), "qBias": s.values(hw, 0.1),
-                            "kProjection": lin(c_s, hw), "vProjection": lin(c_s, hw),
-                            "gatingQuery": lin(c_s, hw), "outputProjection": lin(hw, c_s)}
-    w["singleTransition"] = trans(c_s)
-    return w

@@ -67,12 +67,12 @@ def _contract(a, b, direction):
 
     `cpu-reference.js:76-88` (outgoing, f64 accumulator) and `pairformer.js:247-258` (both).
     """
-    a = np.asarray(a, F64).transpose(2, 0, 1)   # [H, N, N]
-    b = np.asarray(b, F64).transpose(2, 0, 1)
+    a = np.ascontiguousarray(np.asarray(a, F64).transpose(2, 0, 1))   # [H, N, N]
+    b = np.ascontiguousarray(np.asarray(b, F64).transpose(2, 0, 1))
     if direction == "outgoing":
-        x = a @ b.transpose(0, 2, 1)           # [H, i, j] = sum_k a[h,i,k] b[h,j,k]
+        x = np.matmul(a, np.ascontiguousarray(b.transpose(0, 2, 1)))    # [H, i, j] = sum_k a[h,i,k] b[h,j,k]
     elif direction == "incoming":
-        x = b.transpose(0, 2, 1) @ a           # [H, i, j] = sum_k b[h,k,i] a[h,k,j]
+        x = np.matmul(np.ascontiguousarray(b.transpose(0, 2, 1)), a)    # [H, i, j] = sum_k b[h,k,i] a[h,k,j]
     else:
         raise ValueError(direction)
     return x.transpose(1, 2, 0)                # [i, j, H]

@@ -4,7 +4,8 @@ from pathlib import Path
 
 import numpy as np
 
-from oracle import codec, ops, prng
+from localfold_amd import synthetic as S
+from oracle import codec, ops
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 FIXTURES = ["openfold_triangle_small", "af2_single_short9", "af2_single_model1_59", "af2_a3m_model1_59"]
@@ -31,58 +32,24 @@ def assert_close(actual, expected, max_abs=MAX_ABS, rel_fro=REL_FRO, label=""):
     return m
 
 
+def decoded(recs: dict) -> dict:
+    """Oracle view of a weight dict: every codec record decoded to float32."""
+    return {k: (codec.decode(v) if isinstance(v, dict) and "dtype" in v else v) for k, v in recs.items()}
+
+
 def quantise_weights(w: dict, names, dtype: str, per_channel: bool, out_axis: int):
     """Returns (records for the kernels, decoded float32 arrays for the oracle)."""
-    recs, dec = dict(w), dict(w)
-    for name in names:
-        if dtype == "float32":
-            continue
-        if dtype in ("float16",):
-            rec = codec.make_record(w[name], "float16")
-        elif per_channel:
-            rec = codec.make_record(w[name], dtype, channel_axis=out_axis)
-        else:
-            rec = codec.make_record(w[name], dtype)
-        recs[name] = rec
-        dec[name] = codec.decode(rec)
-    return recs, dec
+    recs = S.quantise_records(w, names, dtype, per_channel, out_axis)
+    return recs, decoded(recs)
 
 
-TRI_MATS = ["linearAPWeight", "linearAGWeight", "linearBPWeight", "linearBGWeight", "linearZWeight", "linearGWeight"]
-TRI3_MATS = ["projection", "gate", "outputProjection", "gatingLinear"]
+TRI_MATS = S.TRI_MATS
+TRI3_MATS = S.TRI3_MATS
+af3_tri_weights = S.af3_tri_weights
 
 
-def af3_tri_weights(c, seed):
-    s = prng.Stream(seed)
-    r = 1.0 / np.sqrt(c)
-    return {"leftNormInputScale": s.values(c, 0.2, 1), "leftNormInputOffset": s.values(c, 0.1),
-            "projection": s.normal(c * 2 * c, r).reshape(c, 2 * c), "gate": s.normal(c * 2 * c, r).reshape(c, 2 * c),
-            "centerNormScale": s.values(c, 0.2, 1), "centerNormOffset": s.values(c, 0.1),
-            "outputProjection": s.normal(c * c, r).reshape(c, c), "gatingLinear": s.normal(c * c, r).reshape(c, c)}
-
-
-def config2_inputs(n=384, c=128, seed=2, masked_tail=16):
-    """z ~N(0,1), weights N(0,1/fan_in) masters quantised int5 per output channel,
-    mask ones except the last `masked_tail` residues (rows and columns)."""
-    s = prng.Stream(seed)
-    z = s.normal(n * n * c).reshape(n, n, c)
-    mask = np.ones((n, n), np.float32)
-    if masked_tail:
-        mask[n - masked_tail:, :] = 0
-        mask[:, n - masked_tail:] = 0
-
-    def tri(seed_off):
-        t = prng.Stream(seed + 100 + seed_off)
-        rz = 1.0 / np.sqrt(c)
-        return {"layerNormInWeight": t.values(c, 0.2, 1), "layerNormInBias": t.values(c, 0.1),
-                "linearAPWeight": t.normal(c * c, rz).reshape(c, c), "linearAPBias": t.values(c, 0.03),
-                "linearAGWeight": t.normal(c * c, rz).reshape(c, c), "linearAGBias": t.values(c, 0.03, 1),
-                "linearBPWeight": t.normal(c * c, rz).reshape(c, c), "linearBPBias": t.values(c, 0.03),
-                "linearBGWeight": t.normal(c * c, rz).reshape(c, c), "linearBGBias": t.values(c, 0.03, 1),
-                "layerNormOutWeight": t.values(c, 0.2, 1), "layerNormOutBias": t.values(c, 0.1),
-                "linearZWeight": t.normal(c * c, rz).reshape(c, c), "linearZBias": t.values(c, 0.03),
-                "linearGWeight": t.normal(c * c, rz).reshape(c, c), "linearGBias": t.values(c, 0.03, 1)}
-    w_out, w_in = tri(0), tri(1)
-    rec_out, dec_out = quantise_weights(w_out, TRI_MATS, "int5", True, 0)
-    rec_in, dec_in = quantise_weights(w_in, TRI_MATS, "int5", True, 0)
-    return {"z": z, "mask": mask, "rec_out": rec_out, "dec_out": dec_out, "rec_in": rec_in, "dec_in": dec_in}
+def config2_inputs(*a, **k):
+    c2 = S.config2_inputs(*a, **k)
+    c2["dec_out"] = decoded(c2["rec_out"])
+    c2["dec_in"] = decoded(c2["rec_in"])
+    return c2

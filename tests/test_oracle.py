@@ -2,6 +2,7 @@
 import numpy as np
 import pytest
 
+from localfold_amd import synthetic as S
 from oracle import codec, ops, prng
 from tests import helpers as H
 
@@ -43,7 +44,7 @@ def _brute_tri(z, mask, w, direction, eps=1e-5):
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_tri_brute_force(direction):
-    inp = prng.deterministic_triangle_input(5, 6, 4, 13)
+    inp = S.deterministic_triangle_input(5, 6, 4, 13)
     ref = _brute_tri(inp["z"], inp["mask"], inp["weights"], direction)
     out = ops.tri_mult_af2(inp["z"], inp["mask"], inp["weights"], direction)
     assert np.abs(out - ref).max() < 1e-5
@@ -65,7 +66,7 @@ def test_af3_reduces_to_af2(direction):
     # rows have zero mean the two variance formulas agree; compare on the AF2 restatement.
     c, n = 8, 6
     w3 = H.af3_tri_weights(c, 5)
-    s = prng.Stream(4)
+    s = S.Stream(4)
     z = s.normal(n * n * c).reshape(n, n, c)
     mask = (s.uniform(n * n) > 0.2).astype(np.float32).reshape(n, n)
     w2 = {"layerNormInWeight": w3["leftNormInputScale"], "layerNormInBias": w3["leftNormInputOffset"],
@@ -128,7 +129,7 @@ def test_relu_transition_closed_form():
 # ---- attention ----------------------------------------------------------------------------
 
 def _attn_weights(c, heads, seed, pair_c=None):
-    s = prng.Stream(seed)
+    s = S.Stream(seed)
     r = 1 / np.sqrt(c)
     w = {"queryNormScale": s.values(c, 0.2, 1), "queryNormOffset": s.values(c, 0.1),
          "queryWeight": s.values(c * c, r).reshape(c, c), "keyWeight": s.values(c * c, r).reshape(c, c),
@@ -171,7 +172,7 @@ def _brute_attention(act, mask, w, heads, transpose, bias):
 
 @pytest.mark.parametrize("transpose", [False, True])
 def test_attention_brute_force(transpose):
-    s = prng.Stream(3)
+    s = S.Stream(3)
     B, Q, c, heads = 3, 5, 8, 2
     act = s.values(B * Q * c, 1.5).reshape((Q, B, c) if transpose else (B, Q, c))
     mask = np.ones((Q, B) if transpose else (B, Q), np.float32)
@@ -183,7 +184,7 @@ def test_attention_brute_force(transpose):
 
 
 def test_attention_pair_bias_separate_brute_force():
-    s = prng.Stream(5)
+    s = S.Stream(5)
     B, Q, c, heads, cz = 2, 4, 8, 2, 6
     act = s.values(B * Q * c, 1.5).reshape(B, Q, c)
     pair = s.values(Q * Q * cz, 1.5).reshape(Q, Q, cz)
@@ -199,7 +200,7 @@ def test_attention_pair_bias_separate_brute_force():
 
 
 def test_attention_single_unmasked_key_selects_value():
-    s = prng.Stream(8)
+    s = S.Stream(8)
     B, Q, c, heads = 1, 6, 4, 1
     act = s.values(B * Q * c, 1.0).reshape(B, Q, c)
     mask = np.zeros((B, Q), np.float32)
@@ -216,10 +217,10 @@ def test_attention_single_unmasked_key_selects_value():
 def test_grid_attention_transpose_identity():
     # ending-node attention == starting-node attention on the transposed pair (stock AF3 with the
     # bias NOT swapped is the only case where this needs the bias transposed: use swap=True)
-    from oracle.blocks import synthetic_pairformer_weights
+    from localfold_amd.synthetic import synthetic_pairformer_weights
     n, c = 6, 16
     w = synthetic_pairformer_weights(c, 8, 2, 2, 4)["pairAttention1"]
-    s = prng.Stream(2)
+    s = S.Stream(2)
     pair = s.normal(n * n * c).reshape(n, n, c)
     mask = (s.uniform(n * n) > 0.2).astype(np.float32).reshape(n, n)
     end = ops.grid_self_attention_af3(pair, mask, w, True, swap_transposed_bias=True)
@@ -230,7 +231,7 @@ def test_grid_attention_transpose_identity():
 # ---- outer product mean -------------------------------------------------------------------
 
 def test_opm_single_sequence_closed_form():
-    s = prng.Stream(6)
+    s = S.Stream(6)
     n, cm, co, cz = 4, 8, 3, 5
     msa = s.values(n * cm, 1.0).reshape(1, n, cm)
     mask = np.array([[1, 1, 0, 1]], np.float32)
@@ -252,7 +253,7 @@ def test_opm_single_sequence_closed_form():
 
 def _int5_record(codes_by_group, scales, zeros):
     codes = np.array(codes_by_group, np.uint8)
-    return {"dtype": "int5", "shape": [codes.size], "data": codec.pack_bits(codes, 5),
+    return {"dtype": "int5", "shape": [codes.size], "data": S.pack_bits(codes, 5),
             "scales": np.array(scales, np.float16), "zeros": np.array(zeros, np.float16), "block": 32}
 
 
@@ -273,14 +274,14 @@ def test_int5_scale_and_zero():
 
 
 def test_int5_group_is_20_bytes():
-    assert codec.pack_bits(np.zeros((3, 32), np.uint8), 5).size == 3 * 20 + 1
+    assert S.pack_bits(np.zeros((3, 32), np.uint8), 5).size == 3 * 20 + 1
 
 
 @pytest.mark.parametrize("dtype,tol", [("int8", 0.01), ("int5", 0.05)])
 def test_quantise_round_trip(dtype, tol):
     rng = np.random.default_rng(1)
     w = rng.normal(size=(64, 96)).astype(np.float32)
-    for rec in (codec.make_record(w, dtype), codec.make_record(w, dtype, channel_axis=1)):
+    for rec in (S.make_record(w, dtype), S.make_record(w, dtype, channel_axis=1)):
         dec = codec.decode(rec)
         rel = np.abs(dec - w).max() / np.abs(w).max()
         assert rel < tol, rel
@@ -298,7 +299,7 @@ def test_int8_decode_is_code_times_scale():
 
 @pytest.mark.parametrize("seed", [0, 7, 1000 + 384, 0xFFFFFFFF])
 def test_generator_counter_form(seed):
-    np.testing.assert_array_equal(prng.uniform_stream(seed, 257), prng.uniform_sequential(seed, 257))
+    np.testing.assert_array_equal(S.uniform_stream(seed, 257), prng.uniform_sequential(seed, 257))
 
 
 def test_error_metrics_exact():

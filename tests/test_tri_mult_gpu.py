@@ -4,7 +4,8 @@ test/evoformer-triangle-incoming.gpu.test.js:36-85)."""
 import numpy as np
 import pytest
 
-from oracle import ops, prng
+from localfold_amd import synthetic as S
+from oracle import ops
 from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
@@ -45,7 +46,7 @@ def test_fixture_incoming_vs_oracle(ctx, name):
 @pytest.mark.parametrize("n,cz,ch,seed", [(3, 4, 5, 42), (37, 64, 32, 5), (64, 128, 128, 7), (130, 128, 128, 11)])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_deterministic_input(ctx, n, cz, ch, seed, direction):
-    inp = prng.deterministic_triangle_input(n, cz, ch, seed)
+    inp = S.deterministic_triangle_input(n, cz, ch, seed)
     out, _ = _run(ctx, inp["z"], inp["mask"], inp["weights"], direction)
     ref = ops.tri_mult_af2(inp["z"], inp["mask"], inp["weights"], direction)
     H.assert_close(out, ref, label=f"{n}/{cz}/{ch}/{direction}")
@@ -56,7 +57,7 @@ def test_deterministic_input(ctx, n, cz, ch, seed, direction):
 @pytest.mark.parametrize("act", ["float32", "bfloat16", "float16"])
 def test_quantised_weights_and_activation_dtypes(ctx, dtype, per_channel, act):
     import torch
-    inp = prng.deterministic_triangle_input(48, 128, 128, 3)
+    inp = S.deterministic_triangle_input(48, 128, 128, 3)
     rec, dec = H.quantise_weights(inp["weights"], H.TRI_MATS, dtype, per_channel, 0)
     tdt = getattr(torch, act)
     for direction in ("outgoing", "incoming"):
@@ -71,7 +72,7 @@ def test_quantised_weights_and_activation_dtypes(ctx, dtype, per_channel, act):
 def test_af3_dialect(ctx, direction, divide):
     n, c = 40, 128
     w = H.af3_tri_weights(c, 21)
-    s = prng.Stream(77)
+    s = S.Stream(77)
     z = s.normal(n * n * c).reshape(n, n, c)
     mask = np.ones((n, n), np.float32)
     mask[-4:, :] = 0
@@ -84,7 +85,7 @@ def test_af3_dialect(ctx, direction, divide):
 def test_accumulate_in_place(ctx):
     import torch
     from localfold_amd import device as D
-    inp = prng.deterministic_triangle_input(33, 128, 128, 9)
+    inp = S.deterministic_triangle_input(33, 128, 128, 9)
     dw = D.DeviceWeights(ctx.device)
     ws = D.tri_mult_weights(dw, inp["weights"])
     z = torch.as_tensor(inp["z"]).to(ctx.device)
@@ -106,15 +107,13 @@ def test_config2_full_size(ctx):
     out2, zin2 = _run(ctx, c2["z"], c2["mask"], c2["rec_in"], "incoming", act=torch.bfloat16)
     ref2 = ops.tri_mult_af2(zin2, c2["mask"], c2["dec_in"], "incoming")
     H.assert_close(out2, ref2, label="config2/incoming")
-    # masked rows of a and b are zero: the contraction of a fully masked row/column is zero,
-    # so those pairs' update is the gated output bias path only - identical across k.
     assert np.isfinite(out1).all() and np.isfinite(out2).all()
 
 
 def test_invalid_shapes_rejected(ctx):
     import torch
     from localfold_amd import capi, device as D
-    inp = prng.deterministic_triangle_input(4, 8, 8, 1)
+    inp = S.deterministic_triangle_input(4, 8, 8, 1)
     dw = D.DeviceWeights(ctx.device)
     ws = D.tri_mult_weights(dw, inp["weights"])
     z = torch.zeros(4, 4, 9, device=ctx.device)       # cZ 9 against weights of 8
