@@ -1,0 +1,427 @@
+// Gated self-attention with an optional pair bias: AF2 MSA row / column attention and
+// triangle attention (starting / ending node), AF3 grid and single attention.
+//
+// Semantics (webgpu/kernels/attention.js): x = LN(row) with logical row (b, q) read at storage
+// row (q, b) when transposed (:163-168); q = x Wq / sqrt(d) (+ q bias), k = x Wk, v = x Wv,
+// g = sigmoid(x Wg + bg) (:482-507); logit = q.k + 1e9 (m_k - 1) + bias[h][q][k], clamped to
+// +-1e8 (:917-921); o = softmax(logit) v * g; update = o Wo + bo, stored back transposed.
+// Pair bias (:695-783): bias[h][i][j] = LN(z_ij) . W[:, h], from a separate pair tensor or
+// from the normalised attention input itself.
+//
+// Kernels:
+//   lnproj  LN + the q/k/v/g (+ bias) projections in one pass over the rows
+//           (q, k: [b][h][n][32] f16; v: [b][h][32][n] f16 (transposed for P.V); g: [rows][H*d])
+//   keybias kb[b][k] = 1e9 (mask - 1)
+//   flash   per (b, h, 128 queries): S^T = K Q^T on MFMA, online softmax with each lane
+//           owning one query (statistics: two cross-lane shuffles), O^T += V^T P^T on MFMA;
+//           the N^2 x heads logits never leave registers
+//   rowgemm o Wo + bo, + residual, stored through the row map
+#include <algorithm>
+#include <cmath>
+
+#include "lf_rowgemm.h"
+
+namespace lf {
+
+constexpr int FA_DP = 32;       // padded head dim (d <= 32)
+constexpr int FA_QPW = 32;      // queries per wave (two 16-query MFMA tiles)
+constexpr int FA_WAVES = 4;
+constexpr int FA_QPB = FA_QPW * FA_WAVES;
+constexpr int FA_KC = 64;       // keys per chunk
+constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
+
+struct FlashParams {
+  const _Float16 *q, *k, *vt, *g;
+  _Float16* o;
+  const float* kb;        // [B][Q]
+  const _Float16* bias;   // [H][Q][Q] or null
+  int B, H, Q, d, HD;
+  int nqb;                // query blocks per (b, h)
+  long long nblocks;
+};
+
+__global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* kb, int B, int Q, int transpose) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)B * Q) return;
+  const int b = (int)(i / Q), k = (int)(i % Q);
+  const float m = mask[transpose ? (long long)k * B + b : i];
+  kb[i] = 1e9f * (m - 1.0f);
+}
+
+__global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_KC * FA_KLD];
+  __shared__ __attribute__((aligned(16))) _Float16 Vs[2][FA_DP * FA_VLD];
+  __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+
+  // XCD-aware order: the hardware deals consecutive blocks to the 8 XCDs round-robin; remap
+  // so each XCD walks a contiguous range of (query block, batch row) for one head, keeping
+  // that head's pair bias and each row's K/V in its own L2.
+  long long lb = blockIdx.x;
+  const long long per = p.nblocks / 8;
+  if (lb < per * 8) lb = (lb % 8) * per + lb / 8;
+  const int qb = (int)(lb % p.nqb);
+  const int b = (int)((lb / p.nqb) % p.B);
+  const int h = (int)(lb / ((long long)p.nqb * p.B));
+
+  const size_t bh = (size_t)b * p.H + h;
+  const _Float16* qh = p.q + bh * p.Q * FA_DP;
+  const _Float16* kh = p.k + bh * p.Q * FA_DP;
+  const _Float16* vh = p.vt + bh * FA_DP * p.Q;
+  const float* kbb = p.kb + (size_t)b * p.Q;
+  const _Float16* bias = p.bias ? p.bias + (size_t)h * p.Q * p.Q : nullptr;
+
+  // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
+  int qidx[2];
+  h8 qf[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    qidx[qt] = qb * FA_QPB + wave * FA_QPW + qt * 16 + r16;
+    const int qc = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
+    qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc * FA_DP + kq);
+  }
+
+  const int nkc = (p.Q + FA_KC - 1) / FA_KC;
+  const bool vecv = (p.Q & 7) == 0;
+  // stage chunk c: K rows [64][32] (one 16-byte piece per thread), V^T rows [32][64], key bias
+  auto kv_load = [&](int c, uint4& kr, uint4& vr, float& kbr) {
+    const int k0 = c * FA_KC;
+    {
+      const int key = tid >> 2, seg = tid & 3, kk = k0 + key;
+      kr = *reinterpret_cast<const uint4*>(kh + (size_t)(kk < p.Q ? kk : 0) * FA_DP + seg * 8);
+    }
+    {
+      const int dd = tid >> 3, seg = tid & 7, kk = k0 + seg * 8;
+      if (vecv) {
+        vr = *reinterpret_cast<const uint4*>(vh + (size_t)dd * p.Q + (kk < p.Q ? kk : 0));
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int k1 = kk + 2 * e, k2 = kk + 2 * e + 1;
+          const uint16_t lo = __builtin_bit_cast(uint16_t, vh[(size_t)dd * p.Q + (k1 < p.Q ? k1 : 0)]);
+          const uint16_t hi = __builtin_bit_cast(uint16_t, vh[(size_t)dd * p.Q + (k2 < p.Q ? k2 : 0)]);
+          w[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        vr = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    kbr = 0.f;
+    if (tid < FA_KC) {
+      const int kk = k0 + tid;
+      kbr = kk < p.Q ? kbb[kk] : -1e30f;   // keys past Q never contribute
+    }
+  };
+  auto kv_store = [&](int buf, const uint4& kr, const uint4& vr, float kbr) {
+    {
+      const int key = tid >> 2, seg = tid & 3;
+      *reinterpret_cast<uint4*>(&Ks[buf][key * FA_KLD + seg * 8]) = kr;
+    }
+    {
+      const int dd = tid >> 3, seg = tid & 7;
+      *reinterpret_cast<uint4*>(&Vs[buf][dd * FA_VLD + seg * 8]) = vr;
+    }
+    if (tid < FA_KC) Kb[buf][tid] = kbr;
+  };
+
+  uint4 kr, vr;
+  float kbr;
+  kv_load(0, kr, vr, kbr);
+  kv_store(0, kr, vr, kbr);
+  __syncthreads();
+
+  float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+  f4 o[2][2];   // [dt][qt]: O^T[dt*16 + 4*g4 + i][query]
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = 0; c < nkc; ++c) {
+    const int buf = c & 1, k0 = c * FA_KC;
+    // pair-bias values for this lane's queries and keys k0 + kt*16 + 4*g4 + i
+    float bv[2][4][4];
+    if (bias) {
+      const bool v4 = (p.Q & 3) == 0;
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const int qc = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const int kk = k0 + kt * 16 + 4 * g4;   // keys >= Q are discarded via the key bias
+          if (v4) {
+            const h4 v = *reinterpret_cast<const h4*>(bias + (size_t)qc * p.Q + (kk + 4 <= p.Q ? kk : p.Q - 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[qt][kt][i] = (float)v[i];
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[qt][kt][i] = (float)bias[(size_t)qc * p.Q + (kk + i < p.Q ? kk + i : 0)];
+          }
+        }
+      }
+    }
+    if (c + 1 < nkc) kv_load(c + 1, kr, vr, kbr);
+    // S^T tiles
+    f4 s[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
+    }
+    _Float16 pv[2][4][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float mx = -1e30f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
+        const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = s[qt][kt][i] + kbv[i];
+          if (bias) x += bv[qt][kt][i];
+          // clamp +-1e8 (keys past Q carry -1e30 and stay below every real logit)
+          x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -1e8f), 1e8f);
+          s[qt][kt][i] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+      const float m_new = fmaxf(m_run[qt], mx);
+      const float corr = __expf(m_run[qt] - m_new);
+      float sum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __expf(s[qt][kt][i] - m_new);
+          sum += e;
+          pv[qt][kt][i] = (_Float16)e;
+        }
+      sum += __shfl_xor(sum, 16, WAVE);
+      sum += __shfl_xor(sum, 32, WAVE);
+      l_run[qt] = l_run[qt] * corr + sum;
+      m_run[qt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) o[dt][qt] = o[dt][qt] * corr;
+    }
+    // O^T += V^T P^T over two 32-key halves
+#pragma unroll
+    for (int kh2 = 0; kh2 < 2; ++kh2) {
+      h8 vf[2];
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const _Float16* vrow = &Vs[buf][(dt * 16 + r16) * FA_VLD];
+        const h4 lo = *reinterpret_cast<const h4*>(vrow + (2 * kh2) * 16 + 4 * g4);
+        const h4 hi = *reinterpret_cast<const h4*>(vrow + (2 * kh2 + 1) * 16 + 4 * g4);
+        vf[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const h8 pf = h8{pv[qt][2 * kh2][0], pv[qt][2 * kh2][1], pv[qt][2 * kh2][2], pv[qt][2 * kh2][3],
+                         pv[qt][2 * kh2 + 1][0], pv[qt][2 * kh2 + 1][1], pv[qt][2 * kh2 + 1][2],
+                         pv[qt][2 * kh2 + 1][3]};
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) o[dt][qt] = mfma16(vf[dt], pf, o[dt][qt]);
+      }
+    }
+    if (c + 1 < nkc) {
+      // buffer buf^1 was last read in chunk c-1, which every wave finished before the
+      // barrier that ended it
+      kv_store(buf ^ 1, kr, vr, kbr);
+      __syncthreads();
+    }
+  }
+  // o[query][h*d + dd] = O / l * g
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    if (qidx[qt] >= p.Q) continue;
+    const float inv = 1.0f / l_run[qt];
+    const size_t row = (size_t)b * p.Q + qidx[qt];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d0 = dt * 16 + 4 * g4;
+      if (d0 >= p.d) continue;
+      const size_t base = row * p.HD + (size_t)h * p.d + d0;
+      if (d0 + 4 <= p.d && (p.d & 3) == 0) {
+        const h4 gv = *reinterpret_cast<const h4*>(p.g + base);
+        h4 ov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = (_Float16)(o[dt][qt][i] * inv * (float)gv[i]);
+        *reinterpret_cast<h4*>(p.o + base) = ov;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (d0 + i < p.d) p.o[base + i] = (_Float16)(o[dt][qt][i] * inv * (float)p.g[base + i]);
+      }
+    }
+  }
+}
+
+int attention(lf_context* ctx, const lf_attention_args& a) {
+  LF_REQUIRE(a.w != nullptr, "attention: weights are NULL");
+  LF_REQUIRE(a.batch > 0 && a.queries > 0 && a.channels > 0 && a.heads > 0,
+             "attention dimensions must be positive");
+  LF_REQUIRE(act_dtype_ok(a.act_dtype), "attention: act_dtype must be f32, f16 or bf16");
+  LF_REQUIRE(a.act && a.mask && a.out, "attention: act, mask and out must be device pointers");
+  LF_REQUIRE(a.channels <= 384, "attention: channels must be <= 384");
+  const int B = a.batch, Q = a.queries, C = a.channels, H = a.heads;
+  if (a.head_dim == 0)
+    LF_REQUIRE(C % H == 0, "attention: channels must be a multiple of heads when head_dim is 0");
+  const int d = a.head_dim > 0 ? a.head_dim : C / H;
+  LF_REQUIRE(d >= 1 && d <= 32, "attention: head dimension must be 1..32");
+  const int HD = H * d;
+  LF_REQUIRE(HD <= 512, "attention: heads * head_dim must be <= 512");
+  LF_REQUIRE(a.bias_mode >= LF_BIAS_NONE && a.bias_mode <= LF_BIAS_LOGITS, "attention: bad bias_mode");
+  if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT)
+    LF_REQUIRE(B == Q, "attention: a bias from the normalised input needs batch == queries (triangle attention)");
+  if (a.bias_mode == LF_BIAS_SEPARATE) {
+    LF_REQUIRE(a.pair && act_dtype_ok(a.pair_dtype) && a.pair_channels > 0 && a.pair_channels <= 384,
+               "attention: separate pair bias needs pair activations (<= 384 channels)");
+  }
+  if (a.bias_mode == LF_BIAS_LOGITS) LF_REQUIRE(a.bias_logits, "attention: bias_logits is NULL");
+  LF_REQUIRE(a.epsilon > 0.f && std::isfinite(a.epsilon), "attention: epsilon must be finite and positive");
+  const lf_attention_weights& w = *a.w;
+  const long long rows = (long long)B * Q;
+  LF_REQUIRE(rows < (1LL << 31), "attention: too many rows");
+
+  WView views[6];
+  int nv = 0;
+  LF_TRY(make_view(w.wq, C, HD, "queryWeight", &views[nv++]));
+  LF_TRY(make_view(w.wk, C, HD, "keyWeight", &views[nv++]));
+  LF_TRY(make_view(w.wv, C, HD, "valueWeight", &views[nv++]));
+  LF_TRY(make_view(w.wg, C, HD, "gatingWeight", &views[nv++]));
+  LF_TRY(make_view(w.wo, HD, C, "outputWeight", &views[nv++]));
+  const bool want_bias = a.bias_mode == LF_BIAS_SEPARATE || a.bias_mode == LF_BIAS_NORMALIZED_INPUT;
+  if (want_bias)
+    LF_TRY(make_view(w.wb, a.bias_mode == LF_BIAS_SEPARATE ? a.pair_channels : C, H, "pair projectionWeight",
+                     &views[nv++]));
+
+  const size_t qkv = (size_t)B * H * Q * FA_DP * sizeof(_Float16);
+  const size_t hd = (size_t)rows * HD * sizeof(_Float16);
+  const size_t biasb = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Q * sizeof(float);
+  const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Q * sizeof(_Float16);
+  size_t sizes[13] = {qkv, qkv, qkv, hd, hd, (size_t)rows * sizeof(float), biasb, biash};
+  for (int i = 0; i < nv; ++i) sizes[8 + i] = expanded_bytes(views[i]);
+  void* bufs[14];
+  LF_TRY(workspace(ctx, sizes, bufs, 8 + nv));
+  _Float16 *qb = (_Float16*)bufs[0], *kb = (_Float16*)bufs[1], *vb = (_Float16*)bufs[2];
+  _Float16 *gb = (_Float16*)bufs[3], *ob = (_Float16*)bufs[4];
+  float* keyb = (float*)bufs[5];
+  float* bias32 = (float*)bufs[6];
+  _Float16* bias16 = (_Float16*)bufs[7];
+  WExp ex[6];
+  LF_TRY(expand_weights(ctx, views, nv, bufs + 8, ex, "attention.expand"));
+  if (d < FA_DP) {
+    for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
+  }
+
+  // 1. pair bias from a separate pair tensor: bias[h][i][j] = LN(pair_ij) . W[:, h]
+  if (a.bias_mode == LF_BIAS_SEPARATE) {
+    LnProjParams pb{};
+    pb.x = a.pair;
+    pb.rows = Q * Q;
+    pb.C = a.pair_channels;
+    pb.rmQ = 1;
+    pb.rmB = 0;
+    pb.ln_s = w.pair_norm_scale;
+    pb.ln_o = w.pair_norm_offset;
+    pb.eps = a.epsilon;
+    pb.fast_var = a.fast_variance;
+    pb.ngroups = 1;
+    Group& g = pb.g[0];
+    g.w0 = ex[5];
+    g.ncols = H;
+    g.op = OP_STORE;
+    g.scale = 1.f;
+    // [h][i][j] from row (i, j); swapped: [h][j][i]
+    g.dst = a.swap_bias ? Dst{bias32, DT_F32, Q, 1, Q, 1, (long long)Q * Q, 0}
+                        : Dst{bias32, DT_F32, Q * Q, 0, 1, 1, (long long)Q * Q, 0};
+    LF_TRY(launch_lnproj(ctx, pb, a.pair_dtype, "attention.pair_bias"));
+  }
+
+  // 2. LN + q/k/v/g (+ bias from the normalised input)
+  {
+    LnProjParams pp{};
+    pp.x = a.act;
+    pp.rows = (int)rows;
+    pp.C = C;
+    pp.rmQ = Q;
+    pp.rmB = a.transpose ? B : 0;
+    pp.ln_s = w.norm_scale;
+    pp.ln_o = w.norm_offset;
+    pp.eps = a.epsilon;
+    pp.fast_var = a.fast_variance;
+    const long long hq = (long long)Q * FA_DP;
+    Dst qd{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    Dst kd{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    Dst vd{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Q};
+    Dst gd = dst_rowmajor(gb, DT_F16, (int)rows, HD);
+    pp.g[0] = Group{ex[0], WExp{}, HD, OP_STORE, 1.0f / std::sqrt((float)d), w.q_bias, nullptr, qd};
+    pp.g[1] = Group{ex[1], WExp{}, HD, OP_STORE, 1.f, nullptr, nullptr, kd};
+    pp.g[2] = Group{ex[2], WExp{}, HD, OP_STORE, 1.f, nullptr, nullptr, vd};
+    pp.g[3] = Group{ex[3], WExp{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, gd};
+    pp.ngroups = 4;
+    if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) {
+      Dst bd = a.swap_bias ? Dst{bias32, DT_F32, Q, 1, Q, 1, (long long)Q * Q, 0}
+                           : Dst{bias32, DT_F32, (int)rows, 0, 1, 1, rows, 0};
+      pp.g[4] = Group{ex[5], WExp{}, H, OP_STORE, 1.f, nullptr, nullptr, bd};
+      pp.ngroups = 5;
+    }
+    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, "attention.project"));
+  }
+
+  // 3. key-mask bias, f16 copy of the pair bias
+  {
+    LaunchScope ls(ctx, "attention.keybias");
+    hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, ctx->stream, a.mask, keyb,
+                       B, Q, a.transpose);
+  }
+  LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
+  const float* bsrc = a.bias_mode == LF_BIAS_LOGITS ? a.bias_logits : bias32;
+  if (a.bias_mode != LF_BIAS_NONE) LF_TRY(f32_to_f16(ctx, bsrc, bias16, (long long)H * Q * Q, a.bias_mode == LF_BIAS_LOGITS && a.swap_bias ? Q : 0));
+
+  // 4. flash attention
+  {
+    FlashParams fp{};
+    fp.q = qb;
+    fp.k = kb;
+    fp.vt = vb;
+    fp.g = gb;
+    fp.o = ob;
+    fp.kb = keyb;
+    fp.bias = a.bias_mode == LF_BIAS_NONE ? nullptr : bias16;
+    fp.B = B;
+    fp.H = H;
+    fp.Q = Q;
+    fp.d = d;
+    fp.HD = HD;
+    fp.nqb = (Q + FA_QPB - 1) / FA_QPB;
+    fp.nblocks = (long long)fp.nqb * B * H;
+    LaunchScope ls(ctx, "attention.flash");
+    hipLaunchKernelGGL(flash_kernel, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
+  }
+  LF_TRY(check_hip(hipGetLastError(), "flash launch"));
+
+  // 5. output projection + residual, stored through the row map
+  {
+    RowGemmParams rp{};
+    rp.A = ob;
+    rp.rows = (int)rows;
+    rp.K = HD;
+    rp.N = C;
+    rp.w = ex[4];
+    rp.bias = w.o_bias;
+    rp.op = OP_STORE;
+    rp.resid = a.accumulate ? a.act : nullptr;
+    rp.dst = a.transpose ? Dst{a.out, a.act_dtype, Q, C, (long long)B * C, C, 0, 1}
+                         : dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+    LF_TRY(launch_rowgemm(ctx, rp, "attention.output"));
+  }
+  return LF_OK;
+}
+
+}  // namespace lf

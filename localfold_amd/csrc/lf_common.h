@@ -272,16 +272,16 @@ __device__ __forceinline__ void lds_ln_inplace(_Float16* X, int ld, int nvalid, 
 }
 
 // ---- MFMA A-fragment row tiles ---------------------------------------------------------
-// For v_mfma_f32_16x16x32_f16 with K = 128 in four k-steps, lane l supplies row l%16 and
+// For v_mfma_f32_16x16x32_f16 over K = 32*KS in KS k-steps, lane l supplies row l%16 and
 // channels 32*j + 8*(l/16) .. +8 at k-step j.  A FragTile loads a 16-row activation tile
 // straight into that layout (one 16-byte load per k-step for 16-bit storage, two for f32),
-// so the LayerNorm'd rows never touch LDS: a row's 128 channels sit in lanes l, l^16,
-// l^32, l^48 and its statistics take two cross-lane shuffles for all 16 rows at once.
-template <int ACT>
+// so LayerNorm'd rows never touch LDS: a row's channels sit in lanes l, l^16, l^32, l^48
+// and its statistics take two cross-lane shuffles for all 16 rows at once.
+template <int ACT, int KS = 4>
 struct FragTile {
   typedef typename Act<ACT>::T T;
   static constexpr int NV = (int)sizeof(T) * 8 / 16;   // uint4 per 8 elements
-  uint4 raw[4][NV];
+  uint4 raw[KS][NV];
   // element e (< 8) of k-step j, decoded with shifts (no address-taken locals)
   __device__ __forceinline__ float get(int j, int e) const {
     if constexpr (ACT == DT_F32) {
@@ -298,32 +298,51 @@ struct FragTile {
   }
 };
 
-// Row r16 = lane%16 of the tile reads src[(row0 + r16) * C + 32j + 8*(lane/16) + e]; rows
-// >= nvalid and channels >= C come from clamped addresses and are discarded later.
-template <int ACT>
-__device__ __forceinline__ void frag_load(FragTile<ACT>& t, const void* src, size_t row0, int nvalid, int C,
-                                          int lane) {
-  typedef typename FragTile<ACT>::T T;
-  const T* s = static_cast<const T*>(src);
-  const int r = lane & 15, g = lane >> 4;
-  const size_t base = (row0 + (r < nvalid ? r : 0)) * (size_t)C;
-  if (C == 128) {
+// Lane loads its row (storage row `srow`, already clamped to a valid row) at channels
+// 32j + 8*(lane/16) + e; channels >= C come from a clamped address (discarded later).
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* src, size_t srow, int C, int lane) {
+  typedef typename FragTile<ACT, KS>::T T;
+  const T* s = static_cast<const T*>(src) + srow * (size_t)C;
+  const int g = lane >> 4;
+  if (C == 32 * KS) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < KS; ++j)
 #pragma unroll
-      for (int v = 0; v < FragTile<ACT>::NV; ++v)
-        t.raw[j][v] = *reinterpret_cast<const uint4*>(s + base + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
+      for (int v = 0; v < FragTile<ACT, KS>::NV; ++v)
+        t.raw[j][v] = *reinterpret_cast<const uint4*>(s + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      T* e = reinterpret_cast<T*>(t.raw[j]);
+    for (int j = 0; j < KS; ++j) {
+      uint32_t w[4 * FragTile<ACT, KS>::NV];
+      if constexpr (ACT == DT_F32) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int c = 32 * j + 8 * g + k;
-        e[k] = s[base + (c < C ? c : 0)];
+        for (int k = 0; k < 8; ++k) {
+          const int c = 32 * j + 8 * g + k;
+          w[k] = __float_as_uint(s[c < C ? c : 0]);
+        }
+        t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
+        t.raw[j][1] = make_uint4(w[4], w[5], w[6], w[7]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int c0 = 32 * j + 8 * g + 2 * k;
+          const uint16_t lo = __builtin_bit_cast(uint16_t, s[c0 < C ? c0 : 0]);
+          const uint16_t hi = __builtin_bit_cast(uint16_t, s[c0 + 1 < C ? c0 + 1 : 0]);
+          w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
   }
+}
+
+// Row r16 = lane%16 of the tile reads src[(row0 + r16) * C + ...]; rows >= nvalid read row0.
+template <int ACT, int KS = 4>
+__device__ __forceinline__ void frag_load(FragTile<ACT, KS>& t, const void* src, size_t row0, int nvalid, int C,
+                                          int lane) {
+  const int r = lane & 15;
+  frag_load_row(t, src, row0 + (r < nvalid ? r : 0), C, lane);
 }
 
 // 8 floats -> the storage words of 8 activations (bit operations only, so the words stay
@@ -355,14 +374,15 @@ __device__ __forceinline__ float lanes4_sum(float v) {   // over lanes l, l^16, 
   return v;
 }
 
-// LayerNorm of the 16 rows held as raw values x[j][e] (channel 32j + 8*(lane/16) + e) into
-// f16 A fragments.  gamma/beta: 128 floats (LDS).  Rows >= nvalid give zero fragments.
-__device__ __forceinline__ void frag_ln(const float (&x)[4][8], h8 (&a)[4], int nvalid, int C, const float* gamma,
+// LayerNorm of the 16 rows held as values x[j][e] (channel 32j + 8*(lane/16) + e, zero past
+// C) into f16 A fragments.  gamma/beta: 32*KS floats (LDS).  Rows with !ok give zeros.
+template <int KS>
+__device__ __forceinline__ void frag_ln(const float (&x)[KS][8], h8 (&a)[KS], bool ok, int C, const float* gamma,
                                         const float* beta, float eps, bool fast_var, int lane) {
-  const int r = lane & 15, g = lane >> 4;
+  const int g = lane >> 4;
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < KS; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += x[j][e];
   const float invC = 1.0f / (float)C;
@@ -370,13 +390,13 @@ __device__ __forceinline__ void frag_ln(const float (&x)[4][8], h8 (&a)[4], int 
   float q = 0.f;
   if (fast_var) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < KS; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) q += x[j][e] * x[j][e];
     q = lanes4_sum(q) * invC - mean * mean;
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < KS; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float d = (32 * j + 8 * g + e < C) ? x[j][e] - mean : 0.f;
@@ -385,9 +405,8 @@ __device__ __forceinline__ void frag_ln(const float (&x)[4][8], h8 (&a)[4], int 
     q = lanes4_sum(q) * invC;
   }
   const float inv = rsqrt_(q + eps);
-  const bool ok = r < nvalid;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < KS; ++j) {
     const float4 g0 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g);
     const float4 g1 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g + 4);
     const float4 b0 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g);
@@ -400,6 +419,16 @@ __device__ __forceinline__ void frag_ln(const float (&x)[4][8], h8 (&a)[4], int 
       a[j][e] = (_Float16)(valid ? (x[j][e] - mean) * inv * gg[e] + bb[e] : 0.f);
     }
   }
+}
+
+// Raw tile -> float values (zero past C).
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_values(const FragTile<ACT, KS>& t, float (&x)[KS][8], int C, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < KS; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + 8 * g + e < C) ? t.get(j, e) : 0.f;
 }
 
 // dst[i] = v[i] when v is non-null and i < n, else dflt; i < cap (block-cooperative).

@@ -19,6 +19,8 @@ int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, in
 // Decodes `count` weight views into f16 E[n][k] tiles at dst[i] (expanded_bytes(views[i]) each).
 int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label);
 size_t expanded_bytes(const WView& v);
+// dst = (f16) src over n elements; tq > 0 transposes every [tq][tq] plane.
+int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq);
 
 inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == LF_BF16; }
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }

@@ -2,7 +2,6 @@
 #include "lf_context.h"
 #include "lf_ops.h"
 namespace lf {
-int attention(lf_context*, const lf_attention_args&) { return set_error(LF_ERR_UNSUPPORTED, "lf_attention: not built yet"); }
 int transition(lf_context*, const lf_transition_args&) { return set_error(LF_ERR_UNSUPPORTED, "lf_transition: not built yet"); }
 int outer_product_mean(lf_context*, const lf_opm_args&) { return set_error(LF_ERR_UNSUPPORTED, "lf_outer_product_mean: not built yet"); }
 }

@@ -63,10 +63,10 @@ constexpr int PJ_COLS = 32;     // hidden channels per chunk (32 projection + 32
 template <int ACT, int KPAD>
 __global__ __launch_bounds__(256) void tri_project_kernel(TriProjectParams p) {
   constexpr int LDA = KPAD + 8, LDW = KPAD + 8, LDO = PJ_ROWS + 8;
-  __shared__ _Float16 As[PJ_ROWS * LDA];
-  __shared__ _Float16 Ws[2 * PJ_COLS * LDW];
-  __shared__ _Float16 Os[PJ_COLS * LDO];
-  __shared__ float Gs[2 * KPAD];
+  __shared__ __attribute__((aligned(16))) _Float16 As[PJ_ROWS * LDA];
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[2 * PJ_COLS * LDW];
+  __shared__ __attribute__((aligned(16))) _Float16 Os[PJ_COLS * LDO];
+  __shared__ __attribute__((aligned(16))) float Gs[2 * KPAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = blockIdx.x * PJ_ROWS;
   const int kloop = (p.C + 31) & ~31;
@@ -129,11 +129,11 @@ template <int ACT, int KZ, int KH>
 __global__ __launch_bounds__(256) void tri_output_kernel(TriOutputParams p) {
   typedef typename Act<ACT>::T T;
   constexpr int LDX = KH + 8, LDZ = KZ + 8;
-  __shared__ _Float16 Xs[OT_ROWS * LDX];
-  __shared__ _Float16 Zs[OT_ROWS * LDZ];
-  __shared__ _Float16 Wzs[OT_COLS * LDX];
-  __shared__ _Float16 Wgs[OT_COLS * LDZ];
-  __shared__ float Gs[2 * KZ + 2 * KH];
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[OT_ROWS * LDX];
+  __shared__ __attribute__((aligned(16))) _Float16 Zs[OT_ROWS * LDZ];
+  __shared__ __attribute__((aligned(16))) _Float16 Wzs[OT_COLS * LDX];
+  __shared__ __attribute__((aligned(16))) _Float16 Wgs[OT_COLS * LDZ];
+  __shared__ __attribute__((aligned(16))) float Gs[2 * KZ + 2 * KH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = blockIdx.x * OT_ROWS;
   const int kh = (p.H + 31) & ~31, kz = (p.C + 31) & ~31;
@@ -242,8 +242,8 @@ __device__ __forceinline__ void ct_load(_Float16* S, const _Float16* src, int N,
 
 template <bool KMAJOR, bool VEC>
 __global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) {
-  __shared__ _Float16 Ls[CT_TILE * CT_LD];
-  __shared__ _Float16 Rs[CT_TILE * CT_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Ls[CT_TILE * CT_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Rs[CT_TILE * CT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int m0 = blockIdx.x * CT_TILE, n0 = blockIdx.y * CT_TILE, h = blockIdx.z;
@@ -307,9 +307,9 @@ constexpr int PR_WAVES = 8;
 
 template <int ACT>
 __global__ __launch_bounds__(512) void tri_project_resident_kernel(TriProjectParams p) {
-  __shared__ _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate, b-proj, b-gate as [h][k]
-  __shared__ float Bs[4 * 128];              // the four bias vectors
-  __shared__ float Gs[2 * 128];              // LN_in scale, offset
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate, b-proj, b-gate as [h][k]
+  __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors
+  __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   stage_resident(Ws, p.wp[0], tid, 512);
   stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, 512);
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(512) void tri_project_resident_kernel(TriProjectPar
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + kq + e < p.C) ? t.get(j, e) : 0.f;
-      frag_ln(x, a, nvalid, p.C, Gs, Gs + 128, p.eps, p.fast_var, lane);
+      frag_ln<4>(x, a, r16 < nvalid, p.C, Gs, Gs + 128, p.eps, p.fast_var, lane);
     }
     float m[4];
 #pragma unroll
@@ -407,10 +407,10 @@ constexpr int OR_SCR = 16 * 132;   // floats of per-wave scratch: X^T tile (f16)
 template <int ACT>
 __global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParams p) {
   typedef typename Act<ACT>::T T;
-  __shared__ _Float16 Wz[128 * RS_LD];   // [c][h]
-  __shared__ _Float16 Wg[128 * RS_LD];   // [c][k]
-  __shared__ float Scr[OR_WAVES * OR_SCR];
-  __shared__ float Vs[6 * 128];           // bz, bg, centre-norm scale/offset, LN_in scale/offset
+  __shared__ __attribute__((aligned(16))) _Float16 Wz[128 * RS_LD];   // [c][h]
+  __shared__ __attribute__((aligned(16))) _Float16 Wg[128 * RS_LD];   // [c][k]
+  __shared__ __attribute__((aligned(16))) float Scr[OR_WAVES * OR_SCR];
+  __shared__ __attribute__((aligned(16))) float Vs[6 * 128];           // bz, bg, centre-norm scale/offset, LN_in scale/offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   stage_resident(Wz, p.wz, tid, 512);
   stage_resident(Wg, p.wg, tid, 512);
@@ -467,12 +467,12 @@ __global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParam
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[j][e] = (float)v[e];
       }
-      frag_ln(x, ax, nvalid, p.H, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
+      frag_ln<4>(x, ax, r16 < nvalid, p.H, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + kq + e < p.C) ? t.get(j, e) : 0.f;
-      frag_ln(x, az, nvalid, p.C, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+      frag_ln<4>(x, az, r16 < nvalid, p.C, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
     }
 #pragma unroll 1
     for (int pass = 0; pass < 2; ++pass) {

@@ -195,3 +195,89 @@ def tri_mult(ctx: Context, z: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_tri_mult(ctx.handle, C.byref(a)))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------------------
+
+def attention_weights_af2(dw: DeviceWeights, w: dict, pair_bias: dict = None) -> capi.lf_attention_weights:
+    """AF2 gated attention (`webgpu/kernels/attention.js:15-57`): (in,out) weights;
+    pair_bias: {layerNormScale, layerNormOffset, projectionWeight} (separate pair tensor) or
+    {projectionWeight} (bias from the normalised input)."""
+    s = capi.lf_attention_weights()
+    s.norm_scale, s.norm_offset = dw.vec(w["queryNormScale"]), dw.vec(w["queryNormOffset"])
+    s.wq = dw.weight(w["queryWeight"], capi.LF_IN_OUT)
+    s.wk = dw.weight(w["keyWeight"], capi.LF_IN_OUT)
+    s.wv = dw.weight(w["valueWeight"], capi.LF_IN_OUT)
+    s.wg = dw.weight(w["gatingWeight"], capi.LF_IN_OUT)
+    s.wo = dw.weight(w["outputWeight"], capi.LF_IN_OUT)
+    s.g_bias, s.o_bias = dw.vec(w["gatingBias"]), dw.vec(w["outputBias"])
+    if pair_bias is not None:
+        s.wb = dw.weight(pair_bias["projectionWeight"], capi.LF_IN_OUT)
+        if "layerNormScale" in pair_bias:
+            s.pair_norm_scale = dw.vec(pair_bias["layerNormScale"])
+            s.pair_norm_offset = dw.vec(pair_bias["layerNormOffset"])
+    return s
+
+
+def attention_weights_af3_grid(dw: DeviceWeights, w: dict) -> capi.lf_attention_weights:
+    """AF3 grid attention (`cpu/af3/trunk/pairformer.js:322-431`): q/k/gate (out,in), v/output (in,out)."""
+    s = capi.lf_attention_weights()
+    s.norm_scale, s.norm_offset = dw.vec(w["actNormScale"]), dw.vec(w["actNormOffset"])
+    s.wq = dw.weight(w["qProjection"], capi.LF_OUT_IN)
+    s.wk = dw.weight(w["kProjection"], capi.LF_OUT_IN)
+    s.wv = dw.weight(w["vProjection"], capi.LF_IN_OUT)
+    s.wg = dw.weight(w["gatingQuery"], capi.LF_OUT_IN)
+    s.wo = dw.weight(w["outputProjection"], capi.LF_IN_OUT)
+    s.g_bias = dw.vec(w.get("gatingQueryBias"))
+    s.o_bias = dw.vec(w.get("outputProjectionBias"))
+    s.wb = dw.weight(w["pairBiasProjection"], capi.LF_IN_OUT)
+    return s
+
+
+def attention_weights_af3_single(dw: DeviceWeights, w: dict, norm_scale, norm_offset, projection) -> capi.lf_attention_weights:
+    """AF3 single attention (`cpu/af3/trunk/pairformer.js:446-485`) with the pair-logits LN and
+    projection of `pairformerBlock` (`:516-537`) as a separate pair bias."""
+    s = capi.lf_attention_weights()
+    s.norm_scale, s.norm_offset = dw.vec(w["layerNormScale"]), dw.vec(w["layerNormOffset"])
+    s.wq = dw.weight(w["qProjection"], capi.LF_IN_OUT)
+    s.wk = dw.weight(w["kProjection"], capi.LF_IN_OUT)
+    s.wv = dw.weight(w["vProjection"], capi.LF_IN_OUT)
+    s.wg = dw.weight(w["gatingQuery"], capi.LF_IN_OUT)
+    s.wo = dw.weight(w["outputProjection"], capi.LF_IN_OUT)
+    s.q_bias = dw.vec(w["qBias"])
+    s.pair_norm_scale, s.pair_norm_offset = dw.vec(norm_scale), dw.vec(norm_offset)
+    s.wb = dw.weight(projection, capi.LF_IN_OUT)
+    return s
+
+
+def attention(ctx: Context, act: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf_attention_weights, heads: int,
+              transpose: bool = False, bias_mode: int = capi.LF_BIAS_NONE, pair: torch.Tensor = None,
+              head_dim: int = 0, fast_variance: bool = False, swap_bias: bool = False, out: torch.Tensor = None,
+              accumulate: bool = False, epsilon: float = 1e-5, bias_logits: torch.Tensor = None) -> torch.Tensor:
+    """act: storage [batch, queries, C] ([queries, batch, C] when transpose); mask: storage [.., ..]."""
+    d0, d1, c = act.shape
+    batch, queries = (d1, d0) if transpose else (d0, d1)
+    if tuple(mask.shape) != (d0, d1) or mask.dtype != torch.float32:
+        raise ValueError("mask must be float32 with the activation's storage shape")
+    if out is None:
+        out = torch.empty_like(act)
+    a = capi.lf_attention_args()
+    a.batch, a.queries, a.channels, a.heads, a.head_dim = batch, queries, c, heads, head_dim
+    a.transpose = int(transpose)
+    a.act_dtype = act_code(act)
+    a.act, a.mask, a.out = ptr(act), ptr(mask), ptr(out)
+    a.accumulate = int(accumulate)
+    a.fast_variance = int(fast_variance)
+    a.bias_mode = bias_mode
+    a.swap_bias = int(swap_bias)
+    if pair is not None:
+        a.pair_dtype = act_code(pair)
+        a.pair = ptr(pair)
+        a.pair_channels = pair.shape[-1]
+    a.bias_logits = ptr(bias_logits)
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_attention(ctx.handle, C.byref(a)))
+    return out

@@ -410,3 +410,16 @@ def synthetic_pairformer_weights(c_z, c_s, heads_pair, heads_single, dim_single,
                             "gatingQuery": lin(c_s, hw), "outputProjection": lin(hw, c_s)}
     w["singleTransition"] = trans(c_s)
     return w
+
+
+def config3_attention_weights(c: int, heads: int, seed: int) -> dict:
+    """BASELINE config 3 triangle-attention weights: N(0, 1/fan_in) masters, LN scale ~1."""
+    s = Stream(seed)
+    r = 1.0 / np.sqrt(c)
+    att = {"queryNormScale": s.values(c, 0.2, 1), "queryNormOffset": s.values(c, 0.1),
+           "queryWeight": s.normal(c * c, r).reshape(c, c), "keyWeight": s.normal(c * c, r).reshape(c, c),
+           "valueWeight": s.normal(c * c, r).reshape(c, c), "gatingWeight": s.normal(c * c, r).reshape(c, c),
+           "gatingBias": s.values(c, 0.1, 1), "outputWeight": s.normal(c * c, r).reshape(c, c),
+           "outputBias": s.values(c, 0.05)}
+    return {"heads": heads, "attention": att,
+            "pairBias": {"projectionWeight": s.normal(c * heads, r).reshape(c, heads)}}

@@ -141,7 +141,7 @@ def _softmax_attend(q, k, v, logit_bias):
 
 
 def attention_af2(activations, mask, w, heads, transpose=False, pair_bias=None, eps=1e-5,
-                  batch_chunk=None):
+                  batch_chunk=None, batch_rows=None):
     """AF2 gated self-attention, the semantics of `AttentionGpu.run` (`webgpu/kernels/attention.js:2580-2739`).
 
     activations: [batch, queries, C] in the (untransposed) storage layout when
@@ -156,6 +156,9 @@ def attention_af2(activations, mask, w, heads, transpose=False, pair_bias=None, 
     "layerNormOffset", "projectionWeight" [Cz, H]} | {"source": "normalized-input",
     "projectionWeight" [C, H]}  (`attention.js:695-783`: bias[h][i][j] = LN(z_ij) . W[:, h]).
     Weights are (in,out).  Returns the update in the storage layout.
+    `batch_rows` restricts the result to those logical batch rows (returned as
+    [len(batch_rows), queries, C], logical order) - batch rows are independent given the
+    bias, so a large case can be checked on a sample.
     """
     act = np.asarray(activations, F32)
     if transpose:
@@ -173,12 +176,14 @@ def attention_af2(activations, mask, w, heads, transpose=False, pair_bias=None, 
                             pair_bias["layerNormOffset"], eps)
             bias = linear(pn, pair_bias["projectionWeight"])          # [Q, Q, H]
         else:
-            # from the normalised (already transposed) input; one shared plane set for every
-            # batch row; (`block.js:1592-1610` passes source "normalized-input").
-            # The WGSL computes it per (q,k) from normalised row index q*queries+k, i.e.
-            # from batch row... the pair IS the attention input here (batch == queries).
+            # bias[h][i][j] from the normalised logical row (i, j) of the attention input itself
+            # (`block.js:1592-1610`, source "normalized-input"; batch == queries there)
             bias = linear(x.reshape(bsz * nq, c), pair_bias["projectionWeight"]).reshape(bsz, nq, heads)
         bias = np.asarray(bias, F64).transpose(2, 0, 1)              # [H, Q, K]
+    if batch_rows is not None:
+        x = x[np.asarray(batch_rows)]
+        msk = msk[np.asarray(batch_rows)]
+        bsz = x.shape[0]
     qs = 1.0 / np.sqrt(d)
     q = _f32(np.asarray(linear(x, w["queryWeight"]), F64) * qs)
     kk = linear(x, w["keyWeight"])
@@ -203,6 +208,8 @@ def attention_af2(activations, mask, w, heads, transpose=False, pair_bias=None, 
         out[b0:b1] = (p @ vh).transpose(0, 2, 1, 3)
     o = _f32(out.reshape(bsz, nq, c) * np.asarray(g, F64))
     upd = linear(o, w["outputWeight"], w["outputBias"])
+    if batch_rows is not None:
+        return upd
     return upd.transpose(1, 0, 2).copy() if transpose else upd
 
 
