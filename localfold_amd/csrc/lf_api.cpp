@@ -63,14 +63,15 @@ LaunchScope::~LaunchScope() {
   if (idx >= 0) hipEventRecord(ctx->recs[idx].stop, ctx->stream);
 }
 
-int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off, int col_stride) {
+int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off, int col_stride,
+              bool subset) {
   const std::string nm(name);
   if (!w.data) return set_error(LF_ERR_INVALID, nm + ": weight data is NULL");
   if (w.layout != LF_IN_OUT && w.layout != LF_OUT_IN) return set_error(LF_ERR_INVALID, nm + ": bad layout");
   const int in = w.layout == LF_IN_OUT ? w.rows : w.cols;
   const int outc = w.layout == LF_IN_OUT ? w.cols : w.rows;
   if (in != K) return set_error(LF_ERR_INVALID, nm + " has " + std::to_string(in) + " inputs; expected " + std::to_string(K));
-  if (col_off + (long long)(N - 1) * col_stride >= outc || (col_stride == 1 && col_off == 0 && outc != N))
+  if (col_off + (long long)(N - 1) * col_stride >= outc || (!subset && col_stride == 1 && col_off == 0 && outc != N))
     return set_error(LF_ERR_INVALID,
                      nm + " has " + std::to_string(outc) + " outputs; expected " + std::to_string((long long)N * col_stride));
   WView v{};

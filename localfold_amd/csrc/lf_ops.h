@@ -13,8 +13,10 @@ namespace lf {
 // Validates `w` as a logical [K x N] matrix (K inputs, N outputs) and builds its view.
 // `col_off`/`col_stride` select a strided subset of the stored output columns (AF3's
 // interleaved a/b split); the stored output count must cover them.
+// `subset` allows the view to cover only part of the stored outputs (e.g. one half of a fused
+// projection); otherwise a unit-stride view must match the stored output count exactly.
 int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off = 0,
-              int col_stride = 1);
+              int col_stride = 1, bool subset = false);
 
 // Decodes `count` weight views into f16 E[n][k] tiles at dst[i] (expanded_bytes(views[i]) each).
 int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label);

@@ -1,10 +1,6 @@
 // Entry points not yet implemented: they fail loudly with LF_ERR_UNSUPPORTED.
 #include "lf_context.h"
 #include "lf_ops.h"
-namespace lf {
-int transition(lf_context*, const lf_transition_args&) { return set_error(LF_ERR_UNSUPPORTED, "lf_transition: not built yet"); }
-int outer_product_mean(lf_context*, const lf_opm_args&) { return set_error(LF_ERR_UNSUPPORTED, "lf_outer_product_mean: not built yet"); }
-}
 extern "C" {
 int lf_evoformer_block(lf_context*, const lf_evoformer_block_args*) { return lf::set_error(LF_ERR_UNSUPPORTED, "not built yet"); }
 int lf_evoformer_stack(lf_context*, const lf_evoformer_block_args*, const lf_evoformer_weights*, int) { return lf::set_error(LF_ERR_UNSUPPORTED, "not built yet"); }

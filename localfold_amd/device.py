@@ -281,3 +281,85 @@ def attention(ctx: Context, act: torch.Tensor, mask: torch.Tensor, wstruct: capi
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_attention(ctx.handle, C.byref(a)))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# Transition and outer product mean
+# ---------------------------------------------------------------------------------------
+
+def transition_weights(dw: DeviceWeights, w: dict, kind: int = capi.LF_TRANSITION_RELU) -> capi.lf_transition_weights:
+    """AF2 (`webgpu/kernels/transition.js:445-460`): layerNormScale/Offset, firstWeight [C,H],
+    firstBias, secondWeight [H,C], secondBias.  AF3 SwiGLU (`cpu/af3/trunk/pairformer.js:180-201`):
+    inputLayerNormScale/Offset, transition1 [C,2H], transition2 [H,C]."""
+    s = capi.lf_transition_weights()
+    if kind == capi.LF_TRANSITION_RELU:
+        s.norm_scale, s.norm_offset = dw.vec(w["layerNormScale"]), dw.vec(w["layerNormOffset"])
+        s.w1, s.b1 = dw.weight(w["firstWeight"], capi.LF_IN_OUT), dw.vec(w["firstBias"])
+        s.w2, s.b2 = dw.weight(w["secondWeight"], capi.LF_IN_OUT), dw.vec(w["secondBias"])
+    else:
+        s.norm_scale, s.norm_offset = dw.vec(w["inputLayerNormScale"]), dw.vec(w["inputLayerNormOffset"])
+        s.w1 = dw.weight(w["transition1"], capi.LF_IN_OUT)
+        s.w2 = dw.weight(w["transition2"], capi.LF_IN_OUT)
+    return s
+
+
+def transition(ctx: Context, x: torch.Tensor, wstruct: capi.lf_transition_weights, hidden: int,
+               kind: int = capi.LF_TRANSITION_RELU, out: torch.Tensor = None, accumulate: bool = False,
+               fast_variance: bool = False, chunk_bytes: int = 0, epsilon: float = 1e-5) -> torch.Tensor:
+    if out is None:
+        out = torch.empty_like(x)
+    a = capi.lf_transition_args()
+    a.kind = kind
+    a.channels = x.shape[-1]
+    a.rows = x.numel() // a.channels
+    a.hidden = hidden
+    a.act_dtype = act_code(x)
+    a.act, a.out = ptr(x), ptr(out)
+    a.accumulate = int(accumulate)
+    a.fast_variance = int(fast_variance)
+    a.chunk_bytes = chunk_bytes
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_transition(ctx.handle, C.byref(a)))
+    return out
+
+
+def opm_weights(dw: DeviceWeights, w: dict, dialect: int = capi.LF_AF2) -> capi.lf_opm_weights:
+    """AF2 (`webgpu/kernels/outer-product-mean.js:38-85`): layerNormScale/Offset, leftWeight,
+    leftBias, rightWeight, rightBias, outputWeight [c*c, cZ], outputBias.  AF3
+    (`cpu/af3/trunk/msa.js:72-155`): layerNormInputScale/Offset, leftProjection,
+    rightProjection, outputW, outputB."""
+    s = capi.lf_opm_weights()
+    if dialect == capi.LF_AF2:
+        s.norm_scale, s.norm_offset = dw.vec(w["layerNormScale"]), dw.vec(w["layerNormOffset"])
+        s.wl, s.bl = dw.weight(w["leftWeight"], capi.LF_IN_OUT), dw.vec(w["leftBias"])
+        s.wr, s.br = dw.weight(w["rightWeight"], capi.LF_IN_OUT), dw.vec(w["rightBias"])
+        s.wo, s.bo = dw.weight(w["outputWeight"], capi.LF_IN_OUT), dw.vec(w["outputBias"])
+    else:
+        s.norm_scale, s.norm_offset = dw.vec(w["layerNormInputScale"]), dw.vec(w["layerNormInputOffset"])
+        s.wl = dw.weight(w["leftProjection"], capi.LF_IN_OUT)
+        s.wr = dw.weight(w["rightProjection"], capi.LF_IN_OUT)
+        s.wo, s.bo = dw.weight(w["outputW"], capi.LF_IN_OUT), dw.vec(w.get("outputB"))
+    return s
+
+
+def outer_product_mean(ctx: Context, msa: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf_opm_weights,
+                       c_outer: int, c_z: int, pair: torch.Tensor = None, out: torch.Tensor = None,
+                       accumulate: bool = False, fast_variance: bool = False, epsilon: float = 1e-5,
+                       norm_epsilon: float = 1e-3) -> torch.Tensor:
+    s_, n, cm = msa.shape
+    if out is None:
+        out = torch.empty((n, n, c_z), dtype=pair.dtype if pair is not None else msa.dtype, device=msa.device)
+    a = capi.lf_opm_args()
+    a.sequences, a.length, a.c_m, a.c_outer, a.c_z = s_, n, cm, c_outer, c_z
+    a.msa_dtype = act_code(msa)
+    a.msa, a.mask = ptr(msa), ptr(mask)
+    a.pair_dtype = act_code(out)
+    a.pair_in = ptr(pair)
+    a.out = ptr(out)
+    a.accumulate = int(accumulate)
+    a.fast_variance = int(fast_variance)
+    a.epsilon, a.norm_epsilon = epsilon, norm_epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_outer_product_mean(ctx.handle, C.byref(a)))
+    return out

@@ -1,0 +1,94 @@
+"""Transitions (AF2 ReLU, AF3 SwiGLU, row chunking) and outer product mean (AF2, AF3) on the GPU
+through the C ABI, against the oracle."""
+import numpy as np
+import pytest
+
+from localfold_amd import synthetic as S
+from oracle import ops
+from tests import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(ctx, x, dt=None):
+    import torch
+    t = torch.as_tensor(np.ascontiguousarray(x)).to(ctx.device)
+    return t.to(dt) if dt is not None else t
+
+
+@pytest.fixture(scope="module")
+def blockw():
+    return S.synthetic_block_weights(c_m=256, c_z=128, c_outer=32, heads_msa=8, heads_pair=4, tri_hidden=128,
+                                     msa_hidden=1024, pair_hidden=512, seed=1)
+
+
+@pytest.mark.parametrize("rows_shape,which,chunk", [((37, 37), "pairTransition", 0), ((6, 45), "msaTransition", 0),
+                                                    ((64, 64), "pairTransition", 128 * 1024)])
+def test_transition_relu(ctx, blockw, rows_shape, which, chunk):
+    import torch
+    from localfold_amd import device as D
+    w = blockw[which]
+    c = w["firstWeight"].shape[0]
+    hid = w["firstWeight"].shape[1]
+    x = S.Stream(5).values(int(np.prod(rows_shape)) * c, 1.5).reshape(*rows_shape, c)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.transition_weights(dw, w)
+    out = D.transition(ctx, _dev(ctx, x), ws, hid, chunk_bytes=chunk)
+    torch.cuda.synchronize()
+    ref = ops.transition_af2(x, w)
+    H.assert_close(out.cpu().numpy(), ref, label=f"{which} {rows_shape} chunk={chunk}")
+
+
+@pytest.mark.parametrize("c,n", [(128, 40), (384, 50)])
+def test_transition_swiglu(ctx, c, n):
+    import torch
+    from localfold_amd import capi, device as D
+    pw = S.synthetic_pairformer_weights(128, 384, 4, 16, 24, seed=6)
+    w = pw["pairTransition"] if c == 128 else pw["singleTransition"]
+    rows = n * n if c == 128 else n
+    x = S.Stream(8).normal(rows * c).reshape(rows, c)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.transition_weights(dw, w, capi.LF_TRANSITION_SWIGLU)
+    xt = _dev(ctx, x)
+    D.transition(ctx, xt, ws, 4 * c, capi.LF_TRANSITION_SWIGLU, out=xt, accumulate=True, fast_variance=True)
+    torch.cuda.synchronize()
+    ref = x.astype(np.float64) + ops.transition_af3(x, w)
+    H.assert_close(xt.cpu().numpy(), ref, label=f"swiglu {c}")
+
+
+@pytest.mark.parametrize("s,n", [(1, 16), (5, 37), (16, 64)])
+def test_opm_af2(ctx, blockw, s, n):
+    import torch
+    from localfold_amd import device as D
+    act = S.synthetic_activations(s, n, 256, 128, seed=s * 7 + n)
+    mask = act["msaMask"].copy()
+    if s > 2:
+        mask[2, ::3] = 0
+    w = blockw["outerProductMean"]
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.opm_weights(dw, w)
+    pair = _dev(ctx, act["pair"])
+    D.outer_product_mean(ctx, _dev(ctx, act["msa"]), _dev(ctx, mask), ws, 32, 128, pair=pair, out=pair,
+                         accumulate=True)
+    torch.cuda.synchronize()
+    ref = act["pair"].astype(np.float64) + ops.outer_product_mean_af2(act["msa"], mask, w)
+    H.assert_close(pair.cpu().numpy(), ref, label=f"opm {s}x{n}")
+
+
+def test_opm_af3(ctx):
+    import torch
+    from localfold_amd import capi, device as D
+    s_, n, cm, co, cz = 6, 30, 64, 32, 128
+    st = S.Stream(4)
+    msa = st.normal(s_ * n * cm).reshape(s_, n, cm)
+    mask = (st.uniform(s_ * n) > 0.2).astype(np.float32).reshape(s_, n)
+    w = {"layerNormInputScale": st.values(cm, 0.2, 1), "layerNormInputOffset": st.values(cm, 0.1),
+         "leftProjection": st.normal(cm * co, 1 / np.sqrt(cm)).reshape(cm, co),
+         "rightProjection": st.normal(cm * co, 1 / np.sqrt(cm)).reshape(cm, co),
+         "outputW": st.normal(co * co * cz, 1 / co).reshape(co * co, cz), "outputB": st.values(cz, 0.05)}
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.opm_weights(dw, w, capi.LF_AF3)
+    out = D.outer_product_mean(ctx, _dev(ctx, msa), _dev(ctx, mask), ws, co, cz, fast_variance=True)
+    torch.cuda.synchronize()
+    ref = ops.outer_product_mean_af3(msa, mask, w)
+    H.assert_close(out.cpu().numpy(), ref, label="opm af3")
