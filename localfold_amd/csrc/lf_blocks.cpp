@@ -1,0 +1,273 @@
+// Block and stack composition: AF2 Evoformer block / stack and AF3 Pairformer block, as
+// ordered calls of the op entry points with every residual written in place.
+//   Evoformer order: webgpu/af2/evoformer/block.js:1536-1629 (encodeEvoformerBlock)
+//   Stack:           webgpu/af2/evoformer/stack.js:44-160
+//   Pairformer:      cpu/af3/trunk/pairformer.js:495-541 (pairformerBlock)
+#include <cmath>
+
+#include "lf_context.h"
+#include "lf_ops.h"
+
+namespace lf {
+
+static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, const lf_evoformer_weights& w) {
+  LF_REQUIRE(a.sequences > 0 && a.length > 0 && a.c_m > 0 && a.c_z > 0, "evoformer block dimensions must be positive");
+  LF_REQUIRE(a.msa && a.pair && a.msa_mask && a.pair_mask, "evoformer block: NULL activation or mask");
+  const float eps = a.epsilon > 0.f ? a.epsilon : 1e-5f;
+  const long long chunk = 1LL << 30;   // transition hidden budget per chunk on a 288 GB device
+
+  {  // 1. MSA row attention with pair bias
+    lf_attention_args x{};
+    x.batch = a.sequences;
+    x.queries = a.length;
+    x.channels = a.c_m;
+    x.heads = w.row_heads;
+    x.act_dtype = a.msa_dtype;
+    x.act = a.msa;
+    x.mask = a.msa_mask;
+    x.out = a.msa;
+    x.accumulate = 1;
+    x.bias_mode = LF_BIAS_SEPARATE;
+    x.pair_dtype = a.pair_dtype;
+    x.pair = a.pair;
+    x.pair_channels = a.c_z;
+    x.epsilon = eps;
+    x.w = &w.row_attention;
+    LF_TRY(attention(ctx, x));
+  }
+  {  // 2. MSA column attention
+    lf_attention_args x{};
+    x.batch = a.length;
+    x.queries = a.sequences;
+    x.channels = a.c_m;
+    x.heads = w.column_heads;
+    x.transpose = 1;
+    x.act_dtype = a.msa_dtype;
+    x.act = a.msa;
+    x.mask = a.msa_mask;
+    x.out = a.msa;
+    x.accumulate = 1;
+    x.epsilon = eps;
+    x.w = &w.column_attention;
+    LF_TRY(attention(ctx, x));
+  }
+  {  // 3. MSA transition
+    lf_transition_args x{};
+    x.kind = LF_TRANSITION_RELU;
+    x.rows = a.sequences * a.length;
+    x.channels = a.c_m;
+    x.hidden = a.msa_hidden;
+    x.act_dtype = a.msa_dtype;
+    x.act = a.msa;
+    x.out = a.msa;
+    x.accumulate = 1;
+    x.chunk_bytes = chunk;
+    x.epsilon = eps;
+    x.w = &w.msa_transition;
+    LF_TRY(transition(ctx, x));
+  }
+  {  // 4. outer product mean into the pair
+    lf_opm_args x{};
+    x.sequences = a.sequences;
+    x.length = a.length;
+    x.c_m = a.c_m;
+    x.c_outer = a.c_outer;
+    x.c_z = a.c_z;
+    x.msa_dtype = a.msa_dtype;
+    x.msa = a.msa;
+    x.mask = a.msa_mask;
+    x.pair_dtype = a.pair_dtype;
+    x.pair_in = a.pair;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.epsilon = eps;
+    x.norm_epsilon = 1e-3f;
+    x.w = &w.outer_product_mean;
+    LF_TRY(outer_product_mean(ctx, x));
+  }
+  for (int dir = 0; dir < 2; ++dir) {  // 5, 6. triangle multiplication outgoing, incoming
+    lf_tri_mult_args x{};
+    x.direction = dir == 0 ? LF_OUTGOING : LF_INCOMING;
+    x.dialect = LF_AF2;
+    x.length = a.length;
+    x.c_z = a.c_z;
+    x.c_hidden = a.tri_hidden;
+    x.act_dtype = a.pair_dtype;
+    x.z = a.pair;
+    x.mask = a.pair_mask;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.epsilon = eps;
+    x.w = dir == 0 ? &w.tri_out : &w.tri_in;
+    LF_TRY(tri_mult(ctx, x));
+  }
+  for (int end = 0; end < 2; ++end) {  // 7, 8. triangle attention starting, ending
+    lf_attention_args x{};
+    x.batch = a.length;
+    x.queries = a.length;
+    x.channels = a.c_z;
+    x.heads = end ? w.tri_att_end_heads : w.tri_att_start_heads;
+    x.transpose = end;
+    x.act_dtype = a.pair_dtype;
+    x.act = a.pair;
+    x.mask = a.pair_mask;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.bias_mode = LF_BIAS_NORMALIZED_INPUT;
+    x.epsilon = eps;
+    x.w = end ? &w.tri_att_end : &w.tri_att_start;
+    LF_TRY(attention(ctx, x));
+  }
+  {  // 9. pair transition
+    lf_transition_args x{};
+    x.kind = LF_TRANSITION_RELU;
+    x.rows = a.length * a.length;
+    x.channels = a.c_z;
+    x.hidden = a.pair_hidden;
+    x.act_dtype = a.pair_dtype;
+    x.act = a.pair;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.chunk_bytes = chunk;
+    x.epsilon = eps;
+    x.w = &w.pair_transition;
+    LF_TRY(transition(ctx, x));
+  }
+  return LF_OK;
+}
+
+static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) {
+  LF_REQUIRE(a.w != nullptr, "pairformer block: weights are NULL");
+  LF_REQUIRE(a.tokens > 0 && a.c_z > 0, "pairformer block dimensions must be positive");
+  LF_REQUIRE(a.pair && a.pair_mask, "pairformer block: NULL pair or pair mask");
+  const lf_pairformer_weights& w = *a.w;
+  const float eps = a.epsilon > 0.f ? a.epsilon : 1e-5f;
+  const long long chunk = a.transition_chunk_bytes > 0 ? a.transition_chunk_bytes : (1LL << 30);
+  const int N = a.tokens;
+  for (int dir = 0; dir < 2; ++dir) {
+    lf_tri_mult_args x{};
+    x.direction = dir == 0 ? LF_OUTGOING : LF_INCOMING;
+    x.dialect = LF_AF3;
+    x.divide_by_length = a.divide_by_length;
+    x.length = N;
+    x.c_z = a.c_z;
+    x.c_hidden = a.c_z;
+    x.act_dtype = a.pair_dtype;
+    x.z = a.pair;
+    x.mask = a.pair_mask;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.epsilon = eps;
+    x.w = dir == 0 ? &w.tri_out : &w.tri_in;
+    LF_TRY(tri_mult(ctx, x));
+  }
+  for (int end = 0; end < 2; ++end) {
+    lf_attention_args x{};
+    x.batch = N;
+    x.queries = N;
+    x.channels = a.c_z;
+    x.heads = w.pair_heads;
+    x.transpose = end;
+    x.act_dtype = a.pair_dtype;
+    x.act = a.pair;
+    x.mask = a.pair_mask;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.bias_mode = LF_BIAS_NORMALIZED_INPUT;
+    // the bias comes from the untransposed pair unless the dialect swaps it
+    // (cpu/af3/trunk/pairformer.js:338-353); the library's swap is relative to the
+    // transposed logical rows
+    x.swap_bias = end && !a.swap_transposed_bias;
+    x.epsilon = eps;
+    x.w = end ? &w.att_end : &w.att_start;
+    LF_TRY(attention(ctx, x));
+  }
+  {
+    lf_transition_args x{};
+    x.kind = LF_TRANSITION_SWIGLU;
+    x.rows = N * N;
+    x.channels = a.c_z;
+    x.hidden = 4 * a.c_z;
+    x.act_dtype = a.pair_dtype;
+    x.act = a.pair;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.chunk_bytes = chunk;
+    x.epsilon = eps;
+    x.w = &w.pair_transition;
+    LF_TRY(transition(ctx, x));
+  }
+  if (!a.single) return LF_OK;
+  LF_REQUIRE(a.seq_mask && a.c_s > 0, "pairformer block: single track needs seq_mask and c_s");
+  {
+    lf_attention_weights sw = w.single_attention;
+    sw.pair_norm_scale = w.single_logits_norm_scale;
+    sw.pair_norm_offset = w.single_logits_norm_offset;
+    sw.wb = w.single_logits_projection;
+    lf_attention_args x{};
+    x.batch = 1;
+    x.queries = N;
+    x.channels = a.c_s;
+    x.heads = w.single_heads;
+    x.head_dim = w.single_head_dim;
+    x.act_dtype = a.single_dtype;
+    x.act = a.single;
+    x.mask = a.seq_mask;
+    x.out = a.single;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.bias_mode = LF_BIAS_SEPARATE;
+    x.pair_dtype = a.pair_dtype;
+    x.pair = a.pair;
+    x.pair_channels = a.c_z;
+    x.epsilon = eps;
+    x.w = &sw;
+    LF_TRY(attention(ctx, x));
+  }
+  {
+    lf_transition_args x{};
+    x.kind = LF_TRANSITION_SWIGLU;
+    x.rows = N;
+    x.channels = a.c_s;
+    x.hidden = 4 * a.c_s;
+    x.act_dtype = a.single_dtype;
+    x.act = a.single;
+    x.out = a.single;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.chunk_bytes = chunk;
+    x.epsilon = eps;
+    x.w = &w.single_transition;
+    LF_TRY(transition(ctx, x));
+  }
+  return LF_OK;
+}
+
+}  // namespace lf
+
+extern "C" {
+
+int lf_evoformer_block(lf_context* ctx, const lf_evoformer_block_args* args) {
+  if (!ctx || !args || !args->w) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_block: NULL argument");
+  hipSetDevice(ctx->device);
+  return lf::evoformer_block(ctx, *args, *args->w);
+}
+
+int lf_evoformer_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_evoformer_weights* blocks,
+                       int block_count) {
+  if (!ctx || !args || (!blocks && block_count > 0)) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_stack: NULL argument");
+  if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_stack: negative block count");
+  hipSetDevice(ctx->device);
+  for (int i = 0; i < block_count; ++i) LF_TRY(lf::evoformer_block(ctx, *args, blocks[i]));
+  return LF_OK;
+}
+
+int lf_pairformer_block(lf_context* ctx, const lf_pairformer_block_args* args) {
+  if (!ctx || !args) return lf::set_error(LF_ERR_INVALID, "lf_pairformer_block: NULL argument");
+  hipSetDevice(ctx->device);
+  return lf::pairformer_block(ctx, *args);
+}
+
+}  // extern "C"

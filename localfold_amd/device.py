@@ -363,3 +363,99 @@ def outer_product_mean(ctx: Context, msa: torch.Tensor, mask: torch.Tensor, wstr
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_outer_product_mean(ctx.handle, C.byref(a)))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# Blocks
+# ---------------------------------------------------------------------------------------
+
+def evoformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_evoformer_weights:
+    """lf_evoformer_weights from the `syntheticBlockWeights` / AlphaFoldFixture structure
+    (`tools/gpu/af2-synthetic-block.js:36-138`)."""
+    s = capi.lf_evoformer_weights()
+    row = w["msaRowAttention"]
+    s.row_attention = attention_weights_af2(dw, row["attention"], row["pairBias"])
+    s.row_heads = row["heads"]
+    col = w["msaColumnAttention"]
+    s.column_attention = attention_weights_af2(dw, col["attention"])
+    s.column_heads = col["heads"]
+    s.msa_transition = transition_weights(dw, w["msaTransition"])
+    s.outer_product_mean = opm_weights(dw, w["outerProductMean"])
+    s.tri_out = tri_mult_weights(dw, w["triangleMultiplicationOutgoing"])
+    s.tri_in = tri_mult_weights(dw, w["triangleMultiplicationIncoming"])
+    st, en = w["triangleAttentionStarting"], w["triangleAttentionEnding"]
+    s.tri_att_start = attention_weights_af2(dw, st["attention"], st["pairBias"])
+    s.tri_att_start_heads = st["heads"]
+    s.tri_att_end = attention_weights_af2(dw, en["attention"], en["pairBias"])
+    s.tri_att_end_heads = en["heads"]
+    s.pair_transition = transition_weights(dw, w["pairTransition"])
+    return s
+
+
+def evoformer_block_args(msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor, pair_mask: torch.Tensor,
+                         w: dict, epsilon: float = 1e-5) -> capi.lf_evoformer_block_args:
+    s_, n, cm = msa.shape
+    a = capi.lf_evoformer_block_args()
+    a.sequences, a.length, a.c_m, a.c_z = s_, n, cm, pair.shape[-1]
+    a.c_outer = np.shape(_plain(w["outerProductMean"]["leftWeight"]))[1]
+    a.tri_hidden = np.shape(_plain(w["triangleMultiplicationOutgoing"]["linearAPWeight"]))[0]
+    a.msa_hidden = np.shape(_plain(w["msaTransition"]["firstWeight"]))[1]
+    a.pair_hidden = np.shape(_plain(w["pairTransition"]["firstWeight"]))[1]
+    a.msa_dtype, a.msa = act_code(msa), ptr(msa)
+    a.pair_dtype, a.pair = act_code(pair), ptr(pair)
+    a.msa_mask, a.pair_mask = ptr(msa_mask), ptr(pair_mask)
+    a.epsilon = epsilon
+    return a
+
+
+def _plain(v):
+    return np.zeros(v["shape"]) if isinstance(v, dict) else v
+
+
+def evoformer_block(ctx: Context, msa, pair, msa_mask, pair_mask, wstruct, w: dict, epsilon: float = 1e-5):
+    """One AF2 Evoformer block, msa and pair updated in place."""
+    a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w, epsilon)
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_evoformer_block(ctx.handle, C.byref(a)))
+
+
+def evoformer_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: dict, epsilon: float = 1e-5):
+    """`len(wstructs)` blocks in order (EvoformerStackGpu.run), msa and pair updated in place."""
+    a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w0, epsilon)
+    arr = (capi.lf_evoformer_weights * len(wstructs))(*wstructs)
+    check(ctx.lib.lf_evoformer_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
+
+
+def pairformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_pairformer_weights:
+    """From the AF3 block structure of `cpu/af3/trunk/pairformer.js:495-541`."""
+    s = capi.lf_pairformer_weights()
+    s.tri_out = tri_mult_weights(dw, w["triangleMultiplicationOutgoing"], capi.LF_AF3)
+    s.tri_in = tri_mult_weights(dw, w["triangleMultiplicationIncoming"], capi.LF_AF3)
+    s.att_start = attention_weights_af3_grid(dw, w["pairAttention1"])
+    s.att_end = attention_weights_af3_grid(dw, w["pairAttention2"])
+    s.pair_heads = w["pairAttention1"]["heads"]
+    s.pair_transition = transition_weights(dw, w["pairTransition"], capi.LF_TRANSITION_SWIGLU)
+    s.single_logits_norm_scale = dw.vec(w["singlePairLogitsNormScale"])
+    s.single_logits_norm_offset = dw.vec(w["singlePairLogitsNormOffset"])
+    s.single_logits_projection = dw.weight(w["singlePairLogitsProjection"], capi.LF_IN_OUT)
+    sa = w["singleAttention"]
+    s.single_attention = attention_weights_af3_single(dw, sa, None, None, w["singlePairLogitsProjection"])
+    s.single_heads, s.single_head_dim = sa["heads"], sa["dimension"]
+    s.single_transition = transition_weights(dw, w["singleTransition"], capi.LF_TRANSITION_SWIGLU)
+    return s
+
+
+def pairformer_block(ctx: Context, pair, single, pair_mask, seq_mask, wstruct, swap_transposed_bias=False,
+                     divide_by_length=False, transition_chunk_bytes=0, epsilon=1e-5):
+    a = capi.lf_pairformer_block_args()
+    a.tokens, a.c_z = pair.shape[0], pair.shape[-1]
+    a.c_s = single.shape[-1] if single is not None else 0
+    a.swap_transposed_bias, a.divide_by_length = int(swap_transposed_bias), int(divide_by_length)
+    a.pair_dtype, a.pair = act_code(pair), ptr(pair)
+    if single is not None:
+        a.single_dtype, a.single = act_code(single), ptr(single)
+    a.pair_mask, a.seq_mask = ptr(pair_mask), ptr(seq_mask)
+    a.transition_chunk_bytes = transition_chunk_bytes
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_pairformer_block(ctx.handle, C.byref(a)))

@@ -423,3 +423,23 @@ def config3_attention_weights(c: int, heads: int, seed: int) -> dict:
            "outputBias": s.values(c, 0.05)}
     return {"heads": heads, "attention": att,
             "pairBias": {"projectionWeight": s.normal(c * heads, r).reshape(c, heads)}}
+
+
+def config1_inputs(seed: int = 0, n: int = 64, c_m: int = 256, c_z: int = 128):
+    """one AF2 Evoformer block, N_res=64, N_seq=1, fp32 weights ~N(0,1/fan_in)
+    (LN scales/offsets as `syntheticBlockWeights`), msa/pair ~N(0,1).  Returns (weights, msa, pair)."""
+    w = synthetic_block_weights(c_m=c_m, c_z=c_z, c_outer=32, heads_msa=8, heads_pair=4, tri_hidden=128,
+                                msa_hidden=4 * c_m, pair_hidden=4 * c_z, seed=seed + 1)
+    s = Stream(seed)
+
+    def renorm(d):
+        for k, v in list(d.items()):
+            if isinstance(v, dict):
+                renorm(v)
+            elif isinstance(v, np.ndarray) and v.ndim == 2:
+                fan_in = v.shape[1] if k.startswith("linear") else v.shape[0]   # triangle weights are (out,in)
+                d[k] = s.normal(v.size, 1.0 / np.sqrt(fan_in)).reshape(v.shape)
+    renorm(w)
+    msa = s.normal(n * c_m).reshape(1, n, c_m)
+    pair = s.normal(n * n * c_z).reshape(n, n, c_z)
+    return w, msa, pair
