@@ -1,0 +1,589 @@
+'use strict';
+// localfold-mi355x Node host: the reference's kernels-as-library classes
+// (webgpu/index.js:1-8 - TriangleMultiplication{Outgoing,Incoming}Gpu, AttentionGpu,
+// OuterProductMeanGpu, TransitionGpu, EvoformerBlockGpu, EvoformerStackGpu - and the AF3
+// pairformer stack of webgpu/af3/trunk/pairformer-block.js:246) over the C ABI of
+// include/localfold.h, reached through the N-API addon lib/localfold_napi.node.
+//
+// `new X(device)` takes a device from createDevice(); `run(input, options)` validates the
+// input the way the reference does (RangeError with the reference's messages), copies it to
+// the device, runs the HIP kernels, copies the result back and resolves to
+// {output, elapsedMilliseconds, memory, kernels}.  Weights are Float32Arrays as in the
+// reference, or quantised records {dtype: 'int8'|'int5'|'float16', codes, scales, zeros?,
+// block} (block = flat group size, 0 = one group per output channel), decoded inside the
+// kernels.  Node-12 syntax throughout (no optional chaining, no class fields).
+
+const fs = require('fs');
+const path = require('path');
+const { performance } = require('perf_hooks');
+
+let addonModule = null;
+function addon() {
+  if (addonModule === null) {
+    // fails loudly when the addon or liblocalfold.so is missing: there is no CPU fallback
+    addonModule = require(path.join(__dirname, '..', 'lib', 'localfold_napi.node'));
+  }
+  return addonModule;
+}
+
+const ACT = { float32: 0, float16: 1, bfloat16: 2 };
+const DIRECTION = { outgoing: 0, incoming: 1 };
+const BIAS = { none: 0, separate: 1, 'normalized-input': 2, logits: 3 };
+
+// ---- device --------------------------------------------------------------------------
+
+function createDevice(ordinal) {
+  const a = addon();
+  const ctx = a.contextCreate(ordinal === undefined ? 0 : ordinal);
+  return {
+    ctx: ctx,
+    addon: a,
+    resident: new WeakMap(),   // weight object -> device-resident records (uploaded once)
+    profile: false,
+    destroy: function destroy() { a.contextDestroy(ctx); },
+  };
+}
+
+// ---- validation (the reference's RangeErrors) ----------------------------------------
+
+function positiveInteger(name, value) {
+  if (!Number.isSafeInteger(value) || value <= 0) {
+    throw new RangeError(name + ' must be a positive safe integer; received ' + value);
+  }
+}
+
+function expectLength(name, value, length) {
+  const got = value === undefined || value === null ? undefined : (value.codes ? value.elements : value.length);
+  if (got !== length) {
+    throw new RangeError(name + ' has ' + got + ' values; expected ' + length);
+  }
+}
+
+// webgpu/kernels/triangle/types.js:13-48
+function validateTriangleInput(input) {
+  const shape = input.shape;
+  positiveInteger('length', shape.length);
+  positiveInteger('cZ', shape.cZ);
+  positiveInteger('cHidden', shape.cHidden);
+  const pairCount = shape.length * shape.length;
+  if (!Number.isSafeInteger(pairCount * Math.max(shape.cZ, shape.cHidden))) {
+    throw new RangeError("tensor dimensions exceed JavaScript's safe integer range");
+  }
+  expectLength('z', input.z, pairCount * shape.cZ);
+  expectLength('mask', input.mask, pairCount);
+  const w = input.weights;
+  const cZ = shape.cZ;
+  const cH = shape.cHidden;
+  const sizes = [
+    ['layerNormInWeight', cZ], ['layerNormInBias', cZ], ['linearAPWeight', cH * cZ], ['linearAPBias', cH],
+    ['linearAGWeight', cH * cZ], ['linearAGBias', cH], ['linearBPWeight', cH * cZ], ['linearBPBias', cH],
+    ['linearBGWeight', cH * cZ], ['linearBGBias', cH], ['layerNormOutWeight', cH], ['layerNormOutBias', cH],
+    ['linearZWeight', cZ * cH], ['linearZBias', cZ], ['linearGWeight', cZ * cZ], ['linearGBias', cZ],
+  ];
+  for (let i = 0; i < sizes.length; i += 1) expectLength(sizes[i][0], w[sizes[i][0]], sizes[i][1]);
+  if (input.epsilon !== undefined && (!(input.epsilon > 0) || !Number.isFinite(input.epsilon))) {
+    throw new RangeError('epsilon must be finite and positive; received ' + input.epsilon);
+  }
+}
+
+// webgpu/kernels/attention.js:15-57
+function validateAttentionInput(input) {
+  const dims = [input.batch, input.queryLength, input.channels, input.heads];
+  if (!dims.every(function ok(v) { return Number.isSafeInteger(v) && v > 0; })) {
+    throw new RangeError('attention dimensions must be positive safe integers');
+  }
+  const headDim = input.headDim || input.channels / input.heads;
+  if (!Number.isInteger(headDim) || headDim > 32) {
+    throw new RangeError('the fused attention path requires an integral head dimension no larger than 32');
+  }
+  const c = input.channels;
+  const projected = input.heads * headDim;
+  const w = input.weights;
+  const expected = [
+    ['activations', input.activations, input.batch * input.queryLength * c],
+    ['mask', input.mask, input.batch * input.queryLength],
+    ['queryNormScale', w.queryNormScale, c], ['queryNormOffset', w.queryNormOffset, c],
+    ['queryWeight', w.queryWeight, c * projected], ['keyWeight', w.keyWeight, c * projected],
+    ['valueWeight', w.valueWeight, c * projected], ['gatingWeight', w.gatingWeight, c * projected],
+    ['gatingBias', w.gatingBias, projected], ['outputWeight', w.outputWeight, projected * c],
+    ['outputBias', w.outputBias, c],
+  ];
+  for (let i = 0; i < expected.length; i += 1) expectLength(expected[i][0], expected[i][1], expected[i][2]);
+  const pair = input.pairBias;
+  if (pair !== undefined && pair !== null && pair.source === 'separate') {
+    expectLength('pair activations', pair.activations, input.queryLength * input.queryLength * pair.channels);
+    expectLength('pair norm scale', pair.layerNormScale, pair.channels);
+    expectLength('pair norm offset', pair.layerNormOffset, pair.channels);
+    expectLength('pair projection', pair.projectionWeight, pair.channels * input.heads);
+  } else if (pair !== undefined && pair !== null) {
+    expectLength('normalized-input pair projection', pair.projectionWeight, c * input.heads);
+  }
+}
+
+// webgpu/kernels/transition.js:445-460
+function validateTransitionInput(input) {
+  if (![input.rows, input.channels, input.hiddenChannels].every(function ok(v) { return Number.isSafeInteger(v) && v > 0; })) {
+    throw new RangeError('transition dimensions must be positive safe integers');
+  }
+  const w = input.weights;
+  const c = input.channels;
+  const h = input.hiddenChannels;
+  const lengths = [
+    ['activations', input.activations, input.rows * c], ['layerNormScale', w.layerNormScale, c],
+    ['layerNormOffset', w.layerNormOffset, c], ['firstWeight', w.firstWeight, c * h], ['firstBias', w.firstBias, h],
+    ['secondWeight', w.secondWeight, h * c], ['secondBias', w.secondBias, c],
+  ];
+  for (let i = 0; i < lengths.length; i += 1) expectLength(lengths[i][0], lengths[i][1], lengths[i][2]);
+}
+
+// webgpu/kernels/outer-product-mean.js:38-70
+function validateOuterProductMeanInput(input) {
+  const dims = [input.sequences, input.length, input.cM, input.cOuter, input.cZ];
+  if (!dims.every(function ok(v) { return Number.isSafeInteger(v) && v > 0; })) {
+    throw new RangeError('outer product mean dimensions must be positive safe integers');
+  }
+  const w = input.weights;
+  const expected = [
+    ['activations', input.activations, input.sequences * input.length * input.cM],
+    ['mask', input.mask, input.sequences * input.length],
+    ['layerNormScale', w.layerNormScale, input.cM], ['layerNormOffset', w.layerNormOffset, input.cM],
+    ['leftWeight', w.leftWeight, input.cM * input.cOuter], ['leftBias', w.leftBias, input.cOuter],
+    ['rightWeight', w.rightWeight, input.cM * input.cOuter], ['rightBias', w.rightBias, input.cOuter],
+    ['outputWeight', w.outputWeight, input.cOuter * input.cOuter * input.cZ], ['outputBias', w.outputBias, input.cZ],
+  ];
+  for (let i = 0; i < expected.length; i += 1) expectLength(expected[i][0], expected[i][1], expected[i][2]);
+}
+
+// webgpu/kernels/triangle/types.js:50-69, plus the relative Frobenius error
+function errorMetrics(actual, expected) {
+  if (actual.length !== expected.length || actual.length === 0) {
+    throw new RangeError('error metrics require equally sized, non-empty arrays');
+  }
+  let absoluteSum = 0;
+  let squareSum = 0;
+  let maximum = 0;
+  let expectedSquares = 0;
+  for (let i = 0; i < actual.length; i += 1) {
+    const delta = Math.abs(actual[i] - expected[i]);
+    absoluteSum += delta;
+    squareSum += delta * delta;
+    expectedSquares += expected[i] * expected[i];
+    maximum = Math.max(maximum, delta);
+  }
+  return {
+    meanAbsoluteError: absoluteSum / actual.length,
+    maxAbsoluteError: maximum,
+    rootMeanSquareError: Math.sqrt(squareSum / actual.length),
+    relativeFrobenius: Math.sqrt(squareSum) / Math.max(Math.sqrt(expectedSquares), 1e-30),
+  };
+}
+
+// ---- deterministic inputs (webgpu/testing/deterministic-input.js:1-45) ----------------
+
+function generator(seed) {
+  let state = seed >>> 0;
+  return function random() {
+    state = (state + 0x6d2b79f5) >>> 0;
+    let value = state;
+    value = Math.imul(value ^ (value >>> 15), value | 1);
+    value ^= value + Math.imul(value ^ (value >>> 7), value | 61);
+    return ((value ^ (value >>> 14)) >>> 0) / 4294967296;
+  };
+}
+
+function createDeterministicTriangleInput(shape, seed) {
+  const random = generator(seed === undefined ? 7 : seed);
+  const values = function values(length, scale, center) {
+    const output = new Float32Array(length);
+    const c = center === undefined ? 0 : center;
+    for (let i = 0; i < length; i += 1) output[i] = c + (random() * 2 - 1) * scale;
+    return output;
+  };
+  const cZ = shape.cZ;
+  const cH = shape.cHidden;
+  const pairs = shape.length * shape.length;
+  const rz = 0.15 / Math.sqrt(cZ);
+  const weights = {};
+  weights.layerNormInWeight = values(cZ, 0.1, 1);
+  weights.layerNormInBias = values(cZ, 0.05);
+  weights.linearAPWeight = values(cH * cZ, rz);
+  weights.linearAPBias = values(cH, 0.03);
+  weights.linearAGWeight = values(cH * cZ, rz);
+  weights.linearAGBias = values(cH, 0.03, 1);
+  weights.linearBPWeight = values(cH * cZ, rz);
+  weights.linearBPBias = values(cH, 0.03);
+  weights.linearBGWeight = values(cH * cZ, rz);
+  weights.linearBGBias = values(cH, 0.03, 1);
+  weights.layerNormOutWeight = values(cH, 0.1, 1);
+  weights.layerNormOutBias = values(cH, 0.05);
+  weights.linearZWeight = values(cZ * cH, 0.15 / Math.sqrt(cH));
+  weights.linearZBias = values(cZ, 0.03);
+  weights.linearGWeight = values(cZ * cZ, rz);
+  weights.linearGBias = values(cZ, 0.03, 1);
+  const mask = new Float32Array(pairs);
+  for (let i = 0; i < pairs; i += 1) mask[i] = random() > 0.15 ? 1 : 0;
+  return { shape: shape, z: values(pairs * cZ, 1), mask: mask, weights: weights };
+}
+
+// ---- device uploads ----------------------------------------------------------------------
+
+// One run's (or one resident weight set's) device buffers.
+function Uploads(device) {
+  this.device = device;
+  this.buffers = [];
+}
+Uploads.prototype.buffer = function buffer(typed) {
+  const b = this.device.addon.upload(this.device.ctx, typed);
+  this.buffers.push(b);
+  return b;
+};
+Uploads.prototype.alloc = function alloc(bytes) {
+  const b = this.device.addon.alloc(this.device.ctx, bytes);
+  this.buffers.push(b);
+  return b;
+};
+Uploads.prototype.vec = function vec(values) {
+  if (values === undefined || values === null) return null;
+  return this.buffer(values instanceof Float32Array ? values : Float32Array.from(values));
+};
+// A weight matrix stored rows x cols in `layout` ('in_out' or 'out_in'): Float32Array values
+// or a quantised record {dtype, codes, scales, zeros?, block}.
+Uploads.prototype.weight = function weight(value, layout, rows, cols) {
+  if (value === undefined || value === null) return null;
+  if (value.codes !== undefined) {
+    return {
+      dtype: value.dtype, layout: layout, rows: rows, cols: cols, group: value.block || 0,
+      data: this.buffer(value.codes), scales: this.buffer(value.scales),
+      zeros: value.zeros ? this.buffer(value.zeros) : null,
+    };
+  }
+  return { dtype: 'float32', layout: layout, rows: rows, cols: cols, group: 0, data: this.vec(value) };
+};
+Uploads.prototype.release = function release() {
+  for (let i = 0; i < this.buffers.length; i += 1) this.device.addon.free(this.buffers[i]);
+  this.buffers = [];
+};
+
+// Resident (cached) device weights for a host weight object: uploaded on first use.
+function resident(device, key, build) {
+  let entry = device.resident.get(key);
+  if (entry === undefined) {
+    const up = new Uploads(device);
+    entry = { uploads: up, value: build(up) };
+    device.resident.set(key, entry);
+  }
+  return entry.value;
+}
+
+function finish(device, up, outputs, start) {
+  const results = outputs.map(function download(o) {
+    const host = new Float32Array(o.elements);
+    device.addon.download(device.ctx, o.buffer, host);
+    return host;
+  });
+  const elapsed = performance.now() - start;
+  const kernels = device.profile ? device.addon.profileRead(device.ctx) : [];
+  const memory = device.addon.memoryStats(device.ctx);
+  up.release();
+  return { results: results, elapsedMilliseconds: elapsed, memory: memory, kernels: kernels };
+}
+
+// ---- weight-set builders (reference names -> addon records) ------------------------------
+
+function triangleWeights(up, w, cZ, cH) {
+  return {
+    lnInScale: up.vec(w.layerNormInWeight), lnInOffset: up.vec(w.layerNormInBias),
+    ap: up.weight(w.linearAPWeight, 'out_in', cH, cZ), ag: up.weight(w.linearAGWeight, 'out_in', cH, cZ),
+    bp: up.weight(w.linearBPWeight, 'out_in', cH, cZ), bg: up.weight(w.linearBGWeight, 'out_in', cH, cZ),
+    apBias: up.vec(w.linearAPBias), agBias: up.vec(w.linearAGBias),
+    bpBias: up.vec(w.linearBPBias), bgBias: up.vec(w.linearBGBias),
+    lnOutScale: up.vec(w.layerNormOutWeight), lnOutOffset: up.vec(w.layerNormOutBias),
+    wz: up.weight(w.linearZWeight, 'out_in', cZ, cH), wzBias: up.vec(w.linearZBias),
+    wg: up.weight(w.linearGWeight, 'out_in', cZ, cZ), wgBias: up.vec(w.linearGBias),
+  };
+}
+
+function attentionWeights(up, w, c, projected, pairBias, heads) {
+  const out = {
+    normScale: up.vec(w.queryNormScale), normOffset: up.vec(w.queryNormOffset),
+    wq: up.weight(w.queryWeight, 'in_out', c, projected), wk: up.weight(w.keyWeight, 'in_out', c, projected),
+    wv: up.weight(w.valueWeight, 'in_out', c, projected), wg: up.weight(w.gatingWeight, 'in_out', c, projected),
+    wo: up.weight(w.outputWeight, 'in_out', projected, c),
+    gBias: up.vec(w.gatingBias), oBias: up.vec(w.outputBias),
+  };
+  if (pairBias) {
+    const pc = pairBias.source === 'separate' ? pairBias.channels : c;
+    out.wb = up.weight(pairBias.projectionWeight, 'in_out', pc, heads);
+    if (pairBias.source === 'separate') {
+      out.pairNormScale = up.vec(pairBias.layerNormScale);
+      out.pairNormOffset = up.vec(pairBias.layerNormOffset);
+    }
+  }
+  return out;
+}
+
+function transitionWeights(up, w, c, h) {
+  return {
+    normScale: up.vec(w.layerNormScale), normOffset: up.vec(w.layerNormOffset),
+    w1: up.weight(w.firstWeight, 'in_out', c, h), b1: up.vec(w.firstBias),
+    w2: up.weight(w.secondWeight, 'in_out', h, c), b2: up.vec(w.secondBias),
+  };
+}
+
+function opmWeights(up, w, cM, cOuter, cZ) {
+  return {
+    normScale: up.vec(w.layerNormScale), normOffset: up.vec(w.layerNormOffset),
+    wl: up.weight(w.leftWeight, 'in_out', cM, cOuter), bl: up.vec(w.leftBias),
+    wr: up.weight(w.rightWeight, 'in_out', cM, cOuter), br: up.vec(w.rightBias),
+    wo: up.weight(w.outputWeight, 'in_out', cOuter * cOuter, cZ), bo: up.vec(w.outputBias),
+  };
+}
+
+// ---- kernels-as-library classes -------------------------------------------------------
+
+// webgpu/kernels/triangle/webgpu.js:38-169
+function TriangleMultiplicationGpu(device, direction) {
+  this.device = device;
+  this.direction = direction;
+}
+TriangleMultiplicationGpu.prototype.run = function run(input, options) {
+  const self = this;
+  return new Promise(function execute(resolve) {
+    validateTriangleInput(input);
+    const dev = self.device;
+    const shape = input.shape;
+    const up = new Uploads(dev);
+    const start = performance.now();
+    if (options && options.profile) { dev.profile = true; dev.addon.profileEnable(dev.ctx, true); }
+    const weights = resident(dev, input.weights, function build(wu) {
+      return triangleWeights(wu, input.weights, shape.cZ, shape.cHidden);
+    });
+    const elements = shape.length * shape.length * shape.cZ;
+    const z = up.vec(input.z);
+    const out = up.alloc(elements * 4);
+    dev.addon.triMult(dev.ctx, {
+      direction: DIRECTION[self.direction], dialect: 0, length: shape.length, cZ: shape.cZ,
+      cHidden: shape.cHidden, actDtype: ACT.float32, z: z, mask: up.vec(input.mask), out: out,
+      accumulate: 0, epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon, weights: weights,
+    });
+    const r = finish(dev, up, [{ buffer: out, elements: elements }], start);
+    resolve({ output: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
+  });
+};
+
+function TriangleMultiplicationOutgoingGpu(device) { TriangleMultiplicationGpu.call(this, device, 'outgoing'); }
+TriangleMultiplicationOutgoingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+function TriangleMultiplicationIncomingGpu(device) { TriangleMultiplicationGpu.call(this, device, 'incoming'); }
+TriangleMultiplicationIncomingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+
+// webgpu/kernels/attention.js:2580-2739: returns the update in the activation's layout
+function AttentionGpu(device) { this.device = device; }
+AttentionGpu.prototype.run = function run(input) {
+  const self = this;
+  return new Promise(function execute(resolve) {
+    validateAttentionInput(input);
+    const dev = self.device;
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const c = input.channels;
+    const headDim = input.headDim || c / input.heads;
+    const pb = input.pairBias || null;
+    const weights = resident(dev, input.weights, function build(wu) {
+      return attentionWeights(wu, input.weights, c, input.heads * headDim, pb, input.heads);
+    });
+    const elements = input.batch * input.queryLength * c;
+    const out = up.alloc(elements * 4);
+    const args = {
+      batch: input.batch, queries: input.queryLength, channels: c, heads: input.heads,
+      headDim: input.headDim || 0, transpose: input.transpose ? 1 : 0, actDtype: ACT.float32,
+      act: up.vec(input.activations), mask: up.vec(input.mask), out: out, accumulate: 0,
+      biasMode: pb ? BIAS[pb.source] : 0, epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+      weights: weights,
+    };
+    if (pb && pb.source === 'separate') {
+      args.pair = up.vec(pb.activations);
+      args.pairDtype = ACT.float32;
+      args.pairChannels = pb.channels;
+    }
+    dev.addon.attention(dev.ctx, args);
+    const r = finish(dev, up, [{ buffer: out, elements: elements }], start);
+    resolve({ output: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
+  });
+};
+
+// webgpu/kernels/transition.js:1009-1105: returns the update
+function TransitionGpu(device, options) { this.device = device; this.options = options || {}; }
+TransitionGpu.prototype.run = function run(input) {
+  const self = this;
+  return new Promise(function execute(resolve) {
+    validateTransitionInput(input);
+    const dev = self.device;
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const weights = resident(dev, input.weights, function build(wu) {
+      return transitionWeights(wu, input.weights, input.channels, input.hiddenChannels);
+    });
+    const elements = input.rows * input.channels;
+    const out = up.alloc(elements * 4);
+    dev.addon.transition(dev.ctx, {
+      kind: 0, rows: input.rows, channels: input.channels, hidden: input.hiddenChannels, actDtype: ACT.float32,
+      act: up.vec(input.activations), out: out, accumulate: 0,
+      chunkBytes: self.options.transitionBufferLimit || 0,
+      epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon, weights: weights,
+    });
+    const r = finish(dev, up, [{ buffer: out, elements: elements }], start);
+    resolve({ output: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
+  });
+};
+
+// webgpu/kernels/outer-product-mean.js:1748-1907: returns the pair update
+function OuterProductMeanGpu(device) { this.device = device; }
+OuterProductMeanGpu.prototype.run = function run(input) {
+  const self = this;
+  return new Promise(function execute(resolve) {
+    validateOuterProductMeanInput(input);
+    const dev = self.device;
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const weights = resident(dev, input.weights, function build(wu) {
+      return opmWeights(wu, input.weights, input.cM, input.cOuter, input.cZ);
+    });
+    const elements = input.length * input.length * input.cZ;
+    const out = up.alloc(elements * 4);
+    dev.addon.outerProductMean(dev.ctx, {
+      sequences: input.sequences, length: input.length, cM: input.cM, cOuter: input.cOuter, cZ: input.cZ,
+      msaDtype: ACT.float32, msa: up.vec(input.activations), mask: up.vec(input.mask),
+      pairDtype: ACT.float32, out: out, accumulate: 0,
+      epsilon: input.layerNormEpsilon === undefined ? 1e-5 : input.layerNormEpsilon,
+      normEpsilon: input.normalizationEpsilon === undefined ? 1e-3 : input.normalizationEpsilon,
+      weights: weights,
+    });
+    const r = finish(dev, up, [{ buffer: out, elements: elements }], start);
+    resolve({ output: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
+  });
+};
+
+function evoformerBlockWeights(up, w, dims) {
+  const row = w.msaRowAttention;
+  const col = w.msaColumnAttention;
+  const st = w.triangleAttentionStarting;
+  const en = w.triangleAttentionEnding;
+  return {
+    rowAttention: attentionWeights(up, row.attention, dims.cM, dims.cM,
+      { source: 'separate', channels: dims.cZ, layerNormScale: row.pairBias.layerNormScale,
+        layerNormOffset: row.pairBias.layerNormOffset, projectionWeight: row.pairBias.projectionWeight }, row.heads),
+    rowHeads: row.heads,
+    columnAttention: attentionWeights(up, col.attention, dims.cM, dims.cM, null, col.heads),
+    columnHeads: col.heads,
+    msaTransition: transitionWeights(up, w.msaTransition, dims.cM, dims.msaHidden),
+    outerProductMean: opmWeights(up, w.outerProductMean, dims.cM, dims.cOuter, dims.cZ),
+    triOut: triangleWeights(up, w.triangleMultiplicationOutgoing, dims.cZ, dims.triangleHidden),
+    triIn: triangleWeights(up, w.triangleMultiplicationIncoming, dims.cZ, dims.triangleHidden),
+    triAttStart: attentionWeights(up, st.attention, dims.cZ, dims.cZ,
+      { source: 'normalized-input', projectionWeight: st.pairBias.projectionWeight }, st.heads),
+    triAttStartHeads: st.heads,
+    triAttEnd: attentionWeights(up, en.attention, dims.cZ, dims.cZ,
+      { source: 'normalized-input', projectionWeight: en.pairBias.projectionWeight }, en.heads),
+    triAttEndHeads: en.heads,
+    pairTransition: transitionWeights(up, w.pairTransition, dims.cZ, dims.pairHidden),
+  };
+}
+
+function blockDims(input, w) {
+  return {
+    cM: input.cM, cZ: input.cZ, cOuter: input.cOuter, triangleHidden: input.triangleHidden,
+    msaHidden: input.msaHidden || (w.msaTransition.firstBias.length),
+    pairHidden: input.pairHidden || (w.pairTransition.firstBias.length),
+  };
+}
+
+function runEvoformer(device, input, blockWeights) {
+  return new Promise(function execute(resolve) {
+    const dims = blockDims(input, blockWeights[0]);
+    const up = new Uploads(device);
+    const start = performance.now();
+    const ws = blockWeights.map(function each(w) {
+      return resident(device, w, function build(wu) { return evoformerBlockWeights(wu, w, dims); });
+    });
+    const msaElements = input.sequences * input.length * input.cM;
+    const pairElements = input.length * input.length * input.cZ;
+    expectLength('msa', input.msa, msaElements);
+    expectLength('pair', input.pair, pairElements);
+    const msa = up.vec(input.msa);
+    const pair = up.vec(input.pair);
+    device.addon.evoformerStack(device.ctx, {
+      sequences: input.sequences, length: input.length, cM: dims.cM, cZ: dims.cZ, cOuter: dims.cOuter,
+      triangleHidden: dims.triangleHidden, msaHidden: dims.msaHidden, pairHidden: dims.pairHidden,
+      msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair,
+      msaMask: up.vec(input.msaMask), pairMask: up.vec(input.pairMask), epsilon: 1e-5,
+    }, ws);
+    const r = finish(device, up, [{ buffer: msa, elements: msaElements }, { buffer: pair, elements: pairElements }],
+      start);
+    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels });
+  });
+}
+
+// webgpu/af2/evoformer/block.js:1783-1824
+function EvoformerBlockGpu(device) { this.device = device; }
+EvoformerBlockGpu.prototype.run = function run(input) {
+  return runEvoformer(this.device, input, [input.weights]);
+};
+
+// webgpu/af2/evoformer/stack.js:44-160: input.blocks is the per-block weight list
+function EvoformerStackGpu(device) { this.device = device; }
+EvoformerStackGpu.prototype.run = function run(input) {
+  return runEvoformer(this.device, input, input.blocks);
+};
+
+// shared/bundles/node.js:11-40: a triangle fixture directory (manifest.json + *.f32.bin)
+const TRIANGLE_WEIGHT_NAMES = [
+  'layerNormInWeight', 'layerNormInBias', 'linearAPWeight', 'linearAPBias', 'linearAGWeight', 'linearAGBias',
+  'linearBPWeight', 'linearBPBias', 'linearBGWeight', 'linearBGBias', 'layerNormOutWeight', 'layerNormOutBias',
+  'linearZWeight', 'linearZBias', 'linearGWeight', 'linearGBias',
+];
+
+function loadTriangleReferenceBundleFromFiles(manifestPath) {
+  return new Promise(function load(resolve) {
+    const manifest = JSON.parse(fs.readFileSync(manifestPath, 'utf8'));
+    if (manifest.formatVersion !== 1 || manifest.operator !== 'TriangleMultiplicationOutgoing') {
+      throw new Error('unsupported triangle reference manifest');
+    }
+    const directory = path.dirname(manifestPath);
+    const tensor = function tensor(name) {
+      const record = manifest.tensors[name];
+      if (record === undefined || record.dtype !== 'float32') throw new Error('missing float32 tensor ' + name);
+      const bytes = fs.readFileSync(path.resolve(directory, record.file));
+      const count = record.shape.reduce(function mul(a, b) { return a * b; }, 1);
+      if (bytes.byteLength !== count * 4) throw new Error('invalid byte length for tensor ' + name);
+      return new Float32Array(bytes.buffer.slice(bytes.byteOffset, bytes.byteOffset + bytes.byteLength));
+    };
+    const weights = {};
+    TRIANGLE_WEIGHT_NAMES.forEach(function each(name) { weights[name] = tensor(name); });
+    resolve({
+      source: manifest.source,
+      input: { shape: manifest.shape, epsilon: manifest.epsilon, z: tensor('z'), mask: tensor('mask'), weights: weights },
+      expected: tensor('expected'),
+    });
+  });
+}
+
+module.exports = {
+  loadTriangleReferenceBundleFromFiles: loadTriangleReferenceBundleFromFiles,
+  createDevice: createDevice,
+  TriangleMultiplicationOutgoingGpu: TriangleMultiplicationOutgoingGpu,
+  TriangleMultiplicationIncomingGpu: TriangleMultiplicationIncomingGpu,
+  AttentionGpu: AttentionGpu,
+  TransitionGpu: TransitionGpu,
+  OuterProductMeanGpu: OuterProductMeanGpu,
+  EvoformerBlockGpu: EvoformerBlockGpu,
+  EvoformerStackGpu: EvoformerStackGpu,
+  validateTriangleInput: validateTriangleInput,
+  validateAttentionInput: validateAttentionInput,
+  validateTransitionInput: validateTransitionInput,
+  validateOuterProductMeanInput: validateOuterProductMeanInput,
+  errorMetrics: errorMetrics,
+  generator: generator,
+  createDeterministicTriangleInput: createDeterministicTriangleInput,
+  addon: addon,
+};

@@ -1,0 +1,72 @@
+'use strict';
+// CPU checks of the Node host (no GPU): the reference's validation errors and errorMetrics
+// (test/cpu-reference.test.js:29-41), the generator against Python's vectorised restatement
+// (values passed in a JSON file), and the addon's exported functions.
+//   node cpu.test.js <generator-expectations.json>
+const assert = require('assert');
+const fs = require('fs');
+const lf = require('../index.js');
+
+let failures = 0;
+function check(name, fn) {
+  try { fn(); console.log('ok   ' + name); } catch (e) { failures += 1; console.log('FAIL ' + name + ': ' + e.message); }
+}
+
+check('deterministic input has one value per pair channel', function t() {
+  const a = lf.createDeterministicTriangleInput({ length: 3, cZ: 4, cHidden: 5 }, 42);
+  const b = lf.createDeterministicTriangleInput({ length: 3, cZ: 4, cHidden: 5 }, 42);
+  assert.strictEqual(a.z.length, 36);
+  assert.deepStrictEqual(Array.from(a.z), Array.from(b.z));
+});
+
+check('rejects inconsistent tensor shapes', function t() {
+  const input = lf.createDeterministicTriangleInput({ length: 2, cZ: 3, cHidden: 2 });
+  assert.throws(function bad() { lf.validateTriangleInput(Object.assign({}, input, { z: input.z.subarray(1) })); },
+    /z has/);
+  assert.throws(function bad() {
+    lf.validateTriangleInput(Object.assign({}, input, { shape: { length: 0, cZ: 3, cHidden: 2 } }));
+  }, RangeError);
+  assert.throws(function bad() { lf.validateTriangleInput(Object.assign({}, input, { epsilon: -1 })); },
+    /epsilon must be finite and positive/);
+});
+
+check('attention validation', function t() {
+  const c = 64;
+  const w = {
+    queryNormScale: new Float32Array(c), queryNormOffset: new Float32Array(c), queryWeight: new Float32Array(c * c),
+    keyWeight: new Float32Array(c * c), valueWeight: new Float32Array(c * c), gatingWeight: new Float32Array(c * c),
+    gatingBias: new Float32Array(c), outputWeight: new Float32Array(c * c), outputBias: new Float32Array(c),
+  };
+  const ok = { batch: 2, queryLength: 3, channels: c, heads: 2, activations: new Float32Array(2 * 3 * c),
+    mask: new Float32Array(6), weights: w };
+  lf.validateAttentionInput(ok);
+  assert.throws(function bad() { lf.validateAttentionInput(Object.assign({}, ok, { heads: 1 })); },
+    /head dimension no larger than 32/);
+  assert.throws(function bad() { lf.validateAttentionInput(Object.assign({}, ok, { mask: new Float32Array(5) })); },
+    /mask has 5 values; expected 6/);
+});
+
+check('reports exact error metrics', function t() {
+  const m = lf.errorMetrics(new Float32Array([1, 3]), new Float32Array([2, 1]));
+  assert.strictEqual(m.meanAbsoluteError, 1.5);
+  assert.strictEqual(m.maxAbsoluteError, 2);
+  assert.strictEqual(m.rootMeanSquareError, Math.sqrt(2.5));
+});
+
+check('generator matches the vectorised restatement', function t() {
+  const cases = JSON.parse(fs.readFileSync(process.argv[2], 'utf8'));
+  cases.forEach(function each(c) {
+    const random = lf.generator(c.seed);
+    for (let i = 0; i < c.values.length; i += 1) assert.strictEqual(random(), c.values[i], 'seed ' + c.seed + ' draw ' + i);
+  });
+});
+
+check('addon exports every entry point', function t() {
+  const names = ['contextCreate', 'contextDestroy', 'upload', 'alloc', 'download', 'free', 'synchronize', 'memoryStats',
+    'profileEnable', 'profileRead', 'triMult', 'attention', 'transition', 'outerProductMean', 'evoformerStack',
+    'pairformerBlock', 'version'];
+  const a = lf.addon();
+  names.forEach(function each(n) { assert.strictEqual(typeof a[n], 'function', n); });
+});
+
+process.exitCode = failures === 0 ? 0 : 1;

@@ -1,0 +1,75 @@
+'use strict';
+// GPU checks of the Node host on an MI355X: the reference's own GPU test pattern
+// (test/triangle-multiplication-outgoing.gpu.test.js:31-69) on the committed fixtures written
+// out in the reference's manifest format, plus oracle cases for the other classes.
+//   node gpu.test.js <case directory written by tests/test_js_host.py>
+const assert = require('assert');
+const fs = require('fs');
+const path = require('path');
+const lf = require('../index.js');
+
+const dir = process.argv[2];
+const device = lf.createDevice(0);
+let failures = 0;
+
+function f32(name) {
+  const b = fs.readFileSync(path.join(dir, name));
+  return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+}
+
+function report(name, metrics, bounds) {
+  const ok = metrics.meanAbsoluteError < bounds.mean && metrics.maxAbsoluteError < bounds.max;
+  if (!ok) failures += 1;
+  console.log((ok ? 'ok   ' : 'FAIL ') + name + ' ' + JSON.stringify(metrics));
+}
+
+function loadWeights(prefix, names) {
+  const w = {};
+  names.forEach(function each(n) { w[n] = f32(prefix + n + '.f32.bin'); });
+  return w;
+}
+
+async function main() {
+  const cases = JSON.parse(fs.readFileSync(path.join(dir, 'cases.json'), 'utf8'));
+  for (const fixture of cases.fixtures) {
+    const bundle = await lf.loadTriangleReferenceBundleFromFiles(path.join(dir, fixture, 'manifest.json'));
+    const out = await new lf.TriangleMultiplicationOutgoingGpu(device).run(bundle.input, { precision: 'f32' });
+    // the reference's f16 bounds for these fixtures
+    report('triangle outgoing ' + fixture, lf.errorMetrics(out.output, bundle.expected), { mean: 1e-3, max: 1e-2 });
+  }
+  const inc = cases.incoming;
+  const bundle = await lf.loadTriangleReferenceBundleFromFiles(path.join(dir, inc.fixture, 'manifest.json'));
+  const outIn = await new lf.TriangleMultiplicationIncomingGpu(device).run(bundle.input);
+  report('triangle incoming ' + inc.fixture, lf.errorMetrics(outIn.output, f32(inc.expected)), { mean: 1e-3, max: 1e-2 });
+
+  const at = cases.attention;
+  const attentionWeights = loadWeights('attention.', at.names);
+  const attIn = {
+    batch: at.batch, queryLength: at.queries, channels: at.channels, heads: at.heads, transpose: at.transpose,
+    activations: f32('attention.act.f32.bin'), mask: f32('attention.mask.f32.bin'), weights: attentionWeights,
+    pairBias: { source: 'normalized-input', projectionWeight: f32('attention.pairProjection.f32.bin') },
+  };
+  const attOut = await new lf.AttentionGpu(device).run(attIn);
+  report('attention (triangle ending)', lf.errorMetrics(attOut.output, f32('attention.expected.f32.bin')),
+    { mean: 2e-3, max: 2e-2 });
+
+  const tr = cases.transition;
+  const trOut = await new lf.TransitionGpu(device).run({
+    rows: tr.rows, channels: tr.channels, hiddenChannels: tr.hidden, activations: f32('transition.act.f32.bin'),
+    weights: loadWeights('transition.', tr.names),
+  });
+  report('transition', lf.errorMetrics(trOut.output, f32('transition.expected.f32.bin')), { mean: 2e-3, max: 2e-2 });
+
+  const op = cases.opm;
+  const opOut = await new lf.OuterProductMeanGpu(device).run({
+    sequences: op.sequences, length: op.length, cM: op.cM, cOuter: op.cOuter, cZ: op.cZ,
+    activations: f32('opm.act.f32.bin'), mask: f32('opm.mask.f32.bin'), weights: loadWeights('opm.', op.names),
+  });
+  report('outer product mean', lf.errorMetrics(opOut.output, f32('opm.expected.f32.bin')), { mean: 2e-3, max: 2e-2 });
+
+  assert.ok(opOut.memory.peakBytes > 0);
+  device.destroy();
+  process.exitCode = failures === 0 ? 0 : 1;
+}
+
+main().catch(function fail(e) { console.log('FAIL ' + e.stack); process.exitCode = 1; });
