@@ -58,12 +58,110 @@ def cpu_baseline(c2, budget_s=30.0):
             "sample": sample + f"; numpy oracle, {secs:.1f} s per step", "ms_per_step": round(secs * 1e3, 1)}
 
 
+def tri_attention_flops(n, c=128, heads=4, d=32):
+    """One triangle-attention direction: q/k/v/gate + bias projections, QK^T and PV, output."""
+    p = n * n
+    return 2 * p * c * (4 * heads * d + heads) + 4 * n * n * n * heads * d + 2 * p * heads * d * c
+
+
+def profile_ops(ctx, fn, reps):
+    """Mean ms per call of each labelled launch over `reps` calls of fn (library hipEvents)."""
+    import torch
+    ctx.profile(True)
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    recs = ctx.read_profile()
+    ctx.profile(False)
+    per = {}
+    for label, t in recs:
+        per[label] = per.get(label, 0.0) + t
+    return {k: round(v / reps, 4) for k, v in sorted(per.items(), key=lambda kv: -kv[1])}
+
+
+def timed(fn, reps):
+    import torch
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def triangle_attention_config3(ctx, D, synthetic, reps):
+    """starting then ending node triangle attention, N=512, fp16."""
+    import torch
+    from localfold_amd import capi
+    c3 = synthetic.config3_inputs()
+    n = c3["pair"].shape[0]
+    dev = ctx.device
+    dw = D.DeviceWeights(dev)
+    w_s = D.attention_weights_af2(dw, c3["starting"]["attention"], c3["starting"]["pairBias"])
+    w_e = D.attention_weights_af2(dw, c3["ending"]["attention"], c3["ending"]["pairBias"])
+    z0 = torch.as_tensor(c3["pair"]).to(dev).to(torch.float16)
+    mask = torch.as_tensor(c3["mask"]).to(dev)
+    z1, z2 = torch.empty_like(z0), torch.empty_like(z0)
+    del c3
+
+    def step():
+        D.attention(ctx, z0, mask, w_s, 4, False, capi.LF_BIAS_NORMALIZED_INPUT, out=z1, accumulate=True)
+        D.attention(ctx, z1, mask, w_e, 4, True, capi.LF_BIAS_NORMALIZED_INPUT, out=z2, accumulate=True)
+
+    step()
+    ms = timed(step, reps)
+    flops = 2 * tri_attention_flops(n)
+    kern = profile_ops(ctx, step, 3)
+    flash = sum(v for k, v in kern.items() if k.endswith(".flash"))
+    flash_flops = 2 * 4 * n ** 3 * 128
+    return {"workload": "BASELINE config 3: triangle attention starting then ending node, N_res=512, c_z=128, "
+                        "4x32 heads, fp16 pair and weights, last 26 residues masked",
+            "ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "pct_of_mfma_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 2),
+            "flash_tflops": round(flash_flops / (flash * 1e-3) / 1e12, 2) if flash else None,
+            "kernels_ms": kern}
+
+
+def evoformer_block_config4(ctx, D, synthetic, reps):
+    """BASELINE config 4 at one block: N_res=384, N_seq=512, int8 weights, bf16 activations."""
+    import torch
+    c4 = synthetic.config4_inputs()
+    dev = ctx.device
+    dw = D.DeviceWeights(dev)
+    w = c4["weights"]
+    ws = D.evoformer_weights(dw, w)
+    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16)
+    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16)
+    mm = torch.as_tensor(c4["msa_mask"]).to(dev)
+    pm = torch.as_tensor(c4["pair_mask"]).to(dev)
+    msa0, pair0 = msa.clone(), pair.clone()
+    s_, n = c4["msa_mask"].shape
+    del c4
+
+    def block():
+        D.evoformer_block(ctx, msa, pair, mm, pm, ws, w)
+
+    block()
+    msa.copy_(msa0)
+    pair.copy_(pair0)
+    ms = timed(block, reps)
+    kern = profile_ops(ctx, block, 2)
+    finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
+    return {"workload": f"BASELINE config 4, one AF2 Evoformer block: N_res={n}, N_seq={s_}, c_m=256, c_z=128, "
+                        "int8 weights (fp16 scales, groups of 64), bf16 activations",
+            "ms_per_block": round(ms, 3), "stack_48_blocks_s_estimate": round(48 * ms / 1e3, 3),
+            "outputs_finite": finite, "kernels_ms": kern}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the config 3 / config 4 measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the pair stack's row "
@@ -138,6 +236,13 @@ def main():
     roof["mfma_tflops"] = round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2)
     roof["traffic"] = None
 
+    extras = {}
+    if not args.no_extras:
+        log("config 3: triangle attention ...")
+        extras["triangle_attention"] = triangle_attention_config3(ctx, D, synthetic, 10)
+        log("config 4: one Evoformer block ...")
+        extras["evoformer_block"] = evoformer_block_config4(ctx, D, synthetic, 5)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle ...")
@@ -167,6 +272,8 @@ def main():
         "wall_s": round(wall, 3),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "evoformer_block": extras.get("evoformer_block"),
+        "triangle_attention": extras.get("triangle_attention"),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

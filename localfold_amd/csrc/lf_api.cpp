@@ -52,7 +52,7 @@ int workspace(lf_context* ctx, const size_t* sizes, void** out, int n) {
 LaunchScope::LaunchScope(lf_context* c, const char* label) : ctx(c) {
   if (!ctx->profile) return;
   lf_context::Rec r;
-  r.label = label;
+  r.label = ctx->label_prefix ? std::string(ctx->label_prefix) + "/" + label : std::string(label);
   if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return;
   hipEventRecord(r.start, ctx->stream);
   ctx->recs.push_back(r);

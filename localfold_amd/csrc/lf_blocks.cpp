@@ -33,6 +33,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.pair_channels = a.c_z;
     x.epsilon = eps;
     x.w = &w.row_attention;
+    StageScope stage(ctx, "row_attention");
     LF_TRY(attention(ctx, x));
   }
   {  // 2. MSA column attention
@@ -49,6 +50,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.accumulate = 1;
     x.epsilon = eps;
     x.w = &w.column_attention;
+    StageScope stage(ctx, "column_attention");
     LF_TRY(attention(ctx, x));
   }
   {  // 3. MSA transition
@@ -64,6 +66,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.chunk_bytes = chunk;
     x.epsilon = eps;
     x.w = &w.msa_transition;
+    StageScope stage(ctx, "msa_transition");
     LF_TRY(transition(ctx, x));
   }
   {  // 4. outer product mean into the pair
@@ -83,6 +86,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.epsilon = eps;
     x.norm_epsilon = 1e-3f;
     x.w = &w.outer_product_mean;
+    StageScope stage(ctx, "outer_product_mean");
     LF_TRY(outer_product_mean(ctx, x));
   }
   for (int dir = 0; dir < 2; ++dir) {  // 5, 6. triangle multiplication outgoing, incoming
@@ -99,6 +103,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.accumulate = 1;
     x.epsilon = eps;
     x.w = dir == 0 ? &w.tri_out : &w.tri_in;
+    StageScope stage(ctx, dir == 0 ? "tri_mult_outgoing" : "tri_mult_incoming");
     LF_TRY(tri_mult(ctx, x));
   }
   for (int end = 0; end < 2; ++end) {  // 7, 8. triangle attention starting, ending
@@ -116,6 +121,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.bias_mode = LF_BIAS_NORMALIZED_INPUT;
     x.epsilon = eps;
     x.w = end ? &w.tri_att_end : &w.tri_att_start;
+    StageScope stage(ctx, end ? "tri_attention_ending" : "tri_attention_starting");
     LF_TRY(attention(ctx, x));
   }
   {  // 9. pair transition
@@ -131,6 +137,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     x.chunk_bytes = chunk;
     x.epsilon = eps;
     x.w = &w.pair_transition;
+    StageScope stage(ctx, "pair_transition");
     LF_TRY(transition(ctx, x));
   }
   return LF_OK;
@@ -159,6 +166,7 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
     x.accumulate = 1;
     x.epsilon = eps;
     x.w = dir == 0 ? &w.tri_out : &w.tri_in;
+    StageScope stage(ctx, dir == 0 ? "tri_mult_outgoing" : "tri_mult_incoming");
     LF_TRY(tri_mult(ctx, x));
   }
   for (int end = 0; end < 2; ++end) {
@@ -181,6 +189,7 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
     x.swap_bias = end && !a.swap_transposed_bias;
     x.epsilon = eps;
     x.w = end ? &w.att_end : &w.att_start;
+    StageScope stage(ctx, end ? "tri_attention_ending" : "tri_attention_starting");
     LF_TRY(attention(ctx, x));
   }
   {
@@ -197,6 +206,7 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
     x.chunk_bytes = chunk;
     x.epsilon = eps;
     x.w = &w.pair_transition;
+    StageScope stage(ctx, "pair_transition");
     LF_TRY(transition(ctx, x));
   }
   if (!a.single) return LF_OK;
@@ -224,6 +234,7 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
     x.pair_channels = a.c_z;
     x.epsilon = eps;
     x.w = &sw;
+    StageScope stage(ctx, "single_attention");
     LF_TRY(attention(ctx, x));
   }
   {
@@ -240,6 +251,7 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
     x.chunk_bytes = chunk;
     x.epsilon = eps;
     x.w = &w.single_transition;
+    StageScope stage(ctx, "single_transition");
     LF_TRY(transition(ctx, x));
   }
   return LF_OK;

@@ -21,6 +21,7 @@ struct lf_context {
   std::vector<std::pair<void*, size_t>> user_allocs;
   // profiling
   bool profile = false;
+  const char* label_prefix = nullptr;   // block stage naming the launches (profiling only)
   struct Rec {
     std::string label;
     hipEvent_t start, stop;
@@ -43,6 +44,14 @@ struct LaunchScope {
   int idx = -1;
   LaunchScope(lf_context* c, const char* label);
   ~LaunchScope();
+};
+
+// Names the block stage that the launches inside it belong to ("stage/kernel" labels).
+struct StageScope {
+  lf_context* ctx;
+  const char* saved;
+  StageScope(lf_context* c, const char* stage) : ctx(c), saved(c->label_prefix) { c->label_prefix = stage; }
+  ~StageScope() { ctx->label_prefix = saved; }
 };
 
 }  // namespace lf

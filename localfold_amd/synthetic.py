@@ -443,3 +443,53 @@ def config1_inputs(seed: int = 0, n: int = 64, c_m: int = 256, c_z: int = 128):
     msa = s.normal(n * c_m).reshape(1, n, c_m)
     pair = s.normal(n * n * c_z).reshape(n, n, c_z)
     return w, msa, pair
+
+
+def quantise_tree(w: dict, dtype: str, block: int = 64) -> dict:
+    """Every 2-D matrix in a nested block-weight dict replaced by a flat-group codec record."""
+    out = {}
+    for k, v in w.items():
+        if isinstance(v, dict):
+            out[k] = quantise_tree(v, dtype, block)
+        elif isinstance(v, np.ndarray) and v.ndim == 2:
+            out[k] = make_record(v, dtype, block=block)
+        else:
+            out[k] = v
+    return out
+
+
+def config3_inputs(n: int = 512, c: int = 128, heads: int = 4, seed: int = 33):
+    """fp16 pair ~N(0,1), fp16 weights ~N(0,1/fan_in) for starting and ending
+    node attention, key padding with the last 5% of residues masked (rows and columns)."""
+    s = Stream(seed)
+    pair = s.normal(n * n * c).reshape(n, n, c)
+    masked = int(round(0.05 * n))
+    mask = np.ones((n, n), np.float32)
+    mask[:, n - masked:] = 0
+    mask[n - masked:, :] = 0
+    mats = ["queryWeight", "keyWeight", "valueWeight", "gatingWeight", "outputWeight"]
+    weights = []
+    for seed_w in (seed + 8, seed + 9):
+        w = config3_attention_weights(c, heads, seed_w)
+        weights.append(dict(w, attention=quantise_records(w["attention"], mats, "float16", False, 1),
+                            pairBias={"projectionWeight": make_record(w["pairBias"]["projectionWeight"], "float16")}))
+    return {"pair": pair, "mask": mask, "starting": weights[0], "ending": weights[1], "masked": masked}
+
+
+def config4_inputs(n: int = 384, sequences: int = 512, c_m: int = 256, c_z: int = 128, seed: int = 4,
+                   block: int = 64):
+    """BASELINE config 4, one block's inputs: an MSA of random tokens over 21 classes (gap
+    probability 0.2, the first row the gap-free query) embedded through a random N(0,1) table,
+    pair ~N(0,1), block weights ~N(0,1/fan_in) quantised to int8 with fp16 scales (flat groups
+    of `block`).  Masks are all ones (no padding)."""
+    w, _, _ = config1_inputs(seed=seed, n=1, c_m=c_m, c_z=c_z)
+    s = Stream(seed + 50)
+    u = s.uniform(sequences * n).reshape(sequences, n)
+    aa = np.minimum((s.uniform(sequences * n) * 20).astype(np.int64), 19).reshape(sequences, n)
+    tokens = np.where(u < 0.2, 20, aa)
+    tokens[0] = aa[0]
+    table = s.normal(21 * c_m).reshape(21, c_m).astype(np.float32)
+    msa = table[tokens]
+    pair = s.normal(n * n * c_z).reshape(n, n, c_z)
+    return {"weights": quantise_tree(w, "int8", block), "msa": msa, "pair": pair, "tokens": tokens,
+            "msa_mask": np.ones((sequences, n), np.float32), "pair_mask": np.ones((n, n), np.float32)}
