@@ -199,65 +199,104 @@ struct TriContractParams {
 
 constexpr int CT_TILE = 128, CT_BK = 64, CT_LD = CT_BK + 8;
 
-// Loads the [128 x 64] (m, k) tile of one operand into S[m][k].
+// Loads the [128 x 64] (m, k) tile of one operand into S[m][k], element by element (any N).
 // KMAJOR: element (m, k) is stored at src[k*N + m]; otherwise at src[m*N + k].
-template <bool KMAJOR, bool VEC>
+template <bool KMAJOR>
 __device__ __forceinline__ void ct_load(_Float16* S, const _Float16* src, int N, int m0, int k0, int tid) {
-  if (!KMAJOR) {
-    if (VEC) {
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int e = tid + it * 256, m = e >> 3, seg = e & 7;
-        const int gm = m0 + m, gk = k0 + seg * 8;
-        h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (gm < N && gk < N) v = *reinterpret_cast<const h8*>(src + (size_t)gm * N + gk);
-        *reinterpret_cast<h8*>(S + m * CT_LD + seg * 8) = v;
-      }
+  for (int e = tid; e < CT_TILE * CT_BK; e += 256) {
+    int m, k;
+    if (!KMAJOR) {
+      m = e / CT_BK;
+      k = e % CT_BK;
     } else {
-      for (int e = tid; e < CT_TILE * CT_BK; e += 256) {
-        const int m = e / CT_BK, k = e % CT_BK, gm = m0 + m, gk = k0 + k;
-        S[m * CT_LD + k] = (gm < N && gk < N) ? src[(size_t)gm * N + gk] : (_Float16)0.f;
-      }
+      k = e / CT_TILE;
+      m = e % CT_TILE;
     }
-  } else {
-    if (VEC) {
-      // lane -> k, so the eight 2-byte LDS stores of a wave hit 64 consecutive k (no bank conflicts)
+    const int gm = m0 + m, gk = k0 + k;
+    S[m * CT_LD + k] = (gm < N && gk < N) ? src[KMAJOR ? (size_t)gk * N + gm : (size_t)gm * N + gk] : (_Float16)0.f;
+  }
+}
+
+// Vector form (N % 8 == 0) split in two: global -> registers (issued before the current K
+// step's MFMAs so the loads are in flight during them) and registers -> LDS.
+struct CtRegs {
+  h8 v[4];
+};
+
+template <bool KMAJOR>
+__device__ __forceinline__ void ct_fetch(CtRegs& r, const _Float16* src, int N, int m0, int k0, int tid) {
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int k = tid & 63, seg = (tid >> 6) + it * 4;
-        const int gk = k0 + k, gm = m0 + seg * 8;
-        h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (gk < N && gm < N) v = *reinterpret_cast<const h8*>(src + (size_t)gk * N + gm);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) S[(seg * 8 + j) * CT_LD + k] = v[j];
-      }
+  for (int it = 0; it < 4; ++it) {
+    int gm, gk;
+    if (!KMAJOR) {
+      const int e = tid + it * 256;
+      gm = m0 + (e >> 3);
+      gk = k0 + (e & 7) * 8;
     } else {
-      for (int e = tid; e < CT_TILE * CT_BK; e += 256) {
-        const int k = e / CT_TILE, m = e % CT_TILE, gm = m0 + m, gk = k0 + k;
-        S[m * CT_LD + k] = (gm < N && gk < N) ? src[(size_t)gk * N + gm] : (_Float16)0.f;
-      }
+      gk = k0 + (tid & 63);
+      gm = m0 + ((tid >> 6) + it * 4) * 8;
+    }
+    r.v[it] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (gm < N && gk < N) r.v[it] = *reinterpret_cast<const h8*>(src + (KMAJOR ? (size_t)gk * N + gm : (size_t)gm * N + gk));
+  }
+}
+
+template <bool KMAJOR>
+__device__ __forceinline__ void ct_store(_Float16* S, const CtRegs& r, int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    if (!KMAJOR) {
+      const int e = tid + it * 256;
+      *reinterpret_cast<h8*>(S + (e >> 3) * CT_LD + (e & 7) * 8) = r.v[it];
+    } else {
+      // lane -> k, so the eight 2-byte LDS stores of a wave hit 64 consecutive k
+      const int k = tid & 63, seg = (tid >> 6) + it * 4;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) S[(seg * 8 + j) * CT_LD + k] = r.v[it][j];
     }
   }
 }
 
+// One 128x128 tile of X[h] per block.  The 1-D grid is remapped so that consecutive logical
+// blocks (the tiles of one channel, which share their A rows and B rows) run on the same
+// XCD: the hardware deals block ids round-robin over the 8 XCDs, each with its own L2.
 template <bool KMAJOR, bool VEC>
 __global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) {
   __shared__ __attribute__((aligned(16))) _Float16 Ls[CT_TILE * CT_LD];
   __shared__ __attribute__((aligned(16))) _Float16 Rs[CT_TILE * CT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.x * CT_TILE, n0 = blockIdx.y * CT_TILE, h = blockIdx.z;
+  const int tm = (p.N + CT_TILE - 1) / CT_TILE, tiles = tm * tm;
+  const int total = (int)gridDim.x, per = total >> 3;
+  int lin = (int)blockIdx.x;
+  if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
+  const int h = lin / tiles, t = lin - h * tiles;
+  const int m0 = (t / tm) * CT_TILE, n0 = (t % tm) * CT_TILE;
   const size_t plane = (size_t)p.N * p.N;
   const _Float16* L = p.L + h * plane;
   const _Float16* R = p.R + h * plane;
   f4 acc[4][4];
   zero_acc(acc);
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  CtRegs rl, rr;
+  if (VEC) {
+    ct_fetch<KMAJOR>(rl, L, p.N, m0, 0, tid);
+    ct_fetch<KMAJOR>(rr, R, p.N, n0, 0, tid);
+  }
   for (int k0 = 0; k0 < p.N; k0 += CT_BK) {
     __syncthreads();
-    ct_load<KMAJOR, VEC>(Ls, L, p.N, m0, k0, tid);
-    ct_load<KMAJOR, VEC>(Rs, R, p.N, n0, k0, tid);
+    if (VEC) {
+      ct_store<KMAJOR>(Ls, rl, tid);
+      ct_store<KMAJOR>(Rs, rr, tid);
+    } else {
+      ct_load<KMAJOR>(Ls, L, p.N, m0, k0, tid);
+      ct_load<KMAJOR>(Rs, R, p.N, n0, k0, tid);
+    }
     __syncthreads();
+    if (VEC && k0 + CT_BK < p.N) {
+      ct_fetch<KMAJOR>(rl, L, p.N, m0, k0 + CT_BK, tid);
+      ct_fetch<KMAJOR>(rr, R, p.N, n0, k0 + CT_BK, tid);
+    }
 #pragma unroll
     for (int kk = 0; kk < CT_BK; kk += 32) {
       h8 a[4], b[4];
@@ -666,7 +705,8 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   cp.R = outgoing ? pp.out[1] : pp.out[0];
   {
     LaunchScope ls(ctx, outgoing ? "tri_out.contract" : "tri_in.contract");
-    dim3 grid((N + CT_TILE - 1) / CT_TILE, (N + CT_TILE - 1) / CT_TILE, H);
+    const int tm = (N + CT_TILE - 1) / CT_TILE;
+    dim3 grid((unsigned)(tm * tm * H));
     const bool vec = (N % 8) == 0;
     if (outgoing) {
       if (vec) hipLaunchKernelGGL((tri_contract_kernel<false, true>), grid, dim3(256), 0, ctx->stream, cp);

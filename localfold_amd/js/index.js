@@ -536,6 +536,110 @@ EvoformerStackGpu.prototype.run = function run(input) {
   return runEvoformer(this.device, input, input.blocks);
 };
 
+// ---- AF3 pairformer stack ------------------------------------------------------------
+
+// Block weights in the CPU reference's structure (cpu/af3/trunk/pairformer.js:495-541):
+// triangle projection/gate (in,out) [cZ, 2cZ] interleaved, grid attention q/k/gating (out,in)
+// and v/output (in,out), SwiGLU transitions (in,out), single attention (in,out) with a q bias.
+function pairformerBlockWeights(up, w, cZ, cS) {
+  const tri = function tri(t) {
+    return {
+      lnInScale: up.vec(t.leftNormInputScale), lnInOffset: up.vec(t.leftNormInputOffset),
+      ap: up.weight(t.projection, 'in_out', cZ, 2 * cZ), ag: up.weight(t.gate, 'in_out', cZ, 2 * cZ),
+      lnOutScale: up.vec(t.centerNormScale), lnOutOffset: up.vec(t.centerNormOffset),
+      wz: up.weight(t.outputProjection, 'in_out', cZ, cZ), wg: up.weight(t.gatingLinear, 'in_out', cZ, cZ),
+    };
+  };
+  const grid = function grid(a) {
+    const hd = a.heads * a.dimension;
+    return {
+      normScale: up.vec(a.actNormScale), normOffset: up.vec(a.actNormOffset),
+      wq: up.weight(a.qProjection, 'out_in', hd, cZ), wk: up.weight(a.kProjection, 'out_in', hd, cZ),
+      wv: up.weight(a.vProjection, 'in_out', cZ, hd), wg: up.weight(a.gatingQuery, 'out_in', hd, cZ),
+      wo: up.weight(a.outputProjection, 'in_out', hd, cZ),
+      gBias: up.vec(a.gatingQueryBias), oBias: up.vec(a.outputProjectionBias),
+      wb: up.weight(a.pairBiasProjection, 'in_out', cZ, a.heads),
+    };
+  };
+  const swiglu = function swiglu(t, c) {
+    return {
+      normScale: up.vec(t.inputLayerNormScale), normOffset: up.vec(t.inputLayerNormOffset),
+      w1: up.weight(t.transition1, 'in_out', c, 8 * c), w2: up.weight(t.transition2, 'in_out', 4 * c, c),
+    };
+  };
+  const out = {
+    triOut: tri(w.triangleMultiplicationOutgoing), triIn: tri(w.triangleMultiplicationIncoming),
+    attStart: grid(w.pairAttention1), attEnd: grid(w.pairAttention2), pairHeads: w.pairAttention1.heads,
+    pairTransition: swiglu(w.pairTransition, cZ),
+  };
+  if (w.singleAttention && cS > 0) {
+    const sa = w.singleAttention;
+    const hd = sa.heads * sa.dimension;
+    out.singleLogitsNormScale = up.vec(w.singlePairLogitsNormScale);
+    out.singleLogitsNormOffset = up.vec(w.singlePairLogitsNormOffset);
+    out.singleLogitsProjection = up.weight(w.singlePairLogitsProjection, 'in_out', cZ, sa.heads);
+    out.singleAttention = {
+      normScale: up.vec(sa.layerNormScale), normOffset: up.vec(sa.layerNormOffset),
+      wq: up.weight(sa.qProjection, 'in_out', cS, hd), wk: up.weight(sa.kProjection, 'in_out', cS, hd),
+      wv: up.weight(sa.vProjection, 'in_out', cS, hd), wg: up.weight(sa.gatingQuery, 'in_out', cS, hd),
+      wo: up.weight(sa.outputProjection, 'in_out', hd, cS), qBias: up.vec(sa.qBias),
+      wb: up.weight(w.singlePairLogitsProjection, 'in_out', cZ, sa.heads),
+    };
+    out.singleHeads = sa.heads;
+    out.singleHeadDim = sa.dimension;
+    out.singleTransition = swiglu(w.singleTransition, cS);
+  }
+  return out;
+}
+
+// webgpu/af3/trunk/pairformer-block.js:246-300: run(state, blocks, dialect, options) with
+// state {pair, single, pairMask, seqMask, tokens}; dialect.swapTransposedBias has no default.
+function Af3PairformerStackGpu(device, options) {
+  this.device = device;
+  this.options = options || {};
+}
+Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, options) {
+  const dev = this.device;
+  const opts = options || {};
+  return new Promise(function execute(resolve) {
+    if (!dialect || typeof dialect.swapTransposedBias !== 'boolean') {
+      throw new Error('dialect.swapTransposedBias has no default');
+    }
+    positiveInteger('tokens', state.tokens);
+    const n = state.tokens;
+    const cZ = state.pair.length / (n * n);
+    if (!Number.isInteger(cZ) || cZ <= 0) throw new RangeError('pair has ' + state.pair.length + ' values; not tokens^2 * cZ');
+    const cS = state.single ? state.single.length / n : 0;
+    expectLength('pairMask', state.pairMask, n * n);
+    expectLength('seqMask', state.seqMask, n);
+    if (opts.variance !== undefined && opts.variance !== 'fast') {
+      throw new RangeError('the pairformer runs the reference\'s fast variance; received ' + opts.variance);
+    }
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const pair = up.vec(state.pair);
+    const single = state.single ? up.vec(state.single) : null;
+    const pairMask = up.vec(state.pairMask);
+    const seqMask = up.vec(state.seqMask);
+    for (let b = 0; b < blocks.length; b += 1) {
+      if (opts.onBlock) opts.onBlock(b);
+      const w = resident(dev, blocks[b], function build(wu) { return pairformerBlockWeights(wu, blocks[b], cZ, cS); });
+      dev.addon.pairformerBlock(dev.ctx, {
+        tokens: n, cZ: cZ, cS: cS, swapTransposedBias: dialect.swapTransposedBias ? 1 : 0,
+        divideByLength: dialect.divideByLength ? 1 : 0, pairDtype: ACT.float32, pair: pair,
+        singleDtype: ACT.float32, single: single, pairMask: pairMask, seqMask: seqMask,
+        transitionChunkBytes: opts.transitionChunkBytes || 0, epsilon: opts.epsilon || 1e-5, weights: w,
+      });
+      if (opts.onBlockDone) opts.onBlockDone(b + 1, blocks.length);
+    }
+    const outs = [{ buffer: pair, elements: n * n * cZ }];
+    if (single) outs.push({ buffer: single, elements: n * cS });
+    const r = finish(dev, up, outs, start);
+    resolve({ pair: r.results[0], single: single ? r.results[1] : null, elapsedMilliseconds: r.elapsedMilliseconds,
+      memory: r.memory, kernels: r.kernels });
+  });
+};
+
 // shared/bundles/node.js:11-40: a triangle fixture directory (manifest.json + *.f32.bin)
 const TRIANGLE_WEIGHT_NAMES = [
   'layerNormInWeight', 'layerNormInBias', 'linearAPWeight', 'linearAPBias', 'linearAGWeight', 'linearAGBias',
@@ -578,6 +682,7 @@ module.exports = {
   OuterProductMeanGpu: OuterProductMeanGpu,
   EvoformerBlockGpu: EvoformerBlockGpu,
   EvoformerStackGpu: EvoformerStackGpu,
+  Af3PairformerStackGpu: Af3PairformerStackGpu,
   validateTriangleInput: validateTriangleInput,
   validateAttentionInput: validateAttentionInput,
   validateTransitionInput: validateTransitionInput,

@@ -23,6 +23,18 @@ function report(name, metrics, bounds) {
   console.log((ok ? 'ok   ' : 'FAIL ') + name + ' ' + JSON.stringify(metrics));
 }
 
+// a JSON tree whose {"$f32": file} leaves are Float32Array files (written by the pytest side)
+function revive(node) {
+  if (Array.isArray(node)) return node.map(revive);
+  if (node !== null && typeof node === 'object') {
+    if (typeof node.$f32 === 'string') return f32(node.$f32);
+    const out = {};
+    Object.keys(node).forEach(function each(k) { out[k] = revive(node[k]); });
+    return out;
+  }
+  return node;
+}
+
 function loadWeights(prefix, names) {
   const w = {};
   names.forEach(function each(n) { w[n] = f32(prefix + n + '.f32.bin'); });
@@ -68,6 +80,16 @@ async function main() {
   report('outer product mean', lf.errorMetrics(opOut.output, f32('opm.expected.f32.bin')), { mean: 2e-3, max: 2e-2 });
 
   assert.ok(opOut.memory.peakBytes > 0);
+
+  const ev = revive(JSON.parse(fs.readFileSync(path.join(dir, 'evoformer.json'), 'utf8')));
+  const evOut = await new lf.EvoformerBlockGpu(device).run(ev.input);
+  report('evoformer block msa', lf.errorMetrics(evOut.msa, ev.expectedMsa), { mean: 2e-3, max: 2e-2 });
+  report('evoformer block pair', lf.errorMetrics(evOut.pair, ev.expectedPair), { mean: 2e-3, max: 2e-2 });
+
+  const pf = revive(JSON.parse(fs.readFileSync(path.join(dir, 'pairformer.json'), 'utf8')));
+  const pfOut = await new lf.Af3PairformerStackGpu(device).run(pf.state, pf.blocks, { swapTransposedBias: false });
+  report('pairformer pair', lf.errorMetrics(pfOut.pair, pf.expectedPair), { mean: 2e-3, max: 2e-2 });
+  report('pairformer single', lf.errorMetrics(pfOut.single, pf.expectedSingle), { mean: 2e-3, max: 2e-2 });
   device.destroy();
   process.exitCode = failures === 0 ? 0 : 1;
 }

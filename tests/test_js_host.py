@@ -51,6 +51,22 @@ def _write_fixture_dir(name, out: Path):
     return f
 
 
+def _dump_tree(node, out: Path, prefix: str):
+    """JSON-able copy of a nested weight/input dict with arrays written as float32 files."""
+    if isinstance(node, dict):
+        return {k: _dump_tree(v, out, f"{prefix}.{k}") for k, v in node.items()}
+    if isinstance(node, (list, tuple)):
+        return [_dump_tree(v, out, f"{prefix}.{i}") for i, v in enumerate(node)]
+    if isinstance(node, np.ndarray):
+        np.ascontiguousarray(node, "<f4").tofile(out / f"{prefix}.f32.bin")
+        return {"$f32": f"{prefix}.f32.bin"}
+    if isinstance(node, (np.integer,)):
+        return int(node)
+    if isinstance(node, (np.floating,)):
+        return float(node)
+    return node
+
+
 @pytest.mark.gpu
 def test_js_gpu_suite(tmp_path):
     cases = {"fixtures": H.FIXTURES}
@@ -90,6 +106,34 @@ def test_js_gpu_suite(tmp_path):
     np.asarray(act["msaMask"], "<f4").tofile(tmp_path / "opm.mask.f32.bin")
     np.asarray(ops.outer_product_mean_af2(act["msa"], act["msaMask"], ow), "<f4").tofile(tmp_path / "opm.expected.f32.bin")
     cases["opm"] = {"sequences": 3, "length": 30, "cM": 256, "cOuter": 32, "cZ": 128, "names": list(ow.keys())}
+
+    # EvoformerBlockGpu (the reference test's input fields, test/evoformer-block.gpu.test.js:144-156)
+    from oracle import blocks
+    ew = S.synthetic_block_weights(c_m=256, c_z=128, c_outer=32, heads_msa=8, heads_pair=4, tri_hidden=128,
+                                   msa_hidden=1024, pair_hidden=512, seed=4)
+    ea = S.synthetic_activations(4, 21, 256, 128, seed=6)
+    rm, rp = blocks.evoformer_block_af2(ea["msa"], ea["pair"], ea["msaMask"], ea["pairMask"], ew)
+    ev = {"input": {"msa": ea["msa"], "pair": ea["pair"], "msaMask": ea["msaMask"], "pairMask": ea["pairMask"],
+                    "sequences": 4, "length": 21, "cM": 256, "cZ": 128, "cOuter": 32, "triangleHidden": 128,
+                    "weights": ew},
+          "expectedMsa": rm, "expectedPair": rp}
+    (tmp_path / "evoformer.json").write_text(json.dumps(_dump_tree(ev, tmp_path, "evo")))
+
+    # Af3PairformerStackGpu: two blocks
+    n, cz, cs = 24, 128, 384
+    pws = [S.synthetic_pairformer_weights(cz, cs, 4, 16, 24, seed=s_) for s_ in (21, 22)]
+    st = S.Stream(23)
+    pair0 = st.normal(n * n * cz).reshape(n, n, cz)
+    single0 = st.normal(n * cs).reshape(n, cs)
+    seq_mask = np.ones(n, np.float32)
+    seq_mask[-3:] = 0
+    pair_mask = np.outer(seq_mask, seq_mask).astype(np.float32)
+    rp, rs = pair0, single0
+    for pw in pws:
+        rp, rs = blocks.pairformer_block_af3(rp, rs, pair_mask, seq_mask, pw, False, False)
+    pf = {"state": {"pair": pair0, "single": single0, "pairMask": pair_mask, "seqMask": seq_mask, "tokens": n},
+          "blocks": pws, "expectedPair": rp, "expectedSingle": rs}
+    (tmp_path / "pairformer.json").write_text(json.dumps(_dump_tree(pf, tmp_path, "pf")))
 
     (tmp_path / "cases.json").write_text(json.dumps(cases))
     r = _run_node("gpu.test.js", tmp_path)
