@@ -302,26 +302,13 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
 
   const size_t qkv = (size_t)B * H * Q * FA_DP * sizeof(_Float16);
   const size_t hd = (size_t)rows * HD * sizeof(_Float16);
-  const size_t biasb = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Q * sizeof(float);
   const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Q * sizeof(_Float16);
-  size_t sizes[13] = {qkv, qkv, qkv, hd, hd, (size_t)rows * sizeof(float), biasb, biash};
-  for (int i = 0; i < nv; ++i) sizes[8 + i] = expanded_bytes(views[i]);
-  void* bufs[14];
-  LF_TRY(workspace(ctx, sizes, bufs, 8 + nv));
-  _Float16 *qb = (_Float16*)bufs[0], *kb = (_Float16*)bufs[1], *vb = (_Float16*)bufs[2];
-  _Float16 *gb = (_Float16*)bufs[3], *ob = (_Float16*)bufs[4];
-  float* keyb = (float*)bufs[5];
-  float* bias32 = (float*)bufs[6];
-  _Float16* bias16 = (_Float16*)bufs[7];
-  WExp ex[6];
-  LF_TRY(expand_weights(ctx, views, nv, bufs + 8, ex, "attention.expand"));
-  if (d < FA_DP) {
-    for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
-  }
+  // buffers: q, k, v, g, o, key bias, f16 pair bias, output weights, packed lnproj weights x 2
+  void* bufs[9];
 
   // 1. pair bias from a separate pair tensor: bias[h][i][j] = LN(pair_ij) . W[:, h]
+  LnProjParams pb{};
   if (a.bias_mode == LF_BIAS_SEPARATE) {
-    LnProjParams pb{};
     pb.x = a.pair;
     pb.rows = Q * Q;
     pb.C = a.pair_channels;
@@ -333,45 +320,60 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     pb.fast_var = a.fast_variance;
     pb.ngroups = 1;
     Group& g = pb.g[0];
-    g.w0 = ex[5];
+    g.w0 = views[5];
     g.ncols = H;
     g.op = OP_STORE;
     g.scale = 1.f;
-    // [h][i][j] from row (i, j); swapped: [h][j][i]
-    g.dst = a.swap_bias ? Dst{bias32, DT_F32, Q, 1, Q, 1, (long long)Q * Q, 0}
-                        : Dst{bias32, DT_F32, Q * Q, 0, 1, 1, (long long)Q * Q, 0};
-    LF_TRY(launch_lnproj(ctx, pb, a.pair_dtype, "attention.pair_bias"));
+  }
+  // 2. LN + q/k/v/g (+ bias from the normalised input)
+  LnProjParams pp{};
+  pp.x = a.act;
+  pp.rows = (int)rows;
+  pp.C = C;
+  pp.rmQ = Q;
+  pp.rmB = a.transpose ? B : 0;
+  pp.ln_s = w.norm_scale;
+  pp.ln_o = w.norm_offset;
+  pp.eps = a.epsilon;
+  pp.fast_var = a.fast_variance;
+  pp.g[0] = Group{views[0], WView{}, HD, OP_STORE, 1.0f / std::sqrt((float)d), w.q_bias, nullptr, Dst{}};
+  pp.g[1] = Group{views[1], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  pp.g[2] = Group{views[2], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  pp.g[3] = Group{views[3], WView{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, Dst{}};
+  pp.ngroups = 4;
+  if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) {
+    pp.g[4] = Group{views[5], WView{}, H, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+    pp.ngroups = 5;
   }
 
-  // 2. LN + q/k/v/g (+ bias from the normalised input)
+  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)rows * sizeof(float), biash, expanded_bytes(views[4]),
+                     std::max(lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb)
+                                                                                       : (size_t)0)};
+  LF_TRY(workspace(ctx, sizes, bufs, 9));
+  _Float16 *qb = (_Float16*)bufs[0], *kb = (_Float16*)bufs[1], *vb = (_Float16*)bufs[2];
+  _Float16 *gb = (_Float16*)bufs[3], *ob = (_Float16*)bufs[4];
+  float* keyb = (float*)bufs[5];
+  _Float16* bias16 = (_Float16*)bufs[6];
+  WExp wo;
+  LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[7], &wo, "attention.expand"));
+  if (d < FA_DP) {
+    for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
+  }
+  // f16 bias [h][i][j] from row (i, j); swapped: [h][j][i]
+  const Dst bias_dst = a.swap_bias ? Dst{bias16, DT_F16, Q, 1, Q, 1, (long long)Q * Q, 0}
+                                   : Dst{bias16, DT_F16, Q * Q, 0, 1, 1, (long long)Q * Q, 0};
+  if (a.bias_mode == LF_BIAS_SEPARATE) {
+    pb.g[0].dst = bias_dst;
+    LF_TRY(launch_lnproj(ctx, pb, a.pair_dtype, bufs[8], "attention.pair_bias"));
+  }
   {
-    LnProjParams pp{};
-    pp.x = a.act;
-    pp.rows = (int)rows;
-    pp.C = C;
-    pp.rmQ = Q;
-    pp.rmB = a.transpose ? B : 0;
-    pp.ln_s = w.norm_scale;
-    pp.ln_o = w.norm_offset;
-    pp.eps = a.epsilon;
-    pp.fast_var = a.fast_variance;
     const long long hq = (long long)Q * FA_DP;
-    Dst qd{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    Dst kd{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    Dst vd{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Q};
-    Dst gd = dst_rowmajor(gb, DT_F16, (int)rows, HD);
-    pp.g[0] = Group{ex[0], WExp{}, HD, OP_STORE, 1.0f / std::sqrt((float)d), w.q_bias, nullptr, qd};
-    pp.g[1] = Group{ex[1], WExp{}, HD, OP_STORE, 1.f, nullptr, nullptr, kd};
-    pp.g[2] = Group{ex[2], WExp{}, HD, OP_STORE, 1.f, nullptr, nullptr, vd};
-    pp.g[3] = Group{ex[3], WExp{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, gd};
-    pp.ngroups = 4;
-    if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) {
-      Dst bd = a.swap_bias ? Dst{bias32, DT_F32, Q, 1, Q, 1, (long long)Q * Q, 0}
-                           : Dst{bias32, DT_F32, (int)rows, 0, 1, 1, rows, 0};
-      pp.g[4] = Group{ex[5], WExp{}, H, OP_STORE, 1.f, nullptr, nullptr, bd};
-      pp.ngroups = 5;
-    }
-    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, "attention.project"));
+    pp.g[0].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    pp.g[1].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    pp.g[2].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Q};
+    pp.g[3].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
+    if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) pp.g[4].dst = bias_dst;
+    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
   }
 
   // 3. key-mask bias, f16 copy of the pair bias
@@ -381,8 +383,10 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
                        B, Q, a.transpose);
   }
   LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
-  const float* bsrc = a.bias_mode == LF_BIAS_LOGITS ? a.bias_logits : bias32;
-  if (a.bias_mode != LF_BIAS_NONE) LF_TRY(f32_to_f16(ctx, bsrc, bias16, (long long)H * Q * Q, a.bias_mode == LF_BIAS_LOGITS && a.swap_bias ? Q : 0));
+  // caller-supplied f32 logits are converted (and transposed per head when swapped); the
+  // projected biases were written as f16 by lnproj
+  if (a.bias_mode == LF_BIAS_LOGITS)
+    LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0));
 
   // 4. flash attention
   {
@@ -413,7 +417,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     rp.rows = (int)rows;
     rp.K = HD;
     rp.N = C;
-    rp.w = ex[4];
+    rp.w = wo;
     rp.bias = w.o_bias;
     rp.op = OP_STORE;
     rp.resid = a.accumulate ? a.act : nullptr;

@@ -299,7 +299,7 @@ struct FragTile {
 };
 
 // Lane loads its row (storage row `srow`, already clamped to a valid row) at channels
-// 32j + 8*(lane/16) + e; channels >= C come from a clamped address (discarded later).
+// 32j + 8*(lane/16) + e; channels >= C read as zero.
 template <int ACT, int KS>
 __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* src, size_t srow, int C, int lane) {
   typedef typename FragTile<ACT, KS>::T T;
@@ -319,7 +319,8 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const int c = 32 * j + 8 * g + k;
-          w[k] = __float_as_uint(s[c < C ? c : 0]);
+          const uint32_t bits = __float_as_uint(s[c < C ? c : 0]);
+          w[k] = c < C ? bits : 0u;
         }
         t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
         t.raw[j][1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -327,8 +328,8 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int c0 = 32 * j + 8 * g + 2 * k;
-          const uint16_t lo = __builtin_bit_cast(uint16_t, s[c0 < C ? c0 : 0]);
-          const uint16_t hi = __builtin_bit_cast(uint16_t, s[c0 + 1 < C ? c0 + 1 : 0]);
+          const uint16_t lo = c0 < C ? __builtin_bit_cast(uint16_t, s[c0 < C ? c0 : 0]) : (uint16_t)0;
+          const uint16_t hi = c0 + 1 < C ? __builtin_bit_cast(uint16_t, s[c0 + 1 < C ? c0 + 1 : 0]) : (uint16_t)0;
           w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
         t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
@@ -418,6 +419,84 @@ __device__ __forceinline__ void frag_ln(const float (&x)[KS][8], h8 (&a)[KS], bo
       const bool valid = ok && (32 * j + 8 * g + e < C);
       a[j][e] = (_Float16)(valid ? (x[j][e] - mean) * inv * gg[e] + bb[e] : 0.f);
     }
+  }
+}
+
+// Keeps the compiler from carrying values decoded from a raw tile from one pass to the
+// next (the packed words stay live; the decoded floats would cost 8x the registers).
+template <int ACT, int KS>
+__device__ __forceinline__ void launder(FragTile<ACT, KS>& t) {
+#pragma unroll
+  for (int j = 0; j < KS; ++j)
+#pragma unroll
+    for (int v = 0; v < FragTile<ACT, KS>::NV; ++v)
+      asm volatile("" : "+v"(t.raw[j][v].x), "+v"(t.raw[j][v].y), "+v"(t.raw[j][v].z), "+v"(t.raw[j][v].w));
+}
+
+// Row statistics of a raw tile whose channels >= C hold zeros (frag_load_row): values are
+// decoded on the fly, one k-step at a time, so only the packed words stay live.  The padding
+// channels add (32*KS - C) * mean^2 to the centred sum, which is subtracted.
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_stats_raw(FragTile<ACT, KS>& t, int C, float eps, bool fast_var, float& mean,
+                                               float& inv) {
+  float s = 0.f, q = 0.f;
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = t.get(j, e);
+      s += v;
+      q += v * v;
+    }
+    __builtin_amdgcn_sched_barrier(0);   // decode one k-step at a time
+  }
+  const float invC = 1.0f / (float)C;
+  mean = lanes4_sum(s) * invC;
+  if (fast_var) {
+    q = lanes4_sum(q) * invC - mean * mean;
+  } else {
+    launder(t);
+    q = 0.f;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = t.get(j, e) - mean;
+        q += d * d;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    q = (lanes4_sum(q) - (float)(32 * KS - C) * mean * mean) * invC;
+  }
+  inv = rsqrt_(q + eps);
+  launder(t);
+}
+
+// LayerNorm of two raw tiles into MFMA fragments, gamma/beta read once per k-step for both.
+// Padding channels normalise to finite values that meet zero weight rows; rows past the end
+// are normalised too (their outputs are never stored).
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_ln_raw2(FragTile<ACT, KS>& t0, FragTile<ACT, KS>& t1, h8 (&a0)[KS],
+                                             h8 (&a1)[KS], int C, const float* gamma, const float* beta,
+                                             float eps, bool fast_var, int lane) {
+  const int g = lane >> 4;
+  float m0, i0, m1, i1;
+  frag_stats_raw(t0, C, eps, fast_var, m0, i0);
+  frag_stats_raw(t1, C, eps, fast_var, m1, i1);
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+    const float4 g0 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g);
+    const float4 g1 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g);
+    const float4 b1 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g + 4);
+    const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a0[j][e] = (_Float16)((t0.get(j, e) - m0) * i0 * gg[e] + bb[e]);
+      a1[j][e] = (_Float16)((t1.get(j, e) - m1) * i1 * gg[e] + bb[e]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 

@@ -12,11 +12,12 @@ __global__ __launch_bounds__(256) void expand_weights_kernel(ExpandBatch b) {
   const int m = blockIdx.y;
   if (m >= b.count) return;
   const WView& v = b.v[m];
-  const int kp = b.kp[m];
-  const long total = (long)v.N * kp;
+  const int kp = b.kp[m], W = b.W[m], off = b.off[m];
+  const long total = (long)b.ncols[m] * kp;
   for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
     const int n = (int)(e / kp), k = (int)(e - (long)n * kp);
-    b.dst[m][e] = (_Float16)wdecode(v, k, n);
+    const long row = (long)(n / W) * 64 + off + n % W;
+    b.dst[m][row * kp + k] = (_Float16)wdecode(v, k, n);
   }
 }
 
@@ -30,6 +31,9 @@ int expand_weights(lf_context* ctx, const WView* views, int count, void* const* 
       b.v[i] = v;
       b.kp[i] = (v.K + 31) & ~31;
       b.dst[i] = static_cast<_Float16*>(dst[base + i]);
+      b.W[i] = std::max(v.N, 1);
+      b.off[i] = 0;
+      b.ncols[i] = v.N;
       out[base + i] = WExp{b.dst[i], b.kp[i], v.N};
       most = std::max(most, (long)v.N * b.kp[i]);
     }
@@ -37,6 +41,30 @@ int expand_weights(lf_context* ctx, const WView* views, int count, void* const* 
     dim3 grid((unsigned)std::min<long>((most + 255) / 256, 1024), b.count);
     hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
     LF_TRY(check_hip(hipGetLastError(), "expand_weights launch"));
+  }
+  return LF_OK;
+}
+
+int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
+                  int count, _Float16* dst, int kp, const char* label) {
+  for (int base = 0; base < count; base += 8) {
+    ExpandBatch b{};
+    b.count = std::min(8, count - base);
+    long most = 0;
+    for (int i = 0; i < b.count; ++i) {
+      const int m = base + i;
+      b.v[i] = views[m];
+      b.kp[i] = kp;
+      b.dst[i] = dst + row0[m] * kp;
+      b.W[i] = W[m];
+      b.off[i] = off[m];
+      b.ncols[i] = (views[m].N + W[m] - 1) / W[m] * W[m];
+      most = std::max(most, (long)b.ncols[i] * kp);
+    }
+    LaunchScope ls(ctx, label);
+    dim3 grid((unsigned)std::min<long>((most + 255) / 256, 1024), b.count);
+    hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
+    LF_TRY(check_hip(hipGetLastError(), "expand_packed launch"));
   }
   return LF_OK;
 }

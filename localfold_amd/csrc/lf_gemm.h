@@ -21,10 +21,14 @@ struct WExp {
   int N;    // valid columns
 };
 
+// Up to 8 matrices decoded per launch.  Matrix m's column n lands in destination row
+// (n / W) * 64 + off + n % W with row pitch `kp` (plain expansion: W = N, off = 0); `ncols`
+// columns are written, those >= N as zeros.
 struct ExpandBatch {
   WView v[8];
   _Float16* dst[8];
   int kp[8];
+  int W[8], off[8], ncols[8];
   int count;
 };
 

@@ -116,37 +116,35 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   LF_TRY(make_view(w.wl, a.c_m, co, "leftWeight", &views[0]));
   LF_TRY(make_view(w.wr, a.c_m, co, "rightWeight", &views[1]));
   LF_TRY(make_view(w.wo, co * co, cz, "outputWeight", &views[2]));
+  // l, r = mask * (LN(msa) W + b), stored [i][a][s]
+  LnProjParams pp{};
+  pp.x = a.msa;
+  pp.rows = (int)rows;
+  pp.C = a.c_m;
+  pp.rmQ = 1;
+  pp.rmB = 0;
+  pp.ln_s = w.norm_scale;
+  pp.ln_o = w.norm_offset;
+  pp.eps = a.epsilon;
+  pp.fast_var = a.fast_variance;
+  pp.rowmask = a.mask;
+  pp.g[0] = Group{views[0], WView{}, co, OP_ROWMASK, 1.f, w.bl, nullptr, Dst{}};
+  pp.g[1] = Group{views[1], WView{}, co, OP_ROWMASK, 1.f, w.br, nullptr, Dst{}};
+  pp.ngroups = 2;
+
   const size_t lr = (size_t)N * co * S * sizeof(_Float16);
   const size_t ob = (size_t)pairs * co * co * sizeof(_Float16);
-  size_t sizes[7] = {lr, lr, ob, (size_t)pairs * sizeof(float)};
-  for (int i = 0; i < 3; ++i) sizes[4 + i] = expanded_bytes(views[i]);
-  void* bufs[7];
-  LF_TRY(workspace(ctx, sizes, bufs, 7));
+  size_t sizes[6] = {lr, lr, ob, (size_t)pairs * sizeof(float), expanded_bytes(views[2]), lnproj_packed_bytes(pp)};
+  void* bufs[6];
+  LF_TRY(workspace(ctx, sizes, bufs, 6));
   _Float16 *L = (_Float16*)bufs[0], *R = (_Float16*)bufs[1], *O = (_Float16*)bufs[2];
   float* den = (float*)bufs[3];
-  WExp ex[3];
-  LF_TRY(expand_weights(ctx, views, 3, bufs + 4, ex, "opm.expand"));
-
-  {  // l, r = mask * (LN(msa) W + b), stored [i][a][s]
-    LnProjParams pp{};
-    pp.x = a.msa;
-    pp.rows = (int)rows;
-    pp.C = a.c_m;
-    pp.rmQ = 1;
-    pp.rmB = 0;
-    pp.ln_s = w.norm_scale;
-    pp.ln_o = w.norm_offset;
-    pp.eps = a.epsilon;
-    pp.fast_var = a.fast_variance;
-    pp.rowmask = a.mask;
-    // logical row r = s*N + i -> (i*co + a)*S + s
-    Dst ld{L, DT_F16, N, 1, (long long)co * S, co, 0, S};
-    Dst rd{R, DT_F16, N, 1, (long long)co * S, co, 0, S};
-    pp.g[0] = Group{ex[0], WExp{}, co, OP_ROWMASK, 1.f, w.bl, nullptr, ld};
-    pp.g[1] = Group{ex[1], WExp{}, co, OP_ROWMASK, 1.f, w.br, nullptr, rd};
-    pp.ngroups = 2;
-    LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, "opm.project"));
-  }
+  WExp wo;
+  LF_TRY(expand_weights(ctx, &views[2], 1, &bufs[4], &wo, "opm.expand"));
+  // logical row r = s*N + i -> (i*co + a)*S + s
+  pp.g[0].dst = Dst{L, DT_F16, N, 1, (long long)co * S, co, 0, S};
+  pp.g[1].dst = Dst{R, DT_F16, N, 1, (long long)co * S, co, 0, S};
+  LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, bufs[5], "opm.project"));
   {
     LaunchScope ls(ctx, "opm.count");
     hipLaunchKernelGGL(opm_count_kernel, dim3((N + 255) / 256, N), dim3(256), 0, ctx->stream, a.mask, den, S, N,
@@ -175,7 +173,7 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
     rp.rows = (int)pairs;
     rp.K = co * co;
     rp.N = cz;
-    rp.w = ex[2];
+    rp.w = wo;
     rp.bias = w.bo;
     rp.op = OP_STORE;
     rp.rowden = den;

@@ -21,6 +21,10 @@ int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, in
 // Decodes `count` weight views into f16 E[n][k] tiles at dst[i] (expanded_bytes(views[i]) each).
 int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label);
 size_t expanded_bytes(const WView& v);
+// Decodes views[m] into the chunk layout of a packed buffer: column n -> row
+// row0[m] + (n / W[m]) * 64 + off[m] + n % W[m], pitch kp, padding columns zeroed.
+int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
+                  int count, _Float16* dst, int kp, const char* label);
 // dst = (f16) src over n elements; tq > 0 transposes every [tq][tq] plane.
 int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq);
 

@@ -28,10 +28,12 @@ struct Dst {
 
 enum GroupOp { OP_STORE = 0, OP_SIGMOID = 1, OP_RELU = 2, OP_SWIGLU = 3, OP_ROWMASK = 4 };
 
-// One output group of an lnproj launch.  Paired ops (OP_SWIGLU) read 32 columns of w0 (gate)
-// and the same 32 columns of w1 (value) per chunk; the others read 64 columns of w0.
+// One output group of an lnproj launch.  Paired ops (OP_SWIGLU) take 32 columns of w0 (gate)
+// and the same 32 columns of w1 (value) per 64-row weight chunk; the others 64 columns of w0.
+// The launcher decodes every group's weights into one packed [chunk][64][KP] f16 buffer in
+// the order the kernel consumes them.
 struct Group {
-  WExp w0, w1;
+  WView w0, w1;
   int ncols;          // logical output columns of the group
   int op;
   float scale;        // multiplies the (biased) GEMM result before the op
@@ -52,6 +54,7 @@ struct LnProjParams {
   const float* rowmask;   // OP_ROWMASK multiplier, indexed by storage row
   Group g[MAX_GROUPS];
   int ngroups;
+  const _Float16* wpk;    // packed weights (set by launch_lnproj)
 };
 
 struct RowGemmParams {
@@ -65,8 +68,11 @@ struct RowGemmParams {
   Dst dst;
 };
 
-// Host launchers (defined in lf_rowgemm.hip).  `act` is the dtype of x.
-int launch_lnproj(lf_context* ctx, const LnProjParams& p, int act, const char* label);
+// Host launchers (defined in lf_rowgemm.hip).  `act` is the dtype of x.  `packed` is
+// workspace of lnproj_packed_bytes(p) bytes for the decoded weights; repeated launches with
+// the same weights (row chunks) pass decode = false after the first.
+size_t lnproj_packed_bytes(const LnProjParams& p);
+int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode = true);
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label);
 
 inline Dst dst_rowmajor(void* ptr, int dtype, int rows, int cols) {

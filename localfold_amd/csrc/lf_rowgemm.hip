@@ -44,26 +44,15 @@ __device__ __forceinline__ void chunk_of(const LnProjParams& p, int ci, int& gi,
   }
 }
 
-// Loads chunk ci's weights ([64][KP] f16: 64 columns of w0, or 32 of w0 then 32 of w1) into
-// registers (`regs`, NREG 16-byte words per thread), to be stored into LDS later.
+// Loads chunk ci of the packed weights (a contiguous [64][KP] f16 block) into registers
+// (NREG 16-byte words per thread), to be stored into LDS later.
 template <int KP, int NREG>
 __device__ __forceinline__ void chunk_load(const LnProjParams& p, int ci, uint4 (&regs)[NREG], int tid) {
-  int gi, c0;
-  chunk_of(p, ci, gi, c0);
-  const Group& G = p.g[gi];
-  const bool paired = G.op == OP_SWIGLU;
-  constexpr int SEGS = KP / 8;
+  const uint4* src = reinterpret_cast<const uint4*>(p.wpk + (size_t)ci * 64 * KP);
 #pragma unroll
   for (int r = 0; r < NREG; ++r) {
     const int i = tid + r * 512;
-    const int n = i / SEGS, seg = i - n * SEGS;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (n < 64) {
-      const WExp& w = (paired && n >= 32) ? G.w1 : G.w0;
-      const int col = paired ? c0 + (n & 31) : c0 + n;
-      if (col < w.N && seg * 8 < w.kp) v = *reinterpret_cast<const uint4*>(w.p + (size_t)col * w.kp + seg * 8);
-    }
-    regs[r] = v;
+    regs[r] = i < 64 * KP / 8 ? src[i] : make_uint4(0, 0, 0, 0);
   }
 }
 
@@ -75,6 +64,43 @@ __device__ __forceinline__ void chunk_store(_Float16* Ws, const uint4 (&regs)[NR
     const int i = tid + r * 512;
     const int n = i / SEGS, seg = i - n * SEGS;
     if (n < 64) *reinterpret_cast<uint4*>(Ws + n * LDW + seg * 8) = regs[r];
+  }
+}
+
+// lnproj: 8 waves x 32 rows (two 16-row tiles) = 256 rows per block.  The LayerNorm'd rows
+// stay in registers as MFMA B fragments for the whole launch; the weights stream through
+// double-buffered LDS in 64-column chunks, and every weight fragment read from LDS feeds two
+// MFMAs (one per row tile).  The weights are the A operand, so a lane ends up holding four
+// consecutive output columns of one row: stores are 8-byte vectors wherever the destination
+// keeps those columns contiguous.  Destinations are f16 with 32-bit element offsets.
+constexpr int LP_ROWS = RG_WAVES * 32;
+
+__device__ __forceinline__ int dst_row32(const Dst& d, int row) {
+  const unsigned q = (unsigned)d.Q;
+  const unsigned b = (unsigned)row / q, n = (unsigned)row - b * q;
+  return (int)b * (int)d.sB + (int)n * (int)d.sN;
+}
+__device__ __forceinline__ int dst_col32(const Dst& d, int col) {
+  const unsigned dd = (unsigned)d.D;
+  const unsigned h = (unsigned)col / dd, e = (unsigned)col - h * dd;
+  return (int)h * (int)d.sH + (int)e * (int)d.sD;
+}
+
+// Four consecutive columns cb..cb+3 of one row: one 8-byte store when they are contiguous in
+// the destination, else element stores (columns >= ncols are dropped).
+__device__ __forceinline__ void store_cols4(const Group& G, int rowpart, int cb, const float (&v)[4]) {
+  _Float16* out = static_cast<_Float16*>(G.dst.ptr);
+  const unsigned dd = (unsigned)G.dst.D;
+  const unsigned e0 = (unsigned)cb % dd;
+  if (G.dst.sD == 1 && cb + 3 < G.ncols && e0 + 3 < dd && ((rowpart + dst_col32(G.dst, cb)) & 3) == 0) {
+    h4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (_Float16)v[i];
+    *reinterpret_cast<h4*>(out + rowpart + dst_col32(G.dst, cb)) = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (cb + i < G.ncols) out[rowpart + dst_col32(G.dst, cb + i)] = (_Float16)v[i];
   }
 }
 
@@ -97,80 +123,91 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
   uint4 regs[NREG];
   chunk_load<KP, NREG>(p, 0, regs, tid);
 
-  // this wave's 16 logical rows, LayerNorm'd into A fragments
-  const int row0 = blockIdx.x * RG_ROWS + wave * 16;
-  const int myrow = row0 + r16;
-  const bool rvalid = myrow < p.rows;
-  const int lrow = rvalid ? myrow : 0;
-  const int srow = p.rmB > 0 ? (lrow % p.rmQ) * p.rmB + lrow / p.rmQ : lrow;
-  h8 a[KS];
+  // this wave's two 16-row tiles, LayerNorm'd into B fragments
+  const int rbase = blockIdx.x * LP_ROWS + wave * 32;
+  h8 xb[2][KS];
+  int srow[2];
+  bool rvalid[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int myrow = rbase + tt * 16 + r16;
+    rvalid[tt] = myrow < p.rows;
+    const int lrow = rvalid[tt] ? myrow : 0;
+    srow[tt] = p.rmB > 0 ? (lrow % p.rmQ) * p.rmB + lrow / p.rmQ : lrow;
+  }
   {
-    FragTile<ACT, KS> t;
-    frag_load_row(t, p.x, (size_t)srow, p.C, lane);
-    float x[KS][8];
-    frag_values(t, x, p.C, lane);
+    FragTile<ACT, KS> t0, t1;
+    frag_load_row(t0, p.x, (size_t)srow[0], p.C, lane);
+    frag_load_row(t1, p.x, (size_t)srow[1], p.C, lane);
     chunk_store<KP, NREG>(Ws[0], regs, tid);
     __syncthreads();  // Gs and chunk 0 staged
-    frag_ln<KS>(x, a, rvalid, p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
+    frag_ln_raw2(t0, t1, xb[0], xb[1], p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
   }
-  // storage rows of the 4 output rows this lane holds (for OP_ROWMASK)
-  int orow[4];
+  float rm[2] = {1.f, 1.f};
+  if (p.rowmask) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) orow[i] = row0 + g4 * 4 + i;
+    for (int tt = 0; tt < 2; ++tt) rm[tt] = p.rowmask[srow[tt]];
+  }
 
   for (int ci = 0; ci < nchunks; ++ci) {
     const _Float16* W = Ws[ci & 1];
     if (ci + 1 < nchunks) chunk_load<KP, NREG>(p, ci + 1, regs, tid);
-    f4 acc[4];
+    f4 acc[2][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[tt][t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
+      h8 w[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc[t] = mfma16(a[j], *reinterpret_cast<const h8*>(W + (t * 16 + r16) * LDW + 32 * j + kq), acc[t]);
+      for (int t = 0; t < 4; ++t) w[t] = *reinterpret_cast<const h8*>(W + (t * 16 + r16) * LDW + 32 * j + kq);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[0][t] = mfma16(w[t], xb[0][j], acc[0][t]);
+        acc[1][t] = mfma16(w[t], xb[1][j], acc[1][t]);
+      }
+      __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
     }
     int gi, c0;
     chunk_of(p, ci, gi, c0);
     const Group& G = p.g[gi];
-    long long rp[4];
-    float rm[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int lr = orow[i] < p.rows ? orow[i] : 0;
-      rp[i] = dst_rowpart(G.dst, lr);
-      rm[i] = 1.f;
-      if (G.op == OP_ROWMASK) rm[i] = p.rowmask[p.rmB > 0 ? (lr % p.rmQ) * p.rmB + lr / p.rmQ : lr];
-    }
-    if (G.op == OP_SWIGLU) {
+    for (int tt = 0; tt < 2; ++tt) {
+      if (!rvalid[tt]) continue;
+      const int rowpart = dst_row32(G.dst, rbase + tt * 16 + r16);
+      if (G.op == OP_SWIGLU) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int col = c0 + t * 16 + r16;
-        if (col >= G.ncols) continue;
-        const float b0 = G.bias0 ? G.bias0[col] : 0.f, b1 = G.bias1 ? G.bias1[col] : 0.f;
-        const long long cp = dst_colpart(G.dst, col);
+        for (int t = 0; t < 2; ++t) {
+          const int cb = c0 + t * 16 + 4 * g4;
+          float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (orow[i] >= p.rows) continue;
-          const float gt = (acc[t][i] + b0) * G.scale, vl = (acc[t + 2][i] + b1) * G.scale;
-          dst_store(G.dst, rp[i] + cp, gt * sigmoidf_(gt) * vl);
+          for (int i = 0; i < 4; ++i) {
+            const int c = cb + i < G.ncols ? cb + i : 0;
+            const float gt = (acc[tt][t][i] + (G.bias0 ? G.bias0[c] : 0.f)) * G.scale;
+            const float vl = (acc[tt][t + 2][i] + (G.bias1 ? G.bias1[c] : 0.f)) * G.scale;
+            v[i] = gt * sigmoidf_(gt) * vl;
+          }
+          if (cb < G.ncols) store_cols4(G, rowpart, cb, v);
+          __builtin_amdgcn_sched_barrier(0);
         }
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int col = c0 + t * 16 + r16;
-        if (col >= G.ncols) continue;
-        const float b0 = G.bias0 ? G.bias0[col] : 0.f;
-        const long long cp = dst_colpart(G.dst, col);
+        for (int t = 0; t < 4; ++t) {
+          const int cb = c0 + t * 16 + 4 * g4;
+          if (cb >= G.ncols) continue;
+          float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (orow[i] >= p.rows) continue;
-          float v = (acc[t][i] + b0) * G.scale;
-          if (G.op == OP_SIGMOID) v = sigmoidf_(v);
-          else if (G.op == OP_RELU) v = fmaxf(v, 0.f);
-          v *= rm[i];
-          dst_store(G.dst, rp[i] + cp, v);
+          for (int i = 0; i < 4; ++i) {
+            const int c = cb + i < G.ncols ? cb + i : 0;
+            float y = (acc[tt][t][i] + (G.bias0 ? G.bias0[c] : 0.f)) * G.scale;
+            if (G.op == OP_SIGMOID) y = sigmoidf_(y);
+            else if (G.op == OP_RELU) y = fmaxf(y, 0.f);
+            else if (G.op == OP_ROWMASK) y *= rm[tt];
+            v[i] = y;
+          }
+          store_cols4(G, rowpart, cb, v);
+          __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
         }
       }
     }
@@ -181,11 +218,62 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
   }
 }
 
-int launch_lnproj(lf_context* ctx, const LnProjParams& p, int act, const char* label) {
+static int lnproj_ks(int C) { return C <= 32 ? 1 : C <= 64 ? 2 : C <= 128 ? 4 : C <= 256 ? 8 : 12; }
+
+static int lnproj_chunks(const LnProjParams& p) {
+  int n = 0;
+  for (int g = 0; g < p.ngroups; ++g) {
+    const int w = p.g[g].op == OP_SWIGLU ? 32 : 64;
+    n += (p.g[g].ncols + w - 1) / w;
+  }
+  return n;
+}
+
+size_t lnproj_packed_bytes(const LnProjParams& p) {
+  return (size_t)lnproj_chunks(p) * 64 * 32 * lnproj_ks(p.C) * sizeof(_Float16);
+}
+
+int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode) {
   if (p.C > 384) return set_error(LF_ERR_INVALID, std::string(label) + ": LayerNorm width above 384");
   if (p.rows <= 0) return LF_OK;
-  const int ks = p.C <= 32 ? 1 : p.C <= 64 ? 2 : p.C <= 128 ? 4 : p.C <= 256 ? 8 : 12;
-  dim3 grid((p.rows + RG_ROWS - 1) / RG_ROWS);
+  if (!packed) return set_error(LF_ERR_INVALID, std::string(label) + ": no packed-weight workspace");
+  for (int g = 0; g < p.ngroups; ++g) {
+    const Dst& d = p.g[g].dst;
+    if (d.dtype != DT_F16) return set_error(LF_ERR_INVALID, std::string(label) + ": lnproj writes f16 only");
+    const long long span = (long long)((p.rows - 1) / d.Q) * d.sB + (long long)std::min(p.rows - 1, d.Q - 1) * d.sN +
+                           (long long)((p.g[g].ncols - 1) / d.D) * d.sH +
+                           (long long)std::min(p.g[g].ncols - 1, d.D - 1) * d.sD;
+    if (span >= (1LL << 31)) return set_error(LF_ERR_INVALID, std::string(label) + ": destination above 2^31 elements");
+  }
+  // decode every group's weights into chunk order
+  const int KP = 32 * lnproj_ks(p.C);
+  WView views[2 * MAX_GROUPS];
+  int W[2 * MAX_GROUPS], off[2 * MAX_GROUPS];
+  long long row0[2 * MAX_GROUPS];
+  int nv = 0;
+  long long rows_done = 0;
+  for (int g = 0; g < p.ngroups; ++g) {
+    const Group& G = p.g[g];
+    const bool paired = G.op == OP_SWIGLU;
+    const int w = paired ? 32 : 64;
+    views[nv] = G.w0;
+    W[nv] = w;
+    off[nv] = 0;
+    row0[nv++] = rows_done;
+    if (paired) {
+      views[nv] = G.w1;
+      W[nv] = 32;
+      off[nv] = 32;
+      row0[nv++] = rows_done;
+    }
+    rows_done += (long long)(G.ncols + w - 1) / w * 64;
+  }
+  p.wpk = static_cast<const _Float16*>(packed);
+  if (decode)
+    LF_TRY(expand_packed(ctx, views, W, off, row0, nv, static_cast<_Float16*>(packed), KP,
+                       (std::string(label) + ".expand").c_str()));
+  const int ks = lnproj_ks(p.C);
+  dim3 grid((p.rows + LP_ROWS - 1) / LP_ROWS);
   LaunchScope ls(ctx, label);
 #define LF_LP(A, K) hipLaunchKernelGGL((lnproj_kernel<A, K>), grid, dim3(512), 0, ctx->stream, p)
 #define LF_LPK(A)            \

@@ -44,41 +44,41 @@ int transition(lf_context* ctx, const lf_transition_args& a) {
     chunk = (budget / row_bytes) / 128 * 128;
     LF_REQUIRE(chunk >= 128, "transition: chunk budget cannot hold one 128-row tile of the hidden activation");
   }
-  size_t sizes[4] = {(size_t)(chunk * row_bytes)};
-  for (int i = 0; i < nv; ++i) sizes[1 + i] = expanded_bytes(views[i]);
-  void* bufs[4];
-  LF_TRY(workspace(ctx, sizes, bufs, 1 + nv));
+  LnProjParams pp{};
+  pp.C = C;
+  pp.rmQ = 1;
+  pp.rmB = 0;
+  pp.ln_s = w.norm_scale;
+  pp.ln_o = w.norm_offset;
+  pp.eps = a.epsilon;
+  pp.fast_var = a.fast_variance;
+  pp.ngroups = 1;
+  if (a.kind == LF_TRANSITION_RELU)
+    pp.g[0] = Group{views[0], WView{}, Hd, OP_RELU, 1.f, w.b1, nullptr, Dst{}};
+  else
+    pp.g[0] = Group{views[0], views[1], Hd, OP_SWIGLU, 1.f, w.b1, w.b1 ? w.b1 + Hd : nullptr, Dst{}};
+
+  size_t sizes[3] = {(size_t)(chunk * row_bytes), expanded_bytes(views[nv - 1]), lnproj_packed_bytes(pp)};
+  void* bufs[3];
+  LF_TRY(workspace(ctx, sizes, bufs, 3));
   _Float16* hid = static_cast<_Float16*>(bufs[0]);
-  WExp ex[3];
-  LF_TRY(expand_weights(ctx, views, nv, bufs + 1, ex, "transition.expand"));
+  WExp w2;
+  LF_TRY(expand_weights(ctx, &views[nv - 1], 1, &bufs[1], &w2, "transition.expand"));
   const size_t ab = act_bytes(a.act_dtype);
 
   for (long long r0 = 0; r0 < a.rows; r0 += chunk) {
     const int n = (int)std::min<long long>(chunk, a.rows - r0);
-    LnProjParams pp{};
     pp.x = static_cast<const char*>(a.act) + (size_t)r0 * C * ab;
     pp.rows = n;
-    pp.C = C;
-    pp.rmQ = 1;
-    pp.rmB = 0;
-    pp.ln_s = w.norm_scale;
-    pp.ln_o = w.norm_offset;
-    pp.eps = a.epsilon;
-    pp.fast_var = a.fast_variance;
-    pp.ngroups = 1;
-    Dst hd = dst_rowmajor(hid, DT_F16, n, Hd);
-    if (a.kind == LF_TRANSITION_RELU)
-      pp.g[0] = Group{ex[0], WExp{}, Hd, OP_RELU, 1.f, w.b1, nullptr, hd};
-    else
-      pp.g[0] = Group{ex[0], ex[1], Hd, OP_SWIGLU, 1.f, w.b1, w.b1 ? w.b1 + Hd : nullptr, hd};
-    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, "transition.first"));
+    pp.g[0].dst = dst_rowmajor(hid, DT_F16, n, Hd);
+    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[2], "transition.first", r0 == 0));
 
     RowGemmParams rp{};
     rp.A = hid;
     rp.rows = n;
     rp.K = Hd;
     rp.N = C;
-    rp.w = ex[nv - 1];
+    rp.w = w2;
     rp.bias = w.b2;
     rp.op = OP_STORE;
     rp.resid = a.accumulate ? static_cast<const char*>(a.act) + (size_t)r0 * C * ab : nullptr;

@@ -17,8 +17,23 @@
 
 namespace {
 
-struct DevBuf {
+// A context handle shared by the JS context object and every buffer made on it.  Buffers are
+// freed by their finalizers, which N-API may run after contextDestroy (or at exit, in any
+// order), so the holder outlives the context: once the context is gone a finalizer frees
+// nothing (lf_context_destroy released every allocation), and the last reference deletes
+// the holder.
+struct CtxHolder {
   lf_context* ctx;
+  bool alive;
+  long refs;
+};
+
+void holder_release(CtxHolder* h) {
+  if (--h->refs == 0) delete h;
+}
+
+struct DevBuf {
+  CtxHolder* h;
   void* ptr;
   size_t bytes;
 };
@@ -40,13 +55,29 @@ napi_value throw_lf(napi_env env, int rc, const char* what) {
 
 void buf_finalize(napi_env, void* data, void*) {
   DevBuf* b = static_cast<DevBuf*>(data);
-  if (b->ptr && b->ctx) lf_free(b->ctx, b->ptr);
+  if (b->ptr && b->h->alive) lf_free(b->h->ctx, b->ptr);
+  holder_release(b->h);
   delete b;
 }
 
+// a context object collected without contextDestroy releases its device memory here
 void ctx_finalize(napi_env, void* data, void*) {
-  // contexts are destroyed explicitly (contextDestroy); nothing to do here
-  (void)data;
+  CtxHolder* h = static_cast<CtxHolder*>(data);
+  if (h->alive) {
+    lf_context_destroy(h->ctx);
+    h->alive = false;
+  }
+  holder_release(h);
+}
+
+DevBuf* new_buf(CtxHolder* h, size_t bytes) {
+  ++h->refs;
+  return new DevBuf{h, nullptr, bytes};
+}
+
+void drop_buf(DevBuf* b) {
+  holder_release(b->h);
+  delete b;
 }
 
 bool get_args(napi_env env, napi_callback_info info, size_t n, napi_value* argv) {
@@ -55,10 +86,16 @@ bool get_args(napi_env env, napi_callback_info info, size_t n, napi_value* argv)
   return argc >= n;
 }
 
-lf_context* as_ctx(napi_env env, napi_value v) {
+CtxHolder* as_holder(napi_env env, napi_value v) {
   void* p = nullptr;
   napi_get_value_external(env, v, &p);
-  return static_cast<lf_context*>(p);
+  return static_cast<CtxHolder*>(p);
+}
+
+// NULL once destroyed: every lf_* entry point rejects a NULL context with an error
+lf_context* as_ctx(napi_env env, napi_value v) {
+  CtxHolder* h = as_holder(env, v);
+  return h && h->alive ? h->ctx : nullptr;
 }
 
 bool has(napi_env env, napi_value obj, const char* name) {
@@ -214,15 +251,20 @@ napi_value ContextCreate(napi_env env, napi_callback_info info) {
   if (get_args(env, info, 1, argv)) napi_get_value_int32(env, argv[0], &dev);
   lf_context* ctx = lf_context_create(dev);
   if (!ctx) return throw_lf(env, LF_ERR_DEVICE, "lf_context_create");
+  CtxHolder* h = new CtxHolder{ctx, true, 1};
   napi_value ext;
-  NAPI_OK(napi_create_external(env, ctx, ctx_finalize, nullptr, &ext));
+  NAPI_OK(napi_create_external(env, h, ctx_finalize, nullptr, &ext));
   return ext;
 }
 
 napi_value ContextDestroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
-  lf_context_destroy(as_ctx(env, argv[0]));
+  CtxHolder* h = as_holder(env, argv[0]);
+  if (h && h->alive) {
+    lf_context_destroy(h->ctx);
+    h->alive = false;
+  }
   return undefined_value(env);
 }
 
@@ -234,6 +276,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   lf_context* ctx = as_ctx(env, argv[0]);
+  if (!ctx) return throw_lf(env, LF_ERR_INVALID, "upload: the context was destroyed");
   void* data = nullptr;
   size_t bytes = 0;
   bool is_ta = false;
@@ -254,17 +297,17 @@ napi_value Upload(napi_env env, napi_callback_info info) {
   } else {
     NAPI_OK(napi_get_buffer_info(env, argv[1], &data, &bytes));
   }
-  DevBuf* b = new DevBuf{ctx, nullptr, bytes};
+  DevBuf* b = new_buf(as_holder(env, argv[0]), bytes);
   int rc = lf_malloc(ctx, bytes, &b->ptr);
   if (rc != LF_OK) {
-    delete b;
+    drop_buf(b);
     return throw_lf(env, rc, "lf_malloc");
   }
   if (bytes) {
     rc = lf_memcpy_htod(ctx, b->ptr, data, bytes);
     if (rc != LF_OK) {
       lf_free(ctx, b->ptr);
-      delete b;
+      drop_buf(b);
       return throw_lf(env, rc, "lf_memcpy_htod");
     }
   }
@@ -278,12 +321,13 @@ napi_value Alloc(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!get_args(env, info, 2, argv)) return nullptr;
   lf_context* ctx = as_ctx(env, argv[0]);
+  if (!ctx) return throw_lf(env, LF_ERR_INVALID, "alloc: the context was destroyed");
   double bytes = 0;
   napi_get_value_double(env, argv[1], &bytes);
-  DevBuf* b = new DevBuf{ctx, nullptr, (size_t)bytes};
+  DevBuf* b = new_buf(as_holder(env, argv[0]), (size_t)bytes);
   int rc = lf_malloc(ctx, b->bytes, &b->ptr);
   if (rc != LF_OK) {
-    delete b;
+    drop_buf(b);
     return throw_lf(env, rc, "lf_malloc");
   }
   napi_value ext;
@@ -323,7 +367,7 @@ napi_value Free(napi_env env, napi_callback_info info) {
   napi_get_value_external(env, argv[0], &p);
   DevBuf* b = static_cast<DevBuf*>(p);
   if (b && b->ptr) {
-    lf_free(b->ctx, b->ptr);
+    if (b->h->alive) lf_free(b->h->ctx, b->ptr);
     b->ptr = nullptr;
   }
   return undefined_value(env);
