@@ -43,6 +43,7 @@ struct Group {
 };
 
 constexpr int MAX_GROUPS = 6;
+constexpr int MAX_CHUNKS = 128;   // 64-column weight chunks per lnproj launch
 
 struct LnProjParams {
   const void* x;
@@ -55,6 +56,9 @@ struct LnProjParams {
   Group g[MAX_GROUPS];
   int ngroups;
   const _Float16* wpk;    // packed weights (set by launch_lnproj)
+  int nchunks;            // set by launch_lnproj: chunk ci covers group chunk_group[ci]'s
+  unsigned char chunk_group[MAX_CHUNKS];   // logical columns from chunk_c0[ci]
+  short chunk_c0[MAX_CHUNKS];
 };
 
 struct RowGemmParams {

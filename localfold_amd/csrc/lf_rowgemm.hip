@@ -6,43 +6,7 @@
 
 namespace lf {
 
-constexpr int RG_WAVES = 8;            // 8 waves x 16 rows = 128 rows per block
-constexpr int RG_ROWS = RG_WAVES * 16;
-
-__device__ __forceinline__ long long dst_rowpart(const Dst& d, int row) {
-  return (long long)(row / d.Q) * d.sB + (long long)(row % d.Q) * d.sN;
-}
-__device__ __forceinline__ long long dst_colpart(const Dst& d, int col) {
-  return (long long)(col / d.D) * d.sH + (long long)(col % d.D) * d.sD;
-}
-
-__device__ __forceinline__ void dst_store(const Dst& d, long long idx, float v) {
-  if (d.dtype == DT_F32) static_cast<float*>(d.ptr)[idx] = v;
-  else if (d.dtype == DT_F16) static_cast<_Float16*>(d.ptr)[idx] = (_Float16)v;
-  else static_cast<uint16_t*>(d.ptr)[idx] = f2bf(v);
-}
-
-__device__ __forceinline__ float dst_load(const void* ptr, int dtype, long long idx) {
-  if (dtype == DT_F32) return static_cast<const float*>(ptr)[idx];
-  if (dtype == DT_F16) return (float)static_cast<const _Float16*>(ptr)[idx];
-  return bf2f(static_cast<const uint16_t*>(ptr)[idx]);
-}
-
-// Chunk `ci` of an lnproj launch -> (group, first logical column, columns per half)
-__device__ __forceinline__ void chunk_of(const LnProjParams& p, int ci, int& gi, int& c0) {
-  gi = 0;
-  c0 = 0;
-  for (int g = 0; g < p.ngroups; ++g) {
-    const int w = p.g[g].op == OP_SWIGLU ? 32 : 64;
-    const int n = (p.g[g].ncols + w - 1) / w;
-    if (ci < n) {
-      gi = g;
-      c0 = ci * w;
-      return;
-    }
-    ci -= n;
-  }
-}
+constexpr int LP_ROWS = 8 * 32;         // 8 waves x 32 rows
 
 // Loads chunk ci of the packed weights (a contiguous [64][KP] f16 block) into registers
 // (NREG 16-byte words per thread), to be stored into LDS later.
@@ -67,14 +31,6 @@ __device__ __forceinline__ void chunk_store(_Float16* Ws, const uint4 (&regs)[NR
   }
 }
 
-// lnproj: 8 waves x 32 rows (two 16-row tiles) = 256 rows per block.  The LayerNorm'd rows
-// stay in registers as MFMA B fragments for the whole launch; the weights stream through
-// double-buffered LDS in 64-column chunks, and every weight fragment read from LDS feeds two
-// MFMAs (one per row tile).  The weights are the A operand, so a lane ends up holding four
-// consecutive output columns of one row: stores are 8-byte vectors wherever the destination
-// keeps those columns contiguous.  Destinations are f16 with 32-bit element offsets.
-constexpr int LP_ROWS = RG_WAVES * 32;
-
 __device__ __forceinline__ int dst_row32(const Dst& d, int row) {
   const unsigned q = (unsigned)d.Q;
   const unsigned b = (unsigned)row / q, n = (unsigned)row - b * q;
@@ -86,21 +42,41 @@ __device__ __forceinline__ int dst_col32(const Dst& d, int col) {
   return (int)h * (int)d.sH + (int)e * (int)d.sD;
 }
 
-// Four consecutive columns cb..cb+3 of one row: one 8-byte store when they are contiguous in
-// the destination, else element stores (columns >= ncols are dropped).
-__device__ __forceinline__ void store_cols4(const Group& G, int rowpart, int cb, const float (&v)[4]) {
-  _Float16* out = static_cast<_Float16*>(G.dst.ptr);
-  const unsigned dd = (unsigned)G.dst.D;
-  const unsigned e0 = (unsigned)cb % dd;
-  if (G.dst.sD == 1 && cb + 3 < G.ncols && e0 + 3 < dd && ((rowpart + dst_col32(G.dst, cb)) & 3) == 0) {
+// Per-chunk epilogue table, built by wave 0 for the next chunk while the others work:
+// destination column offsets (-1 past the group's columns) and scaled biases of the chunk's
+// logical columns (64, or 32 gate/value pairs for SwiGLU).
+struct ChunkTab {
+  int cofs[64];
+  float b0[64];
+  float b1[64];
+};
+
+__device__ __forceinline__ void build_chunk_tab(ChunkTab& T, const LnProjParams& p, int ci, int lane) {
+  const Group& G = p.g[__builtin_amdgcn_readfirstlane(p.chunk_group[ci])];
+  const int c = __builtin_amdgcn_readfirstlane(p.chunk_c0[ci]) + lane;
+  const bool ok = c < G.ncols;
+  T.cofs[lane] = ok ? dst_col32(G.dst, c) : -1;
+  T.b0[lane] = ok && G.bias0 ? G.bias0[c] * G.scale : 0.f;
+  T.b1[lane] = ok && G.bias1 ? G.bias1[c] * G.scale : 0.f;
+}
+
+// Four consecutive logical columns of one row.  When every lane of the wave has its four
+// columns valid, contiguous and 8-byte aligned in the destination (the usual case) all
+// lanes take one vector store, decided by a wave-uniform vote; otherwise each lane stores
+// its valid elements.
+__device__ __forceinline__ void store4(_Float16* out, int rowpart, int4 co, bool row_ok, const float (&v)[4]) {
+  const bool vec = row_ok && co.x >= 0 && co.y == co.x + 1 && co.z == co.x + 2 && co.w == co.x + 3 &&
+                   ((rowpart + co.x) & 3) == 0;
+  if (__all(vec)) {
     h4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = (_Float16)v[i];
-    *reinterpret_cast<h4*>(out + rowpart + dst_col32(G.dst, cb)) = o;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (cb + i < G.ncols) out[rowpart + dst_col32(G.dst, cb + i)] = (_Float16)v[i];
+    *reinterpret_cast<h4*>(out + rowpart + co.x) = o;
+  } else if (row_ok) {
+    if (co.x >= 0) out[rowpart + co.x] = (_Float16)v[0];
+    if (co.y >= 0) out[rowpart + co.y] = (_Float16)v[1];
+    if (co.z >= 0) out[rowpart + co.z] = (_Float16)v[2];
+    if (co.w >= 0) out[rowpart + co.w] = (_Float16)v[3];
   }
 }
 
@@ -110,21 +86,24 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
   constexpr int NREG = (64 * KP / 8 + 511) / 512;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[2][64 * LDW];
   __shared__ __attribute__((aligned(16))) float Gs[2 * KP];
+  __shared__ __attribute__((aligned(16))) ChunkTab Tab[2];
+  __shared__ int Rp[MAX_GROUPS][LP_ROWS];   // destination row offsets per group and block row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   stage_vec(Gs, p.ln_s, p.C, 1.f, KP, tid, 512);
   stage_vec(Gs + KP, p.ln_o, p.C, 0.f, KP, tid, 512);
-
-  int nchunks = 0;
-  for (int g = 0; g < p.ngroups; ++g) {
-    const int w = p.g[g].op == OP_SWIGLU ? 32 : 64;
-    nchunks += (p.g[g].ncols + w - 1) / w;
-  }
+  const int nchunks = p.nchunks;
   uint4 regs[NREG];
   chunk_load<KP, NREG>(p, 0, regs, tid);
+  if (wave == 0) build_chunk_tab(Tab[0], p, 0, lane);
+  const int row_block = blockIdx.x * LP_ROWS;
+  for (int i = tid; i < p.ngroups * LP_ROWS; i += 512) {
+    const int g = i / LP_ROWS, r = i - g * LP_ROWS;
+    Rp[g][r] = row_block + r < p.rows ? dst_row32(p.g[g].dst, row_block + r) : 0;
+  }
 
   // this wave's two 16-row tiles, LayerNorm'd into B fragments
-  const int rbase = blockIdx.x * LP_ROWS + wave * 32;
+  const int rbase = row_block + wave * 32;
   h8 xb[2][KS];
   int srow[2];
   bool rvalid[2];
@@ -140,7 +119,7 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
     frag_load_row(t0, p.x, (size_t)srow[0], p.C, lane);
     frag_load_row(t1, p.x, (size_t)srow[1], p.C, lane);
     chunk_store<KP, NREG>(Ws[0], regs, tid);
-    __syncthreads();  // Gs and chunk 0 staged
+    __syncthreads();  // Gs, chunk 0, its table and the row offsets staged
     frag_ln_raw2(t0, t1, xb[0], xb[1], p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
   }
   float rm[2] = {1.f, 1.f};
@@ -151,6 +130,7 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
 
   for (int ci = 0; ci < nchunks; ++ci) {
     const _Float16* W = Ws[ci & 1];
+    const ChunkTab& T = Tab[ci & 1];
     if (ci + 1 < nchunks) chunk_load<KP, NREG>(p, ci + 1, regs, tid);
     f4 acc[2][4];
 #pragma unroll
@@ -169,46 +149,59 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
     }
-    int gi, c0;
-    chunk_of(p, ci, gi, c0);
+    if (wave == 0 && ci + 1 < nchunks) build_chunk_tab(Tab[(ci + 1) & 1], p, ci + 1, lane);
+
+    // wave-uniform by construction; readfirstlane lets the compiler keep them in SGPRs
+    const int gi = __builtin_amdgcn_readfirstlane(p.chunk_group[ci]);
     const Group& G = p.g[gi];
+    _Float16* out = static_cast<_Float16*>(G.dst.ptr);
+    const float scale = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(G.scale)));
+    const int op = __builtin_amdgcn_readfirstlane(G.op);
+    int rowpart[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      if (!rvalid[tt]) continue;
-      const int rowpart = dst_row32(G.dst, rbase + tt * 16 + r16);
-      if (G.op == OP_SWIGLU) {
+    for (int tt = 0; tt < 2; ++tt) rowpart[tt] = Rp[gi][wave * 32 + tt * 16 + r16];
+    if (op == OP_SWIGLU) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int cb = c0 + t * 16 + 4 * g4;
+      for (int t = 0; t < 2; ++t) {
+        const int cc = t * 16 + 4 * g4;
+        const int4 co = *reinterpret_cast<const int4*>(&T.cofs[cc]);
+        const float4 bg = *reinterpret_cast<const float4*>(&T.b0[cc]);
+        const float4 bv = *reinterpret_cast<const float4*>(&T.b1[cc]);
+        const float bgs[4] = {bg.x, bg.y, bg.z, bg.w}, bvs[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
           float v[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int c = cb + i < G.ncols ? cb + i : 0;
-            const float gt = (acc[tt][t][i] + (G.bias0 ? G.bias0[c] : 0.f)) * G.scale;
-            const float vl = (acc[tt][t + 2][i] + (G.bias1 ? G.bias1[c] : 0.f)) * G.scale;
+            const float gt = fmaf(acc[tt][t][i], scale, bgs[i]);
+            const float vl = fmaf(acc[tt][t + 2][i], scale, bvs[i]);
             v[i] = gt * sigmoidf_(gt) * vl;
           }
-          if (cb < G.ncols) store_cols4(G, rowpart, cb, v);
-          __builtin_amdgcn_sched_barrier(0);
+          store4(out, rowpart[tt], co, rvalid[tt], v);
         }
-      } else {
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int cb = c0 + t * 16 + 4 * g4;
-          if (cb >= G.ncols) continue;
+      for (int t = 0; t < 4; ++t) {
+        const int cc = t * 16 + 4 * g4;
+        const int4 co = *reinterpret_cast<const int4*>(&T.cofs[cc]);
+        const float4 bb = *reinterpret_cast<const float4*>(&T.b0[cc]);
+        const float bs[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
           float v[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int c = cb + i < G.ncols ? cb + i : 0;
-            float y = (acc[tt][t][i] + (G.bias0 ? G.bias0[c] : 0.f)) * G.scale;
-            if (G.op == OP_SIGMOID) y = sigmoidf_(y);
-            else if (G.op == OP_RELU) y = fmaxf(y, 0.f);
-            else if (G.op == OP_ROWMASK) y *= rm[tt];
+            float y = fmaf(acc[tt][t][i], scale, bs[i]);
+            if (op == OP_SIGMOID) y = sigmoidf_(y);
+            else if (op == OP_RELU) y = fmaxf(y, 0.f);
+            else if (op == OP_ROWMASK) y *= rm[tt];
             v[i] = y;
           }
-          store_cols4(G, rowpart, cb, v);
-          __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
+          store4(out, rowpart[tt], co, rvalid[tt], v);
         }
+        __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
       }
     }
     if (ci + 1 < nchunks) {
@@ -269,6 +262,16 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
     rows_done += (long long)(G.ncols + w - 1) / w * 64;
   }
   p.wpk = static_cast<const _Float16*>(packed);
+  p.nchunks = 0;
+  for (int g = 0; g < p.ngroups; ++g) {
+    const int w = p.g[g].op == OP_SWIGLU ? 32 : 64;
+    for (int c0 = 0; c0 < p.g[g].ncols; c0 += w) {
+      if (p.nchunks == MAX_CHUNKS) return set_error(LF_ERR_INVALID, std::string(label) + ": too many output columns");
+      if (c0 > 32767) return set_error(LF_ERR_INVALID, std::string(label) + ": group wider than 32767 columns");
+      p.chunk_group[p.nchunks] = (unsigned char)g;
+      p.chunk_c0[p.nchunks++] = (short)c0;
+    }
+  }
   if (decode)
     LF_TRY(expand_packed(ctx, views, W, off, row0, nv, static_cast<_Float16*>(packed), KP,
                        (std::string(label) + ".expand").c_str()));
@@ -292,126 +295,189 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
 
 // ---------------------------------------------------------------------------------------
 
-constexpr int RGK = 128;             // K slice per LDS stage
-constexpr int RG_LDW = RGK + 8;
+// rowgemm: block tile 128 rows x (32 * NT) columns; 8 waves = 4 row groups (32 rows, two
+// 16-row tiles) x 2 column halves (16 * NT columns).  A rows are read from global straight
+// into MFMA B fragments (each A element leaves HBM once; the other column half hits L2), one
+// 64-deep K slice ahead; the weights stream through double-buffered LDS one K slice at a
+// time.  The weights are the A operand, so a lane holds 4 consecutive output columns of one
+// row and the epilogue (bias, ReLU, row denominator, residual) works on 4-element vectors.
+constexpr int RB_K = 64, RB_LDW = RB_K + 8;
 
 template <int DACT>
+__device__ __forceinline__ void ld4(const void* base, int idx, float (&v)[4]) {
+  if constexpr (DACT == DT_F32) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else if constexpr (DACT == DT_F16) {
+    const h4 q = *reinterpret_cast<const h4*>(static_cast<const _Float16*>(base) + idx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)q[i];
+  } else {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
+    v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
+  }
+}
+
+template <int DACT>
+__device__ __forceinline__ void st4(void* base, int idx, const float (&v)[4]) {
+  if constexpr (DACT == DT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (DACT == DT_F16) {
+    h4 q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = (_Float16)v[i];
+    *reinterpret_cast<h4*>(static_cast<_Float16*>(base) + idx) = q;
+  } else {
+    uint2 q;
+    q.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+    q.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + idx) = q;
+  }
+}
+
+template <int DACT, int NT>
 __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
-  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][64 * RG_LDW];
+  constexpr int BN = 32 * NT;                 // block columns
+  constexpr int WREG = (BN * RB_K / 8 + 511) / 512;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][BN * RB_LDW];
+  __shared__ __attribute__((aligned(16))) float Bs[BN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
-  const int row0 = blockIdx.x * RG_ROWS + wave * 16;
-  const int myrow = row0 + r16;
-  const _Float16* arow = p.A + (size_t)(myrow < p.rows ? myrow : 0) * p.K;
-  const int nks = (p.K + RGK - 1) / RGK, ncs = (p.N + 63) / 64, nst = nks * ncs;
-  const bool kvec = (p.K & 7) == 0;
+  const int wr = wave >> 1, wc = wave & 1;    // row group, column half
+  const int col0 = blockIdx.y * BN;           // block's first output column
+  const int rbase = blockIdx.x * 128 + wr * 32;
+  const int nslices = (p.K + RB_K - 1) / RB_K;
+  for (int i = tid; i < BN; i += 512) Bs[i] = (p.bias && col0 + i < p.N) ? p.bias[col0 + i] : 0.f;
 
-  // stage s = (column chunk s / nks, K slice s % nks): [64 cols][128 k] of the expanded weights
-  auto wload = [&](int s, uint4 (&regs)[2]) {
-    const int cc = s / nks, kc = s - cc * nks;
+  // weights of slice s: [BN cols][64 k] of the expanded E[n][kp]
+  auto wload = [&](int sl, uint4 (&regs)[WREG]) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int i = tid + r * 512, n = i >> 4, seg = i & 15;
-      const int col = cc * 64 + n, k = kc * RGK + seg * 8;
+    for (int r = 0; r < WREG; ++r) {
+      const int i = tid + r * 512, n = i >> 3, seg = i & 7;
+      const int col = col0 + n, k = sl * RB_K + seg * 8;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (col < p.w.N && k < p.w.kp) v = *reinterpret_cast<const uint4*>(p.w.p + (size_t)col * p.w.kp + k);
+      if (n < BN && col < p.w.N && k < p.w.kp) v = *reinterpret_cast<const uint4*>(p.w.p + (size_t)col * p.w.kp + k);
       regs[r] = v;
     }
   };
-  auto wstore = [&](_Float16* W, const uint4 (&regs)[2]) {
+  auto wstore = [&](_Float16* W, const uint4 (&regs)[WREG]) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int i = tid + r * 512, n = i >> 4, seg = i & 15;
-      *reinterpret_cast<uint4*>(W + n * RG_LDW + seg * 8) = regs[r];
+    for (int r = 0; r < WREG; ++r) {
+      const int i = tid + r * 512, n = i >> 3, seg = i & 7;
+      if (n < BN) *reinterpret_cast<uint4*>(W + n * RB_LDW + seg * 8) = regs[r];
     }
   };
-  uint4 regs[2];
+  // A fragments of slice s for both row tiles (rows past the end read row 0; K is a multiple
+  // of 8, so an 8-element run is either inside K or wholly past it)
+  const _Float16* arow[2];
+  bool rvalid[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int row = rbase + tt * 16 + r16;
+    rvalid[tt] = row < p.rows;
+    arow[tt] = p.A + (size_t)(rvalid[tt] ? row : 0) * p.K;
+  }
+  auto aload = [&](int sl, h8 (&a)[2][2]) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int k = sl * RB_K + 32 * j + kq;
+        a[tt][j] = k < p.K ? *reinterpret_cast<const h8*>(arow[tt] + k) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+  };
+
+  uint4 regs[WREG];
+  h8 acur[2][2], anext[2][2];
   wload(0, regs);
+  aload(0, acur);
   wstore(Ws[0], regs);
   __syncthreads();
 
-  f4 acc[4];
-  for (int s = 0; s < nst; ++s) {
-    const int cc = s / nks, kc = s - cc * nks;
-    if (kc == 0)
+  f4 acc[2][NT];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-    // this slice's A fragments first, then the next stage's weights: the MFMAs wait only
-    // for the A loads (loads complete in issue order)
-    h8 a[4];
+  for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kc * RGK + 32 * j + kq;
-      if (kvec) {
-        a[j] = *reinterpret_cast<const h8*>(arow + (k + 8 <= p.K ? k : 0));
-        if (k + 8 > p.K) a[j] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      } else {
+    for (int t = 0; t < NT; ++t) acc[tt][t] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int sl = 0; sl < nslices; ++sl) {
+    if (sl + 1 < nslices) {
+      aload(sl + 1, anext);
+      wload(sl + 1, regs);
+    }
+    const _Float16* W = Ws[sl & 1] + (wc * 16 * NT) * RB_LDW;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[j][e] = arow[k + e < p.K ? k + e : 0];
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (k + e >= p.K) a[j][e] = (_Float16)0.f;
+      for (int t = 0; t < NT; ++t) {
+        const h8 w = *reinterpret_cast<const h8*>(W + (t * 16 + r16) * RB_LDW + 32 * j + kq);
+        acc[0][t] = mfma16(w, acur[0][j], acc[0][t]);
+        acc[1][t] = mfma16(w, acur[1][j], acc[1][t]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (s + 1 < nst) wload(s + 1, regs);
-    const _Float16* W = Ws[s & 1];
+    if (sl + 1 < nslices) {
+      wstore(Ws[(sl + 1) & 1], regs);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc[t] = mfma16(a[j], *reinterpret_cast<const h8*>(W + (t * 16 + r16) * RG_LDW + 32 * j + kq), acc[t]);
+        for (int j = 0; j < 2; ++j) acur[tt][j] = anext[tt][j];
+      __syncthreads();
     }
-    if (kc == nks - 1) {
-      long long rp[4], cp[4];
-      float den[4], res[4][4];
+  }
+
+  // epilogue: lane holds columns c..c+3 (c = col0 + wc*16*NT + 16t + 4*g4) of row rbase + 16tt + r16
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    if (!rvalid[tt]) continue;
+    const int row = rbase + tt * 16 + r16;
+    const unsigned q = (unsigned)p.dst.Q;
+    const unsigned b = (unsigned)row / q, n = (unsigned)row - b * q;
+    const int rowpart = (int)b * (int)p.dst.sB + (int)n * (int)p.dst.sN;
+    const float den = p.rowden ? 1.f / p.rowden[row] : 1.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int cl = wc * 16 * NT + t * 16 + 4 * g4;   // column within the block
+      const int c = col0 + cl;
+      if (c >= p.N) continue;
+      const float4 bb = *reinterpret_cast<const float4*>(&Bs[cl]);
+      const float bs[4] = {bb.x, bb.y, bb.z, bb.w};
+      float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = row0 + g4 * 4 + i;
-        rp[i] = dst_rowpart(p.dst, row < p.rows ? row : 0);
-        den[i] = p.rowden ? p.rowden[row < p.rows ? row : 0] : 1.f;
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int col = cc * 64 + t * 16 + r16;
-        cp[t] = dst_colpart(p.dst, col < p.N ? col : 0);
+        float y = acc[tt][t][i] + bs[i];
+        if (p.op == OP_RELU) y = fmaxf(y, 0.f);
+        v[i] = y * den;
       }
       if (p.resid) {
+        float r[4];
+        ld4<DACT>(p.resid, rowpart + c, r);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) res[t][i] = dst_load(p.resid, DACT, rp[i] + cp[t]);
+        for (int i = 0; i < 4; ++i) v[i] += r[i];
       }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int col = cc * 64 + t * 16 + r16;
-        if (col >= p.N) continue;
-        const float b = p.bias ? p.bias[col] : 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = row0 + g4 * 4 + i;
-          if (row >= p.rows) continue;
-          float v = acc[t][i] + b;
-          if (p.op == OP_RELU) v = fmaxf(v, 0.f);
-          if (p.rowden) v = v / den[i];
-          if (p.resid) v += res[t][i];
-          dst_store(p.dst, rp[i] + cp[t], v);
-        }
-      }
-    }
-    if (s + 1 < nst) {
-      wstore(Ws[(s + 1) & 1], regs);
-      __syncthreads();
+      st4<DACT>(p.dst.ptr, rowpart + c, v);
     }
   }
 }
 
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   if (p.rows <= 0) return LF_OK;
-  dim3 grid((p.rows + RG_ROWS - 1) / RG_ROWS);
+  const std::string l(label);
+  if (p.K % 8 != 0 || p.N % 4 != 0) return set_error(LF_ERR_INVALID, l + ": rowgemm needs K % 8 == 0 and N % 4 == 0");
+  const Dst& d = p.dst;
+  if (d.sD != 1 || d.D < p.N || d.sB % 4 != 0 || d.sN % 4 != 0)
+    return set_error(LF_ERR_INVALID, l + ": rowgemm destination columns must be contiguous and 4-aligned");
+  const long long span = (long long)((p.rows - 1) / d.Q) * d.sB + (long long)std::min(p.rows - 1, d.Q - 1) * d.sN + p.N;
+  if (span >= (1LL << 31)) return set_error(LF_ERR_INVALID, l + ": destination above 2^31 elements");
+  const int nt = p.N <= 128 ? 4 : 8;
+  dim3 grid((p.rows + 127) / 128, (p.N + 32 * nt - 1) / (32 * nt));
   LaunchScope ls(ctx, label);
-  if (p.dst.dtype == DT_F32) hipLaunchKernelGGL(rowgemm_kernel<DT_F32>, grid, dim3(512), 0, ctx->stream, p);
-  else if (p.dst.dtype == DT_F16) hipLaunchKernelGGL(rowgemm_kernel<DT_F16>, grid, dim3(512), 0, ctx->stream, p);
-  else hipLaunchKernelGGL(rowgemm_kernel<DT_BF16>, grid, dim3(512), 0, ctx->stream, p);
+#define LF_RG(D, T) hipLaunchKernelGGL((rowgemm_kernel<D, T>), grid, dim3(512), 0, ctx->stream, p)
+  if (d.dtype == DT_F32) { if (nt == 4) LF_RG(DT_F32, 4); else LF_RG(DT_F32, 8); }
+  else if (d.dtype == DT_F16) { if (nt == 4) LF_RG(DT_F16, 4); else LF_RG(DT_F16, 8); }
+  else { if (nt == 4) LF_RG(DT_BF16, 4); else LF_RG(DT_BF16, 8); }
+#undef LF_RG
   return check_hip(hipGetLastError(), label);
 }
 
