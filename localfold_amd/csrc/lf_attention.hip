@@ -40,18 +40,49 @@ struct FlashParams {
   long long nblocks;
 };
 
+// The softmax runs in base 2: q, the pair bias and the key-mask bias are stored pre-multiplied
+// by log2(e), so p = exp2(x - max) with x = log2(e) * logit, and the +-1e8 clamp becomes
+// +-1e8 * log2(e).  Mathematically identical to exp(logit - max).
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float FA_CLAMP = 1e8f * LOG2E;
+
 __global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* kb, int B, int Q, int transpose) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long long)B * Q) return;
   const int b = (int)(i / Q), k = (int)(i % Q);
   const float m = mask[transpose ? (long long)k * B + b : i];
-  kb[i] = 1e9f * (m - 1.0f);
+  kb[i] = (1e9f * LOG2E) * (m - 1.0f);
 }
 
+// Pair-bias values of one lane for one key chunk: queries of the lane's two tiles (rows
+// brow[qt], already offset by 4*g4), keys k0 + 16kt + 4g4 .. +3.  Full chunks with Q % 4 == 0
+// load 8-byte pieces at constant offsets; the last (partial) chunk clamps element-wise.
+__device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[2], int Q, int k0, int g4, bool full,
+                                           h4 (&bv)[2][4]) {
+  if (full) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) bv[qt][kt] = *reinterpret_cast<const h4*>(brow[qt] + k0 + kt * 16);
+  } else {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = k0 + kt * 16 + 4 * g4 + i;   // keys >= Q are discarded via the key bias
+          bv[qt][kt][i] = brow[qt][(kk < Q ? kk : 0) - 4 * g4];
+        }
+  }
+}
+
+template <bool BIAS>
 __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_KC * FA_KLD];
   __shared__ __attribute__((aligned(16))) _Float16 Vs[2][FA_DP * FA_VLD];
   __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
+  __shared__ int Kmasked[2];   // chunk has a masked key or a key past Q
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
 
@@ -70,17 +101,21 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
   const _Float16* kh = p.k + bh * p.Q * FA_DP;
   const _Float16* vh = p.vt + bh * FA_DP * p.Q;
   const float* kbb = p.kb + (size_t)b * p.Q;
-  const _Float16* bias = p.bias ? p.bias + (size_t)h * p.Q * p.Q : nullptr;
+  const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * p.Q : nullptr;
 
   // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
-  int qidx[2];
+  int qidx[2], qc[2];
   h8 qf[2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     qidx[qt] = qb * FA_QPB + wave * FA_QPW + qt * 16 + r16;
-    const int qc = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
-    qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc * FA_DP + kq);
+    qc[qt] = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
+    qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc[qt] * FA_DP + kq);
   }
+  const _Float16* brow[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) brow[qt] = BIAS ? bias + (size_t)qc[qt] * p.Q + 4 * g4 : nullptr;
+  const bool bias_vec = (p.Q & 3) == 0;
 
   const int nkc = (p.Q + FA_KC - 1) / FA_KC;
   const bool vecv = (p.Q & 7) == 0;
@@ -122,12 +157,18 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
       const int dd = tid >> 3, seg = tid & 7;
       *reinterpret_cast<uint4*>(&Vs[buf][dd * FA_VLD + seg * 8]) = vr;
     }
-    if (tid < FA_KC) Kb[buf][tid] = kbr;
+    if (wave == 0) {
+      Kb[buf][tid] = kbr;
+      const bool any = __any(kbr != 0.f);
+      if (tid == 0) Kmasked[buf] = any ? 1 : 0;
+    }
   };
 
   uint4 kr, vr;
   float kbr;
   kv_load(0, kr, vr, kbr);
+  h4 bcur[2][4], bnext[2][4];
+  if (BIAS) bias_fetch(brow, p.Q, 0, g4, bias_vec && FA_KC <= p.Q, bcur);
   kv_store(0, kr, vr, kbr);
   __syncthreads();
 
@@ -139,29 +180,11 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
     for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
 
   for (int c = 0; c < nkc; ++c) {
-    const int buf = c & 1, k0 = c * FA_KC;
-    // pair-bias values for this lane's queries and keys k0 + kt*16 + 4*g4 + i
-    float bv[2][4][4];
-    if (bias) {
-      const bool v4 = (p.Q & 3) == 0;
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const int qc = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const int kk = k0 + kt * 16 + 4 * g4;   // keys >= Q are discarded via the key bias
-          if (v4) {
-            const h4 v = *reinterpret_cast<const h4*>(bias + (size_t)qc * p.Q + (kk + 4 <= p.Q ? kk : p.Q - 4));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bv[qt][kt][i] = (float)v[i];
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bv[qt][kt][i] = (float)bias[(size_t)qc * p.Q + (kk + i < p.Q ? kk + i : 0)];
-          }
-        }
-      }
+    const int buf = c & 1;
+    if (c + 1 < nkc) {
+      kv_load(c + 1, kr, vr, kbr);
+      if (BIAS) bias_fetch(brow, p.Q, (c + 1) * FA_KC, g4, bias_vec && (c + 2) * FA_KC <= p.Q, bnext);
     }
-    if (c + 1 < nkc) kv_load(c + 1, kr, vr, kbr);
     // S^T tiles
     f4 s[2][4];
 #pragma unroll
@@ -170,34 +193,47 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
     }
+    const bool masked = Kmasked[buf] != 0;   // wave-uniform
     _Float16 pv[2][4][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       float mx = -1e30f;
+      if (!masked) {
+        // no masked key in the chunk: the logit is q.k + bias (|x| far below the clamp)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
-        const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = s[qt][kt][i] + kbv[i];
-          if (bias) x += bv[qt][kt][i];
-          // clamp +-1e8 (keys past Q carry -1e30 and stay below every real logit)
-          x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -1e8f), 1e8f);
-          s[qt][kt][i] = x;
-          mx = fmaxf(mx, x);
+          for (int i = 0; i < 4; ++i) {
+            const float x = BIAS ? (float)bcur[qt][kt][i] + s[qt][kt][i] : s[qt][kt][i];
+            s[qt][kt][i] = x;
+            mx = fmaxf(mx, x);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
+          const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = s[qt][kt][i] + kbv[i];
+            if (BIAS) x += (float)bcur[qt][kt][i];
+            // clamp (keys past Q carry -1e30 and stay below every real logit)
+            x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -FA_CLAMP), FA_CLAMP);
+            s[qt][kt][i] = x;
+            mx = fmaxf(mx, x);
+          }
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
       mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
       const float m_new = fmaxf(m_run[qt], mx);
-      const float corr = __expf(m_run[qt] - m_new);
+      const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
       float sum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = __expf(s[qt][kt][i] - m_new);
+          const float e = __builtin_amdgcn_exp2f(s[qt][kt][i] - m_new);
           sum += e;
           pv[qt][kt][i] = (_Float16)e;
         }
@@ -232,6 +268,12 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
       // buffer buf^1 was last read in chunk c-1, which every wave finished before the
       // barrier that ended it
       kv_store(buf ^ 1, kr, vr, kbr);
+      if (BIAS) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) bcur[qt][kt] = bnext[qt][kt];
+      }
       __syncthreads();
     }
   }
@@ -323,7 +365,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     g.w0 = views[5];
     g.ncols = H;
     g.op = OP_STORE;
-    g.scale = 1.f;
+    g.scale = LOG2E;
   }
   // 2. LN + q/k/v/g (+ bias from the normalised input)
   LnProjParams pp{};
@@ -336,13 +378,13 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   pp.ln_o = w.norm_offset;
   pp.eps = a.epsilon;
   pp.fast_var = a.fast_variance;
-  pp.g[0] = Group{views[0], WView{}, HD, OP_STORE, 1.0f / std::sqrt((float)d), w.q_bias, nullptr, Dst{}};
+  pp.g[0] = Group{views[0], WView{}, HD, OP_STORE, LOG2E / std::sqrt((float)d), w.q_bias, nullptr, Dst{}};
   pp.g[1] = Group{views[1], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
   pp.g[2] = Group{views[2], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
   pp.g[3] = Group{views[3], WView{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, Dst{}};
   pp.ngroups = 4;
   if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) {
-    pp.g[4] = Group{views[5], WView{}, H, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+    pp.g[4] = Group{views[5], WView{}, H, OP_STORE, LOG2E, nullptr, nullptr, Dst{}};
     pp.ngroups = 5;
   }
 
@@ -386,7 +428,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   // caller-supplied f32 logits are converted (and transposed per head when swapped); the
   // projected biases were written as f16 by lnproj
   if (a.bias_mode == LF_BIAS_LOGITS)
-    LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0));
+    LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0, LOG2E));
 
   // 4. flash attention
   {
@@ -406,7 +448,8 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     fp.nqb = (Q + FA_QPB - 1) / FA_QPB;
     fp.nblocks = (long long)fp.nqb * B * H;
     LaunchScope ls(ctx, "attention.flash");
-    hipLaunchKernelGGL(flash_kernel, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
+    if (fp.bias) hipLaunchKernelGGL(flash_kernel<true>, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
+    else hipLaunchKernelGGL(flash_kernel<false>, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
   }
   LF_TRY(check_hip(hipGetLastError(), "flash launch"));
 

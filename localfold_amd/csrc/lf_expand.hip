@@ -69,23 +69,24 @@ int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* 
   return LF_OK;
 }
 
-// dst = (f16) src, n elements; with tq > 0 every [tq][tq] plane is transposed.
-__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* src, _Float16* dst, long long n, int tq) {
+// dst = (f16) (scale * src), n elements; with tq > 0 every [tq][tq] plane is transposed.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* src, _Float16* dst, long long n, int tq,
+                                                         float scale) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     long long s = i;
     if (tq > 0) {
       const long long plane = (long long)tq * tq, pl = i / plane, r = i % plane;
       s = pl * plane + (r % tq) * tq + r / tq;
     }
-    dst[i] = (_Float16)src[s];
+    dst[i] = (_Float16)(scale * src[s]);
   }
 }
 
-int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq) {
+int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale) {
   LaunchScope ls(ctx, "convert.f16");
   const long long blocks = std::min<long long>((n + 255) / 256, 65536);
   hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)std::max<long long>(blocks, 1)), dim3(256), 0, ctx->stream,
-                     src, dst, n, tq);
+                     src, dst, n, tq, scale);
   return check_hip(hipGetLastError(), "f32_to_f16 launch");
 }
 

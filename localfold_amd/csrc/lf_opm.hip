@@ -15,88 +15,147 @@
 
 namespace lf {
 
-struct NtGemmParams {
-  const _Float16* A;   // [M][K]
-  const _Float16* B;   // [N][K]
-  int M, N, K;
-  float scale;
-  Dst dst;             // f16, element (m, n)
+// The outer products: O[(i*N + j)][a*co + b] = sum_s L[i][a][s] R[j][b][s], i.e. the NT GEMM
+// (N*co) x (N*co) x S of the rows m = i*co + a and n = j*co + b, stored pair-major f16.
+struct OuterParams {
+  const _Float16* L;   // [N*co][S]
+  const _Float16* R;   // [N*co][S]
+  _Float16* O;         // [N*N][co*co]
+  int N, co, S;
 };
 
-constexpr int NT_TILE = 128, NT_BK = 64, NT_LD = NT_BK + 8;
+constexpr int OT = 128, OT_BK = 64, OT_LD = OT_BK + 8;
 
-template <bool VEC>
-__device__ __forceinline__ void nt_load(_Float16* S, const _Float16* src, int rows, int K, int m0, int k0, int tid) {
-  if (VEC) {
+struct OtRegs {
+  h8 v[4];
+};
+
+// [128 rows][64 k] of a sequence-contiguous operand: global -> registers (issued a K step
+// ahead) -> LDS.  Rows past M and k past S read as zero.
+__device__ __forceinline__ void ot_fetch(OtRegs& r, const _Float16* src, int M, int S, int m0, int k0, int tid,
+                                         bool vec) {
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int e = tid + it * 256, m = e >> 3, seg = e & 7;
-      const int gm = m0 + m, gk = k0 + seg * 8;
-      h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      if (gm < rows && gk < K) v = *reinterpret_cast<const h8*>(src + (size_t)gm * K + gk);
-      *reinterpret_cast<h8*>(S + m * NT_LD + seg * 8) = v;
-    }
-  } else {
-    for (int e = tid; e < NT_TILE * NT_BK; e += 256) {
-      const int m = e / NT_BK, k = e % NT_BK, gm = m0 + m, gk = k0 + k;
-      S[m * NT_LD + k] = (gm < rows && gk < K) ? src[(size_t)gm * K + gk] : (_Float16)0.f;
+  for (int it = 0; it < 4; ++it) {
+    const int e = tid + it * 256, m = m0 + (e >> 3), k = k0 + (e & 7) * 8;
+    if (vec) {
+      r.v[it] = (m < M && k < S) ? *reinterpret_cast<const h8*>(src + (size_t)m * S + k) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) r.v[it][u] = (m < M && k + u < S) ? src[(size_t)m * S + k + u] : (_Float16)0.f;
     }
   }
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(256) void nt_gemm_kernel(NtGemmParams p) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[NT_TILE * NT_LD];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[NT_TILE * NT_LD];
+__device__ __forceinline__ void ot_store(_Float16* Sm, const OtRegs& r, int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int e = tid + it * 256;
+    *reinterpret_cast<h8*>(Sm + (e >> 3) * OT_LD + (e & 7) * 8) = r.v[it];
+  }
+}
+
+// One 128x128 tile per block (4 waves of 64x64).  The 1-D grid is remapped so that each XCD
+// (block ids are dealt round-robin over 8) walks a contiguous band of row tiles, keeping
+// those L rows in its L2.  R is the MFMA A operand, so a lane holds four consecutive b of one
+// (i, a) row: 8-byte stores into the pair-major output.
+__global__ __launch_bounds__(256) void opm_outer_kernel(OuterParams p) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[OT * OT_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[OT * OT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.x * NT_TILE, n0 = blockIdx.y * NT_TILE;
+  const int M = p.N * p.co, tm = (M + OT - 1) / OT;
+  const int total = (int)gridDim.x, per = total >> 3;
+  int lin = (int)blockIdx.x;
+  if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
+  const int m0 = (lin / tm) * OT, n0 = (lin % tm) * OT;
+  const bool vec = (p.S & 7) == 0;
   f4 acc[4][4];
   zero_acc(acc);
-  const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  for (int k0 = 0; k0 < p.K; k0 += NT_BK) {
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+  OtRegs ra, rb;
+  ot_fetch(ra, p.L, M, p.S, m0, 0, tid, vec);
+  ot_fetch(rb, p.R, M, p.S, n0, 0, tid, vec);
+  for (int k0 = 0; k0 < p.S; k0 += OT_BK) {
     __syncthreads();
-    nt_load<VEC>(As, p.A, p.M, p.K, m0, k0, tid);
-    nt_load<VEC>(Bs, p.B, p.N, p.K, n0, k0, tid);
+    ot_store(As, ra, tid);
+    ot_store(Bs, rb, tid);
     __syncthreads();
+    if (k0 + OT_BK < p.S) {
+      ot_fetch(ra, p.L, M, p.S, m0, k0 + OT_BK, tid, vec);
+      ot_fetch(rb, p.R, M, p.S, n0, k0 + OT_BK, tid, vec);
+    }
 #pragma unroll
-    for (int kk = 0; kk < NT_BK; kk += 32) {
+    for (int kk = 0; kk < OT_BK; kk += 32) {
       h8 a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const h8*>(As + (wm * 64 + i * 16 + r16) * NT_LD + kk + kq);
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const h8*>(As + (wm * 64 + i * 16 + r16) * OT_LD + kk + kq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(Bs + (wn * 64 + j * 16 + r16) * NT_LD + kk + kq);
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(Bs + (wn * 64 + j * 16 + r16) * OT_LD + kk + kq);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(b[j], a[i], acc[i][j]);
     }
   }
-  _Float16* out = static_cast<_Float16*>(p.dst.ptr);
+  // acc[i][j][u]: row m = m0 + wm*64 + 16i + r16, columns n = n0 + wn*64 + 16j + 4g4 + u
+  const unsigned co = (unsigned)p.co;
+  const long long cc = (long long)p.co * p.co;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 64 + i * 16 + r16;
+    if (m >= M) continue;
+    const unsigned mi = (unsigned)m / co, ma = (unsigned)m - mi * co;
+    const long long rowpart = (long long)mi * p.N * cc + (long long)ma * p.co;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int gm = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
-      if (gm >= p.M) continue;
-      const long long rp = (long long)(gm / p.dst.Q) * p.dst.sB + (long long)(gm % p.dst.Q) * p.dst.sN;
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 64 + j * 16 + 4 * g4;
+      if (n >= M) continue;
+      const unsigned nj = (unsigned)n / co, nb = (unsigned)n - nj * co;
+      h4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int gn = n0 + wn * 64 + j * 16 + r16;
-        if (gn >= p.N) continue;
-        const long long cp = (long long)(gn / p.dst.D) * p.dst.sH + (long long)(gn % p.dst.D) * p.dst.sD;
-        out[rp + cp] = (_Float16)(acc[i][j][r] * p.scale);
-      }
+      for (int u = 0; u < 4; ++u) o[u] = (_Float16)acc[i][j][u];
+      *reinterpret_cast<h4*>(p.O + rowpart + (long long)nj * cc + nb) = o;
     }
+  }
 }
 
-// den[i*N + j] = eps + sum_s m[s][i] m[s][j]
+// den[i*N + j] = eps + sum_s m[s][i] m[s][j]: a 32x32 tile per block (16x16 threads of 2x2
+// outputs), the mask staged through LDS 64 sequences at a time; sums run in sequence order.
+constexpr int CT_S = 64;
+
 __global__ __launch_bounds__(256) void opm_count_kernel(const float* mask, float* den, int S, int N, float eps) {
-  const int j = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
-  if (j >= N) return;
-  float c = 0.f;
-  for (int s = 0; s < S; ++s) c += mask[(size_t)s * N + i] * mask[(size_t)s * N + j];
-  den[(size_t)i * N + j] = eps + c;
+  __shared__ float Mi[CT_S][32], Mj[CT_S][32];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
+  float acc[2][2] = {};
+  for (int s0 = 0; s0 < S; s0 += CT_S) {
+    for (int e = tid; e < CT_S * 32; e += 256) {
+      const int ss = e >> 5, c = e & 31, sg = s0 + ss;
+      Mi[ss][c] = (sg < S && i0 + c < N) ? mask[(size_t)sg * N + i0 + c] : 0.f;
+      Mj[ss][c] = (sg < S && j0 + c < N) ? mask[(size_t)sg * N + j0 + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int ss = 0; ss < CT_S; ++ss) {
+      const float a0 = Mi[ss][ty * 2], a1 = Mi[ss][ty * 2 + 1];
+      const float b0 = Mj[ss][tx * 2], b1 = Mj[ss][tx * 2 + 1];
+      acc[0][0] = fmaf(a0, b0, acc[0][0]);
+      acc[0][1] = fmaf(a0, b1, acc[0][1]);
+      acc[1][0] = fmaf(a1, b0, acc[1][0]);
+      acc[1][1] = fmaf(a1, b1, acc[1][1]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = i0 + ty * 2 + u;
+    if (i >= N) continue;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int j = j0 + tx * 2 + v;
+      if (j < N) den[(size_t)i * N + j] = eps + acc[u][v];
+    }
+  }
 }
 
 int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
@@ -104,7 +163,7 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   LF_REQUIRE(a.sequences > 0 && a.length > 0 && a.c_m > 0 && a.c_outer > 0 && a.c_z > 0,
              "outer product mean dimensions must be positive safe integers");
   LF_REQUIRE(a.c_m <= 384, "outer product mean: c_m must be <= 384");
-  LF_REQUIRE(a.c_outer <= 64, "outer product mean: c_outer must be <= 64");
+  LF_REQUIRE(a.c_outer <= 64 && a.c_outer % 4 == 0, "outer product mean: c_outer must be a multiple of 4, <= 64");
   LF_REQUIRE(act_dtype_ok(a.msa_dtype) && act_dtype_ok(a.pair_dtype), "outer product mean: bad activation dtype");
   LF_REQUIRE(a.msa && a.mask && a.out, "outer product mean: msa, mask and out must be device pointers");
   LF_REQUIRE(!a.accumulate || a.pair_in, "outer product mean: accumulate needs pair_in");
@@ -121,8 +180,10 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   pp.x = a.msa;
   pp.rows = (int)rows;
   pp.C = a.c_m;
-  pp.rmQ = 1;
-  pp.rmB = 0;
+  // logical row r = i*S + s reads MSA row s*N + i, so a wave's rows are consecutive sequences
+  // of one residue: 16 lanes write 32 contiguous bytes of the sequence-contiguous l and r
+  pp.rmQ = S;
+  pp.rmB = N;
   pp.ln_s = w.norm_scale;
   pp.ln_o = w.norm_offset;
   pp.eps = a.epsilon;
@@ -141,30 +202,21 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   float* den = (float*)bufs[3];
   WExp wo;
   LF_TRY(expand_weights(ctx, &views[2], 1, &bufs[4], &wo, "opm.expand"));
-  // logical row r = s*N + i -> (i*co + a)*S + s
-  pp.g[0].dst = Dst{L, DT_F16, N, 1, (long long)co * S, co, 0, S};
-  pp.g[1].dst = Dst{R, DT_F16, N, 1, (long long)co * S, co, 0, S};
+  // logical row r = i*S + s, column a -> (i*co + a)*S + s
+  pp.g[0].dst = Dst{L, DT_F16, S, (long long)co * S, 1, co, 0, S};
+  pp.g[1].dst = Dst{R, DT_F16, S, (long long)co * S, 1, co, 0, S};
   LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, bufs[5], "opm.project"));
   {
     LaunchScope ls(ctx, "opm.count");
-    hipLaunchKernelGGL(opm_count_kernel, dim3((N + 255) / 256, N), dim3(256), 0, ctx->stream, a.mask, den, S, N,
-                       a.norm_epsilon);
+    hipLaunchKernelGGL(opm_count_kernel, dim3((N + 31) / 32, (N + 31) / 32), dim3(256), 0, ctx->stream, a.mask, den,
+                       S, N, a.norm_epsilon);
   }
   LF_TRY(check_hip(hipGetLastError(), "opm count launch"));
   {  // O[(i, j)][a*co + b] = sum_s l[i][a][s] r[j][b][s]
-    NtGemmParams gp{};
-    gp.A = L;
-    gp.B = R;
-    gp.M = N * co;
-    gp.N = N * co;
-    gp.K = S;
-    gp.scale = 1.f;
-    // element (m = i*co + a, n = j*co + b) -> (i*N + j)*co*co + a*co + b
-    gp.dst = Dst{O, DT_F16, co, (long long)N * co * co, co, co, (long long)co * co, 1};
-    dim3 grid((gp.M + NT_TILE - 1) / NT_TILE, (gp.N + NT_TILE - 1) / NT_TILE);
+    OuterParams op{L, R, O, N, co, S};
+    const int tm = (N * co + OT - 1) / OT;
     LaunchScope ls(ctx, "opm.outer");
-    if ((S & 7) == 0) hipLaunchKernelGGL(nt_gemm_kernel<true>, grid, dim3(256), 0, ctx->stream, gp);
-    else hipLaunchKernelGGL(nt_gemm_kernel<false>, grid, dim3(256), 0, ctx->stream, gp);
+    hipLaunchKernelGGL(opm_outer_kernel, dim3((unsigned)(tm * tm)), dim3(256), 0, ctx->stream, op);
   }
   LF_TRY(check_hip(hipGetLastError(), "opm outer launch"));
   {  // (O W_out + b) / den + residual

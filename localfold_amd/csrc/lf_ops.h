@@ -26,7 +26,7 @@ size_t expanded_bytes(const WView& v);
 int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
                   int count, _Float16* dst, int kp, const char* label);
 // dst = (f16) src over n elements; tq > 0 transposes every [tq][tq] plane.
-int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq);
+int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale = 1.f);
 
 inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == LF_BF16; }
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }
