@@ -58,6 +58,23 @@ def cpu_baseline(c2, budget_s=30.0):
             "sample": sample + f"; numpy oracle, {secs:.1f} s per step", "ms_per_step": round(secs * 1e3, 1)}
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tri_mult_config2_kernel_stats.md")
+TRAFFIC_KERNELS = {"project": ["tri_project_resident_kernel<2>"], "output": ["tri_output_resident_kernel<2>"],
+                   "contract": ["tri_contract_kernel<false, true>", "tri_contract_kernel<true, true>"]}
+
+
+def measured_traffic(kind):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (scaled by the copy-kernel calibration recorded in the same file)."""
+    try:
+        line = next(l for l in open(TRAFFIC_FILE) if l.startswith("traffic_json: "))
+        table = json.loads(line[len("traffic_json: "):])["kernels"]
+        vals = [table[k]["traffic_bytes"] for k in TRAFFIC_KERNELS.get(kind, []) if k in table]
+        return int(sum(vals) / len(vals)) if vals else None
+    except (OSError, StopIteration, ValueError, KeyError):
+        return None
+
+
 def tri_attention_flops(n, c=128, heads=4, d=32):
     """One triangle-attention direction: q/k/v/gate + bias projections, QK^T and PV, output."""
     p = n * n
@@ -245,7 +262,7 @@ def main():
     roof["kernel"] = f"tri_*.{dom}"
     roof["ms_per_launch"] = round(dom_ms, 4)
     roof["mfma_tflops"] = round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2)
-    roof["traffic"] = None
+    roof["traffic"] = measured_traffic(dom)
 
     extras = {}
     if not args.no_extras:
