@@ -500,6 +500,27 @@ __device__ __forceinline__ void frag_ln_raw2(FragTile<ACT, KS>& t0, FragTile<ACT
   }
 }
 
+// LayerNorm of one raw tile into MFMA fragments (frag_ln_raw2 for a single tile).
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_ln_raw1(FragTile<ACT, KS>& t0, h8 (&a0)[KS], int C, const float* gamma,
+                                             const float* beta, float eps, bool fast_var, int lane) {
+  const int g = lane >> 4;
+  float m0, i0;
+  frag_stats_raw(t0, C, eps, fast_var, m0, i0);
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+    const float4 g0 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g);
+    const float4 g1 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g + 4);
+    const float4 b0 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g);
+    const float4 b1 = *reinterpret_cast<const float4*>(beta + 32 * j + 8 * g + 4);
+    const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a0[j][e] = (_Float16)((t0.get(j, e) - m0) * i0 * gg[e] + bb[e]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Raw tile -> float values (zero past C).
 template <int ACT, int KS>
 __device__ __forceinline__ void frag_values(const FragTile<ACT, KS>& t, float (&x)[KS][8], int C, int lane) {

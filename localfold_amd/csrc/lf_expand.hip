@@ -13,15 +13,17 @@ __global__ __launch_bounds__(256) void expand_weights_kernel(ExpandBatch b) {
   if (m >= b.count) return;
   const WView& v = b.v[m];
   const int kp = b.kp[m], W = b.W[m], off = b.off[m];
+  const float sc = b.scale[m];
   const long total = (long)b.ncols[m] * kp;
   for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
     const int n = (int)(e / kp), k = (int)(e - (long)n * kp);
     const long row = (long)(n / W) * 64 + off + n % W;
-    b.dst[m][row * kp + k] = (_Float16)wdecode(v, k, n);
+    b.dst[m][row * kp + k] = (_Float16)(sc * wdecode(v, k, n));
   }
 }
 
-int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label) {
+int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label,
+                   const float* scales) {
   for (int base = 0; base < count; base += 8) {
     ExpandBatch b{};
     b.count = std::min(8, count - base);
@@ -33,6 +35,7 @@ int expand_weights(lf_context* ctx, const WView* views, int count, void* const* 
       b.dst[i] = static_cast<_Float16*>(dst[base + i]);
       b.W[i] = std::max(v.N, 1);
       b.off[i] = 0;
+      b.scale[i] = scales ? scales[base + i] : 1.f;
       b.ncols[i] = v.N;
       out[base + i] = WExp{b.dst[i], b.kp[i], v.N};
       most = std::max(most, (long)v.N * b.kp[i]);
@@ -58,6 +61,7 @@ int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* 
       b.dst[i] = dst + row0[m] * kp;
       b.W[i] = W[m];
       b.off[i] = off[m];
+      b.scale[i] = 1.f;
       b.ncols[i] = (views[m].N + W[m] - 1) / W[m] * W[m];
       most = std::max(most, (long)b.ncols[i] * kp);
     }

@@ -29,6 +29,7 @@ struct ExpandBatch {
   _Float16* dst[8];
   int kp[8];
   int W[8], off[8], ncols[8];
+  float scale[8];   // multiplies the decoded value before the f16 rounding
   int count;
 };
 

@@ -19,7 +19,9 @@ int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, in
               int col_stride = 1, bool subset = false);
 
 // Decodes `count` weight views into f16 E[n][k] tiles at dst[i] (expanded_bytes(views[i]) each).
-int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label);
+// scales (nullable): per-matrix factor applied to the decoded values before the f16 rounding
+int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label,
+                   const float* scales = nullptr);
 size_t expanded_bytes(const WView& v);
 // Decodes views[m] into the chunk layout of a packed buffer: column n -> row
 // row0[m] + (n / W[m]) * 64 + off[m] + n % W[m], pitch kp, padding columns zeroed.

@@ -327,7 +327,41 @@ __global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) 
 // Weight-resident persistent kernels (c_z <= 128 and c_hidden <= 128)
 // ---------------------------------------------------------------------------------------
 
-constexpr int RS_LD = 136;  // 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
+constexpr int RS_LD = 136;
+
+// Four consecutive activations at element index idx (8-/16-byte aligned).
+template <int ACT>
+__device__ __forceinline__ void ld4v(const void* base, size_t idx, float (&v)[4]) {
+  if constexpr (ACT == DT_F32) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else if constexpr (ACT == DT_F16) {
+    const h4 q = *reinterpret_cast<const h4*>(static_cast<const _Float16*>(base) + idx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)q[i];
+  } else {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
+    v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
+  }
+}
+
+template <int ACT>
+__device__ __forceinline__ void st4v(void* base, size_t idx, const float (&v)[4]) {
+  if constexpr (ACT == DT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (ACT == DT_F16) {
+    h4 q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = (_Float16)v[i];
+    *reinterpret_cast<h4*>(static_cast<_Float16*>(base) + idx) = q;
+  } else {
+    uint2 q;
+    q.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+    q.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + idx) = q;
+  }
+}  // 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
 
 __device__ __forceinline__ void stage_resident(_Float16* W, const WExp& e, int tid, int nthreads) {
   const int segs = e.kp >> 3;
@@ -576,9 +610,328 @@ __global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParam
   }
 }
 
+// Project kernel for c_z = c_hidden = 128 (every AF2/AF3 pair width at production size).
+// Weights stay resident in LDS as before; each wave now carries two 16-row tiles, so every
+// weight fragment read from LDS feeds two MFMAs.  The biases are the MFMA accumulators'
+// initial values and the gate weights/biases arrive pre-multiplied by -log2(e), so a gate
+// is rcp(1 + exp2(acc)).  A wave walks tiles w, w + nw, w + 2nw, ... two at a time; when its
+// count is odd the last step runs the first tile's MFMAs only.
+constexpr float TRI_NLOG2E = -1.4426950408889634f;
+// waves per block and 16-row tiles per wave of the 128-wide project / output kernels
+#ifndef TRI_P_NWV
+#define TRI_P_NWV 12
+#endif
+#ifndef TRI_P_TPW
+#define TRI_P_TPW 1
+#endif
+#ifndef TRI_O_NWV
+#define TRI_O_NWV 8
+#endif
+#ifndef TRI_O_TPW
+#define TRI_O_TPW 1
+#endif
+
+template <int ACT>
+__device__ __forceinline__ void tri_tile_load(FragTile<ACT, 4>& t, float (&m)[4], const TriProjectParams& p, int tile,
+                                              int lane) {
+  const int r0 = tile * 16, nv = min(16, p.P - r0), r16 = lane & 15, q4 = (lane >> 4) * 4;
+  frag_load_row(t, p.z, (size_t)(r0 + (r16 < nv ? r16 : 0)), 128, lane);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m[i] = q4 + i < nv ? p.mask[r0 + q4 + i] : 0.f;
+}
+
+template <int ACT, int NWV, int TPW>
+__global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectParams p) {
+  constexpr int NT = 64 * NWV;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate', b-proj, b-gate' [h][k]
+  __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
+  __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  stage_resident(Ws, p.wp[0], tid, NT);
+  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, NT);
+  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, NT);
+  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, NT);
+  for (int i = tid; i < 128; i += NT) {
+    Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
+    Bs[128 + i] = p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f;
+    Bs[256 + i] = p.bp[1] ? p.bp[1][i] : 0.f;
+    Bs[384 + i] = p.bg[1] ? TRI_NLOG2E * p.bg[1][i] : 0.f;
+  }
+  stage_vec(Gs, p.ln_s, 128, 1.f, 128, tid, NT);
+  stage_vec(Gs + 128, p.ln_o, 128, 0.f, 128, tid, NT);
+
+  const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
+  const int ntiles = (p.P + 15) >> 4, nw = gridDim.x * NWV;
+  const bool vec_store = (p.P & 3) == 0;
+  int tile = blockIdx.x * NWV + wave;
+  FragTile<ACT, 4> t[TPW];
+  float mk[TPW][4];
+  if (tile < ntiles) {
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) tri_tile_load(t[tt], mk[tt], p, tile + tt * nw < ntiles ? tile + tt * nw : tile, lane);
+  }
+  __syncthreads();
+
+  for (; tile < ntiles; tile += TPW * nw) {
+    bool valid[TPW];
+    int row0[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      valid[tt] = tile + tt * nw < ntiles;   // wave-uniform
+      row0[tt] = (valid[tt] ? tile + tt * nw : tile) * 16;
+    }
+    h8 xa[TPW][4];
+    if constexpr (TPW == 2) frag_ln_raw2(t[0], t[1], xa[0], xa[1], 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    else frag_ln_raw1(t[0], xa[0], 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    float m[TPW][4];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m[tt][i] = mk[tt][i];
+    // loads of the next tiles are issued before this step's stores (one in-order counter)
+    const int nt = tile + TPW * nw;
+    if (nt < ntiles) {
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) tri_tile_load(t[tt], mk[tt], p, nt + tt * nw < ntiles ? nt + tt * nw : nt, lane);
+    }
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+      const int which = pass >> 1, hh = (pass & 1) * 64;
+      const _Float16* Wp = Ws + (which * 2) * 128 * RS_LD;
+      const _Float16* Wg = Wp + 128 * RS_LD;
+      const float* bp = Bs + which * 256 + hh;
+      const float* bg = bp + 128;
+      f4 acc[TPW][8];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const float b0 = bp[t4 * 16 + r16], b1 = bg[t4 * 16 + r16];
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+          acc[tt][t4] = f4{b0, b0, b0, b0};
+          acc[tt][4 + t4] = f4{b1, b1, b1, b1};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h8 wb[8];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          wb[t4] = *reinterpret_cast<const h8*>(Wp + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+          wb[4 + t4] = *reinterpret_cast<const h8*>(Wg + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+        }
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+          if (tt > 0 && !valid[tt]) break;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[tt][u] = mfma16(xa[tt][j], wb[u], acc[tt][u]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
+      }
+      _Float16* dst = which ? p.out[1] : p.out[0];
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) {
+        if (tt > 0 && !valid[tt]) break;
+        const int nvalid = min(16, p.P - row0[tt]);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const int h = hh + t4 * 16 + r16;
+          h4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            o[i] = (_Float16)(m[tt][i] * acc[tt][t4][i] *
+                              __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(acc[tt][4 + t4][i])));
+          _Float16* d = dst + (size_t)h * p.P + row0[tt] + q4;
+          if (vec_store && q4 + 4 <= nvalid) {
+            *reinterpret_cast<h4*>(d) = o;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (q4 + i < nvalid) d[i] = o[i];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Output kernel for c_z = c_hidden = 128.  Each wave handles two 16-pair tiles (tiles w + k*nw
+// two at a time, as in the project kernel): X rows are transposed through a per-wave LDS
+// patch into the B-fragment layout, LN_out(X) and LN_in(z) stay in registers, and the
+// weights (A operand, resident in LDS) meet both tiles per fragment read.  With the weights as
+// the A operand a lane holds four consecutive channels of one pair, so the residual read and
+// the output write are 4-element vectors straight from the accumulators.  The gate weights
+// and bias arrive pre-multiplied by -log2(e): sigmoid = rcp(1 + exp2(acc)).
+constexpr int O2_LD = 136;
+
+template <int ACT>
+__device__ __forceinline__ void x_transpose(_Float16* Xw, const _Float16* X, int P, int row0, int nvalid, int lane,
+                                            bool vec) {
+  // Xw[r][h] = X[h][row0 + r] for r < 16 (rows past the end zero)
+  if (vec && nvalid == 16) {
+    h8 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+      xv[j] = *reinterpret_cast<const h8*>(X + (size_t)h * P + row0 + seg * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) Xw[(seg * 8 + jj) * O2_LD + h] = xv[j][jj];
+    }
+  } else {
+#pragma unroll 1
+    for (int idx = lane; idx < 128 * 16; idx += 64) {
+      const int h = idx >> 4, r = idx & 15;
+      const _Float16 v = X[(size_t)h * P + row0 + (r < nvalid ? r : 0)];
+      Xw[r * O2_LD + h] = r < nvalid ? v : (_Float16)0.f;
+    }
+  }
+}
+
+template <int ACT, int NWV, int TPW>
+__global__ __launch_bounds__(64 * NWV) void tri_output_v2_kernel(TriOutputParams p) {
+  constexpr int NT = 64 * NWV;
+  __shared__ __attribute__((aligned(16))) _Float16 Wz[128 * RS_LD];   // [c][h]
+  __shared__ __attribute__((aligned(16))) _Float16 Wg[128 * RS_LD];   // [c][k], pre-scaled
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][16 * TPW * O2_LD];
+  __shared__ __attribute__((aligned(16))) float Vs[6 * 128];         // bz, bg', centre-norm s/o, LN_in s/o
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  stage_resident(Wz, p.wz, tid, NT);
+  stage_resident(Wg, p.wg, tid, NT);
+  for (int i = tid; i < 128; i += NT) {
+    Vs[i] = p.bz ? p.bz[i] : 0.f;
+    Vs[128 + i] = p.bg ? TRI_NLOG2E * p.bg[i] : 0.f;
+  }
+  stage_vec(Vs + 256, p.ln_out_s, 128, 1.f, 128, tid, NT);
+  stage_vec(Vs + 384, p.ln_out_o, 128, 0.f, 128, tid, NT);
+  stage_vec(Vs + 512, p.ln_in_s, 128, 1.f, 128, tid, NT);
+  stage_vec(Vs + 640, p.ln_in_o, 128, 0.f, 128, tid, NT);
+  __syncthreads();
+
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+  const int ntiles = (p.P + 15) >> 4, nw = gridDim.x * NWV;
+  const bool vec_x = (p.P & 7) == 0;
+  _Float16* Xw = Xs[wave];
+  for (int tile = blockIdx.x * NWV + wave; tile < ntiles; tile += TPW * nw) {
+    bool valid[TPW];
+    int row0[TPW], nval[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      valid[tt] = tile + tt * nw < ntiles;   // wave-uniform
+      row0[tt] = (valid[tt] ? tile + tt * nw : tile) * 16;
+      nval[tt] = min(16, p.P - row0[tt]);
+    }
+    // z rows (LN_in) and the transposed X rows (LN_out)
+    FragTile<ACT, 4> z[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      frag_load(z[tt], p.z, (size_t)row0[tt], nval[tt], 128, lane);
+      x_transpose<ACT>(Xw + tt * 16 * O2_LD, p.X, p.P, row0[tt], nval[tt], lane, vec_x);
+    }
+    h8 ax[TPW][4], az[TPW][4];
+    {
+      FragTile<DT_F16, 4> x[TPW];
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[tt].raw[j][0] = *reinterpret_cast<const uint4*>(Xw + (tt * 16 + r16) * O2_LD + 32 * j + kq);
+      if constexpr (TPW == 2) {
+        frag_ln_raw2(x[0], x[1], ax[0], ax[1], 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
+      } else {
+        frag_ln_raw1(x[0], ax[0], 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
+      }
+    }
+    if constexpr (TPW == 2) frag_ln_raw2(z[0], z[1], az[0], az[1], 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+    else frag_ln_raw1(z[0], az[0], 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      const int c0 = pass * 64;
+      f4 accz[TPW][4], accg[TPW][4];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const float4 bz = *reinterpret_cast<const float4*>(Vs + c0 + t4 * 16 + 4 * g4);
+        const float4 bg = *reinterpret_cast<const float4*>(Vs + 128 + c0 + t4 * 16 + 4 * g4);
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+          accz[tt][t4] = f4{bz.x, bz.y, bz.z, bz.w};
+          accg[tt][t4] = f4{bg.x, bg.y, bg.z, bg.w};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h8 wz[4], wg[4];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          wz[t4] = *reinterpret_cast<const h8*>(Wz + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+          wg[t4] = *reinterpret_cast<const h8*>(Wg + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+        }
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+          if (tt > 0 && !valid[tt]) break;
+#pragma unroll
+          for (int t4 = 0; t4 < 4; ++t4) {
+            accz[tt][t4] = mfma16(wz[t4], ax[tt][j], accz[tt][t4]);
+            accg[tt][t4] = mfma16(wg[t4], az[tt][j], accg[tt][t4]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
+      }
+      // stage the pass's update (pairs x 64 channels, f32) in this wave's X patch (its X
+      // fragments are in registers), then write whole 128-byte half-rows: lane -> (pair, 8
+      // channels), the residual read the same way
+      float* Us = reinterpret_cast<float*>(Xw);   // [16*TPW pairs][68] f32 (pitch 68: no bank conflicts)
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) {
+        if (tt > 0 && !valid[tt]) break;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          float4 v;
+          v.x = accz[tt][t4][0] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][0]));
+          v.y = accz[tt][t4][1] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][1]));
+          v.z = accz[tt][t4][2] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][2]));
+          v.w = accz[tt][t4][3] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][3]));
+          *reinterpret_cast<float4*>(Us + (tt * 16 + r16) * 68 + t4 * 16 + 4 * g4) = v;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2 * TPW; ++u) {
+        const int pr = u * 8 + (lane >> 3), seg = lane & 7;   // pair slot, 8-channel segment
+        const int tt = pr >> 4, r = pr & 15;
+        if (tt > 0 && !valid[tt]) break;
+        if (r >= nval[tt]) continue;
+        const float4 u0 = *reinterpret_cast<const float4*>(Us + pr * 68 + seg * 8);
+        const float4 u1 = *reinterpret_cast<const float4*>(Us + pr * 68 + seg * 8 + 4);
+        float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        const size_t idx = (size_t)(row0[tt] + r) * 128 + c0 + seg * 8;
+        if (p.accumulate) {
+          float a4[4], b4[4];
+          ld4v<ACT>(p.z, idx, a4);
+          ld4v<ACT>(p.z, idx + 4, b4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] += a4[i];
+            v[4 + i] += b4[i];
+          }
+        }
+        const float lo[4] = {v[0], v[1], v[2], v[3]}, hi[4] = {v[4], v[5], v[6], v[7]};
+        st4v<ACT>(p.out, idx, lo);
+        st4v<ACT>(p.out, idx + 4, hi);
+      }
+    }
+  }
+}
+
 template <int ACT>
 static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool resident, int kz) {
   const int P = pp.P;
+  if (resident && pp.C == 128 && pp.H == 128) {
+    const int tiles = (P + 15) / 16;
+    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_P_NWV - 1) / TRI_P_NWV)));
+    hipLaunchKernelGGL((tri_project_v2_kernel<ACT, TRI_P_NWV, TRI_P_TPW>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
+    return;
+  }
   if (resident) {
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + PR_WAVES - 1) / PR_WAVES)));
@@ -594,6 +947,12 @@ static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool res
 template <int ACT>
 static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resident, int kz, int kh) {
   const int P = op.P;
+  if (resident && op.C == 128 && op.H == 128) {
+    const int tiles = (P + 15) / 16;
+    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_O_NWV - 1) / TRI_O_NWV)));
+    hipLaunchKernelGGL((tri_output_v2_kernel<ACT, TRI_O_NWV, TRI_O_TPW>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
+    return;
+  }
   if (resident) {
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + OR_WAVES - 1) / OR_WAVES)));
@@ -674,8 +1033,12 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   pp.out[1] = static_cast<_Float16*>(bufs[1]);
   _Float16* X = static_cast<_Float16*>(bufs[2]);
   WExp ex[6];
+  // the 128-wide project kernel takes its gate weights pre-multiplied by -log2(e)
+  const bool v2 = C == 128 && H == 128 && N >= 16;
+  const float gate = v2 ? TRI_NLOG2E : 1.f;
+  const float scales[6] = {1.f, gate, 1.f, gate, 1.f, gate};
   LF_TRY(expand_weights(ctx, views, 6, bufs + 3, ex,
-                        a.direction == LF_OUTGOING ? "tri_out.expand" : "tri_in.expand"));
+                        a.direction == LF_OUTGOING ? "tri_out.expand" : "tri_in.expand", scales));
   pp.wp[0] = ex[0];
   pp.wg[0] = ex[1];
   pp.wp[1] = ex[2];

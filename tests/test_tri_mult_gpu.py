@@ -43,7 +43,8 @@ def test_fixture_incoming_vs_oracle(ctx, name):
     assert m["meanAbsoluteError"] < 1e-3 and m["maxAbsoluteError"] < 1e-2, m
 
 
-@pytest.mark.parametrize("n,cz,ch,seed", [(3, 4, 5, 42), (37, 64, 32, 5), (64, 128, 128, 7), (130, 128, 128, 11)])
+@pytest.mark.parametrize("n,cz,ch,seed", [(3, 4, 5, 42), (37, 64, 32, 5), (37, 128, 128, 3), (64, 128, 128, 7),
+                                         (130, 128, 128, 11)])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_deterministic_input(ctx, n, cz, ch, seed, direction):
     inp = S.deterministic_triangle_input(n, cz, ch, seed)
