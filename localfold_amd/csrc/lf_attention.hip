@@ -17,6 +17,7 @@
 //           the N^2 x heads logits never leave registers
 //   rowgemm o Wo + bo, + residual, stored through the row map
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 #include "lf_rowgemm.h"
@@ -24,11 +25,16 @@
 namespace lf {
 
 constexpr int FA_DP = 32;       // padded head dim (d <= 32)
-constexpr int FA_QPW = 32;      // queries per wave (two 16-query MFMA tiles)
-constexpr int FA_WAVES = 4;
-constexpr int FA_QPB = FA_QPW * FA_WAVES;
+constexpr int FA_QPB = 128;          // queries per block (8 / QT waves of QT 16-query tiles)
+#ifndef FA_QT_BIAS
+#define FA_QT_BIAS 1                 // query tiles per wave with a pair bias
+#endif
+#ifndef FA_QT_PLAIN
+#define FA_QT_PLAIN 1                // ... and without
+#endif
 constexpr int FA_KC = 64;       // keys per chunk
 constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
+
 
 struct FlashParams {
   const _Float16 *q, *k, *vt, *g;
@@ -57,16 +63,17 @@ __global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* 
 // Pair-bias values of one lane for one key chunk: queries of the lane's two tiles (rows
 // brow[qt], already offset by 4*g4), keys k0 + 16kt + 4g4 .. +3.  Full chunks with Q % 4 == 0
 // load 8-byte pieces at constant offsets; the last (partial) chunk clamps element-wise.
-__device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[2], int Q, int k0, int g4, bool full,
-                                           h4 (&bv)[2][4]) {
+template <int QT>
+__device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], int Q, int k0, int g4, bool full,
+                                           h4 (&bv)[QT][4]) {
   if (full) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) bv[qt][kt] = *reinterpret_cast<const h4*>(brow[qt] + k0 + kt * 16);
   } else {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -77,8 +84,18 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[2], int
   }
 }
 
-template <bool BIAS>
-__global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
+// One block: 128 queries of one (batch row, head); each wave owns QT 16-query tiles.  Key
+// chunks of 64 are staged in double-buffered LDS two chunks ahead (K rows, V^T rows, key
+// bias); the pair-bias values a lane needs come straight from global memory, also ahead.
+//
+// Online softmax with a lazy running max: after the first chunk, the S accumulators start at
+// bias - m (m = the query's running max), so the MFMA yields x - m directly; when no query's
+// maximum rose (a wave-uniform vote) p = exp2(x - m) needs no subtraction and O no rescale,
+// which is exactly the standard update with an unchanged max.  Otherwise (and in the first
+// chunk, and in chunks holding masked or past-the-end keys) the general update runs.  The
+// row sums come from the PV MFMAs themselves, through an all-ones operand (third d tile).
+template <bool BIAS, int QT>
+__global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_KC * FA_KLD];
   __shared__ __attribute__((aligned(16))) _Float16 Vs[2][FA_DP * FA_VLD];
   __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
@@ -104,23 +121,24 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
   const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * p.Q : nullptr;
 
   // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
-  int qidx[2], qc[2];
-  h8 qf[2];
+  int qidx[QT], qc[QT];
+  h8 qf[QT];
+  const _Float16* brow[QT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    qidx[qt] = qb * FA_QPB + wave * FA_QPW + qt * 16 + r16;
+  for (int qt = 0; qt < QT; ++qt) {
+    qidx[qt] = qb * FA_QPB + (wave * QT + qt) * 16 + r16;
     qc[qt] = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
     qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc[qt] * FA_DP + kq);
+    brow[qt] = BIAS ? bias + (size_t)qc[qt] * p.Q + 4 * g4 : nullptr;
   }
-  const _Float16* brow[2];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) brow[qt] = BIAS ? bias + (size_t)qc[qt] * p.Q + 4 * g4 : nullptr;
   const bool bias_vec = (p.Q & 3) == 0;
+  const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
 
   const int nkc = (p.Q + FA_KC - 1) / FA_KC;
   const bool vecv = (p.Q & 7) == 0;
-  // stage chunk c: K rows [64][32] (one 16-byte piece per thread), V^T rows [32][64], key bias
-  auto kv_load = [&](int c, uint4& kr, uint4& vr, float& kbr) {
+  // stage chunk c: K rows [64][32] (one 16-byte piece per thread of the first 256), V^T rows
+  // [32][64], key bias
+  auto kv_load = [&](int c, uint4& kr, uint4& vr, float& kbr) __attribute__((always_inline)) {
     const int k0 = c * FA_KC;
     {
       const int key = tid >> 2, seg = tid & 3, kk = k0 + key;
@@ -148,7 +166,7 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
       kbr = kk < p.Q ? kbb[kk] : -1e30f;   // keys past Q never contribute
     }
   };
-  auto kv_store = [&](int buf, const uint4& kr, const uint4& vr, float kbr) {
+  auto kv_store = [&](int buf, const uint4& kr, const uint4& vr, float kbr) __attribute__((always_inline)) {
     {
       const int key = tid >> 2, seg = tid & 3;
       *reinterpret_cast<uint4*>(&Ks[buf][key * FA_KLD + seg * 8]) = kr;
@@ -164,124 +182,169 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashParams p) {
     }
   };
 
-  uint4 kr, vr;
-  float kbr;
-  kv_load(0, kr, vr, kbr);
-  h4 bcur[2][4], bnext[2][4];
-  if (BIAS) bias_fetch(brow, p.Q, 0, g4, bias_vec && FA_KC <= p.Q, bcur);
-  kv_store(0, kr, vr, kbr);
+  // loads run two chunks ahead (register set c % 2); chunk c + 1 is written to LDS at the end
+  // of chunk c, into the buffer chunk c - 1 used (every wave passed that chunk's barrier)
+  const bool stager = tid < 256;
+  // two named register sets (set c % 2), chosen with if constexpr so none is ever indexed
+  uint4 kr0, vr0, kr1, vr1;
+  float kb0 = 0.f, kb1 = 0.f;
+  h4 bq0[QT][4], bq1[QT][4];   // bias of chunk c in set c % 2; chunk c + 2's is fetched once c's is used
+  if (stager) {
+    kv_load(0, kr0, vr0, kb0);
+    if (nkc > 1) kv_load(1, kr1, vr1, kb1);
+  }
+  if (BIAS) {
+    bias_fetch<QT>(brow, p.Q, 0, g4, bias_vec && FA_KC <= p.Q, bq0);
+    if (nkc > 1) bias_fetch<QT>(brow, p.Q, FA_KC, g4, bias_vec && 2 * FA_KC <= p.Q, bq1);
+  }
+  if (stager) kv_store(0, kr0, vr0, kb0);
   __syncthreads();
 
-  float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
-  f4 o[2][2];   // [dt][qt]: O^T[dt*16 + 4*g4 + i][query]
+  float m_run[QT];
+  f4 o[3][QT];   // [dt][qt]: O^T[dt*16 + 4*g4 + i][query]; dt = 2: the row sums
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -1e30f;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < 3; ++dt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
+  }
 
-  for (int c = 0; c < nkc; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nkc) {
-      kv_load(c + 1, kr, vr, kbr);
-      if (BIAS) bias_fetch(brow, p.Q, (c + 1) * FA_KC, g4, bias_vec && (c + 2) * FA_KC <= p.Q, bnext);
-    }
-    // S^T tiles
-    f4 s[2][4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
-    }
-    const bool masked = Kmasked[buf] != 0;   // wave-uniform
-    _Float16 pv[2][4][4];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float mx = -1e30f;
-      if (!masked) {
-        // no masked key in the chunk: the logit is q.k + bias (|x| far below the clamp)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x = BIAS ? (float)bcur[qt][kt][i] + s[qt][kt][i] : s[qt][kt][i];
-            s[qt][kt][i] = x;
-            mx = fmaxf(mx, x);
-          }
-      } else {
+  // one chunk; RS = c % 2 is a compile-time constant so every register-set index is static
+  auto chunk = [&](int c, auto rs_tag) __attribute__((always_inline)) {
+      constexpr int rs = decltype(rs_tag)::value;
+      const int buf = rs;
+      h4 (&bq)[QT][4] = rs == 0 ? bq0 : bq1;
+      if (c + 2 < nkc && stager) {
+        if constexpr (rs == 0) kv_load(c + 2, kr0, vr0, kb0);
+        else kv_load(c + 2, kr1, vr1, kb1);
+      }
+      const bool general = c == 0 || Kmasked[buf] != 0;   // wave-uniform
+      _Float16 pv[QT][4][4];
+      if (general) {
+        f4 s[QT][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
-          const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+          const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x = s[qt][kt][i] + kbv[i];
-            if (BIAS) x += (float)bcur[qt][kt][i];
-            // clamp (keys past Q carry -1e30 and stay below every real logit)
-            x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -FA_CLAMP), FA_CLAMP);
-            s[qt][kt][i] = x;
-            mx = fmaxf(mx, x);
+          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
+        }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float mx = -1e30f;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
+            const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float x = s[qt][kt][i] + kbv[i];
+              if (BIAS) x += (float)bq[qt][kt][i];
+              // clamp (keys past Q carry -1e30 and stay below every real logit)
+              x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -FA_CLAMP), FA_CLAMP);
+              s[qt][kt][i] = x;
+              mx = fmaxf(mx, x);
+            }
+          }
+          mx = lanes4_max(mx);
+          const float m_new = fmaxf(m_run[qt], mx);
+          const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[qt][kt][i] = (_Float16)__builtin_amdgcn_exp2f(s[qt][kt][i] - m_new);
+          m_run[qt] = m_new;
+#pragma unroll
+          for (int dt = 0; dt < 3; ++dt) o[dt][qt] = o[dt][qt] * corr;
+        }
+      } else {
+        // S accumulators start at bias - m, so the MFMA yields x - m
+        f4 s[QT][4];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[qt][kt][i] = BIAS ? (float)bq[qt][kt][i] - m_run[qt] : -m_run[qt];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], s[qt][kt]);
+        }
+        float mx[QT];
+        bool rose = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float v = -1e30f;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v = fmaxf(v, s[qt][kt][i]);
+          mx[qt] = v;
+          rose |= v > 0.f;
+        }
+        if (!__any(rose)) {
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pv[qt][kt][i] = (_Float16)__builtin_amdgcn_exp2f(s[qt][kt][i]);
+        } else {
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            const float d = fmaxf(lanes4_max(mx[qt]), 0.f);   // rise of this query's max
+            const float corr = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pv[qt][kt][i] = (_Float16)__builtin_amdgcn_exp2f(s[qt][kt][i] - d);
+            m_run[qt] += d;
+#pragma unroll
+            for (int dt = 0; dt < 3; ++dt) o[dt][qt] = o[dt][qt] * corr;
           }
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-      const float m_new = fmaxf(m_run[qt], mx);
-      const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-      float sum = 0.f;
+      // this chunk's bias values are consumed: fetch chunk c + 2's into the slot
+      if (BIAS && c + 2 < nkc) bias_fetch<QT>(brow, p.Q, (c + 2) * FA_KC, g4, bias_vec && (c + 3) * FA_KC <= p.Q, bq);
+      // O^T += V^T P^T over two 32-key halves; the ones operand accumulates the row sums
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kh2 = 0; kh2 < 2; ++kh2) {
+        h8 vf[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(s[qt][kt][i] - m_new);
-          sum += e;
-          pv[qt][kt][i] = (_Float16)e;
+        for (int dt = 0; dt < 2; ++dt) {
+          const _Float16* vrow = &Vs[buf][(dt * 16 + r16) * FA_VLD];
+          const h4 lo = *reinterpret_cast<const h4*>(vrow + (2 * kh2) * 16 + 4 * g4);
+          const h4 hi = *reinterpret_cast<const h4*>(vrow + (2 * kh2 + 1) * 16 + 4 * g4);
+          vf[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-      sum += __shfl_xor(sum, 16, WAVE);
-      sum += __shfl_xor(sum, 32, WAVE);
-      l_run[qt] = l_run[qt] * corr + sum;
-      m_run[qt] = m_new;
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) o[dt][qt] = o[dt][qt] * corr;
-    }
-    // O^T += V^T P^T over two 32-key halves
+        for (int qt = 0; qt < QT; ++qt) {
+          const h8 pf = h8{pv[qt][2 * kh2][0], pv[qt][2 * kh2][1], pv[qt][2 * kh2][2], pv[qt][2 * kh2][3],
+                           pv[qt][2 * kh2 + 1][0], pv[qt][2 * kh2 + 1][1], pv[qt][2 * kh2 + 1][2],
+                           pv[qt][2 * kh2 + 1][3]};
 #pragma unroll
-    for (int kh2 = 0; kh2 < 2; ++kh2) {
-      h8 vf[2];
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const _Float16* vrow = &Vs[buf][(dt * 16 + r16) * FA_VLD];
-        const h4 lo = *reinterpret_cast<const h4*>(vrow + (2 * kh2) * 16 + 4 * g4);
-        const h4 hi = *reinterpret_cast<const h4*>(vrow + (2 * kh2 + 1) * 16 + 4 * g4);
-        vf[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          for (int dt = 0; dt < 2; ++dt) o[dt][qt] = mfma16(vf[dt], pf, o[dt][qt]);
+          o[2][qt] = mfma16(ones, pf, o[2][qt]);
+        }
       }
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const h8 pf = h8{pv[qt][2 * kh2][0], pv[qt][2 * kh2][1], pv[qt][2 * kh2][2], pv[qt][2 * kh2][3],
-                         pv[qt][2 * kh2 + 1][0], pv[qt][2 * kh2 + 1][1], pv[qt][2 * kh2 + 1][2],
-                         pv[qt][2 * kh2 + 1][3]};
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) o[dt][qt] = mfma16(vf[dt], pf, o[dt][qt]);
+      if (c + 1 < nkc) {
+        if (stager) {
+          if constexpr (rs == 0) kv_store(buf ^ 1, kr1, vr1, kb1);
+          else kv_store(buf ^ 1, kr0, vr0, kb0);
+        }
+        __syncthreads();
       }
-    }
-    if (c + 1 < nkc) {
-      // buffer buf^1 was last read in chunk c-1, which every wave finished before the
-      // barrier that ended it
-      kv_store(buf ^ 1, kr, vr, kbr);
-      if (BIAS) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt) bcur[qt][kt] = bnext[qt][kt];
-      }
-      __syncthreads();
-    }
+  };
+  for (int c0 = 0; c0 < nkc; c0 += 2) {
+    chunk(c0, std::integral_constant<int, 0>{});
+    if (c0 + 1 < nkc) chunk(c0 + 1, std::integral_constant<int, 1>{});
   }
   // o[query][h*d + dd] = O / l * g
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     if (qidx[qt] >= p.Q) continue;
-    const float inv = 1.0f / l_run[qt];
+    const float inv = 1.0f / o[2][qt][0];
     const size_t row = (size_t)b * p.Q + qidx[qt];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -448,8 +511,12 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     fp.nqb = (Q + FA_QPB - 1) / FA_QPB;
     fp.nblocks = (long long)fp.nqb * B * H;
     LaunchScope ls(ctx, "attention.flash");
-    if (fp.bias) hipLaunchKernelGGL(flash_kernel<true>, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
-    else hipLaunchKernelGGL(flash_kernel<false>, dim3((unsigned)fp.nblocks), dim3(256), 0, ctx->stream, fp);
+    if (fp.bias)
+      hipLaunchKernelGGL((flash_kernel<true, FA_QT_BIAS>), dim3((unsigned)fp.nblocks), dim3(512 / FA_QT_BIAS), 0,
+                         ctx->stream, fp);
+    else
+      hipLaunchKernelGGL((flash_kernel<false, FA_QT_PLAIN>), dim3((unsigned)fp.nblocks), dim3(512 / FA_QT_PLAIN), 0,
+                         ctx->stream, fp);
   }
   LF_TRY(check_hip(hipGetLastError(), "flash launch"));
 

@@ -369,10 +369,22 @@ __device__ __forceinline__ void pack8(const float (&v)[8], uint4 (&o)[FragTile<A
   }
 }
 
-__device__ __forceinline__ float lanes4_sum(float v) {   // over lanes l, l^16, l^32, l^48
-  v += __shfl_xor(v, 16, WAVE);
-  v += __shfl_xor(v, 32, WAVE);
-  return v;
+// Reductions over lanes l, l^16, l^32, l^48 with gfx950's VALU lane swaps (no LDS round
+// trip).  With the same register as both operands, v_permlane16_swap pairs row 0 with row 1
+// and row 2 with row 3 (rows of 16 lanes), and v_permlane32_swap the lower half with the
+// upper half: combining the two results gives every lane the pair's reduction.
+__device__ __forceinline__ float lanes4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float lanes4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // LayerNorm of the 16 rows held as values x[j][e] (channel 32j + 8*(lane/16) + e, zero past
