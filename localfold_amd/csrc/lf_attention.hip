@@ -32,6 +32,9 @@ constexpr int FA_QPB = 128;          // queries per block (8 / QT waves of QT 16
 #ifndef FA_QT_PLAIN
 #define FA_QT_PLAIN 1                // ... and without
 #endif
+#ifndef FA_BIASADD
+#define FA_BIASADD 0
+#endif
 constexpr int FA_KC = 64;       // keys per chunk
 constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
 
@@ -52,35 +55,51 @@ struct FlashParams {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float FA_CLAMP = 1e8f * LOG2E;
 
-__global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* kb, int B, int Q, int transpose) {
+// kb[b][k] for k < Qp (keys padded to whole chunks): 1e9 log2(e) (mask - 1), and -1e30 past Q
+__global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* kb, int B, int Q, int Qp,
+                                                      int transpose) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (long long)B * Q) return;
-  const int b = (int)(i / Q), k = (int)(i % Q);
-  const float m = mask[transpose ? (long long)k * B + b : i];
+  if (i >= (long long)B * Qp) return;
+  const int b = (int)(i / Qp), k = (int)(i % Qp);
+  if (k >= Q) {
+    kb[i] = -1e30f;
+    return;
+  }
+  const float m = mask[transpose ? (long long)k * B + b : (long long)b * Q + k];
   kb[i] = (1e9f * LOG2E) * (m - 1.0f);
 }
 
-// Pair-bias values of one lane for one key chunk: queries of the lane's two tiles (rows
-// brow[qt], already offset by 4*g4), keys k0 + 16kt + 4g4 .. +3.  Full chunks with Q % 4 == 0
-// load 8-byte pieces at constant offsets; the last (partial) chunk clamps element-wise.
+// (float)v[i] + c in one instruction (i is a constant once the caller's loop is unrolled)
+__device__ __forceinline__ float bias_add(const h4& v, int i, float c) {
+#if FA_BIASADD == 2
+  return c;
+#endif
+  const uint2 u = __builtin_bit_cast(uint2, v);
+#if FA_BIASADD == 1
+  const uint32_t w1 = i < 2 ? u.x : u.y;
+  float r;
+  if (i & 1) asm("v_cvt_f32_f16_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w1));
+  else asm("v_cvt_f32_f16_e32 %0, %1" : "=v"(r) : "v"(w1));
+  return r + c;
+#endif
+  const uint32_t w = i < 2 ? u.x : u.y;
+  return (i & 1) ? f16_add<1>(w, c) : f16_add<0>(w, c);
+}
+
+// Pair-bias values of one lane for one key chunk: the 16 keys k0 + 16*g4 .. +15 of each of the
+// lane's queries (rows brow[qt], already offset by 16*g4), as two aligned 16-byte loads;
+// bv[qt][kt][i] is key k0 + 16*g4 + 4*kt + i.  Bias rows are padded to whole chunks; values
+// past Q are never used.
 template <int QT>
-__device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], int Q, int k0, int g4, bool full,
-                                           h4 (&bv)[QT][4]) {
-  if (full) {
+__device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], int k0, h4 (&bv)[QT][4]) {
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) bv[qt][kt] = *reinterpret_cast<const h4*>(brow[qt] + k0 + kt * 16);
-  } else {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kk = k0 + kt * 16 + 4 * g4 + i;   // keys >= Q are discarded via the key bias
-          bv[qt][kt][i] = brow[qt][(kk < Q ? kk : 0) - 4 * g4];
-        }
+  for (int qt = 0; qt < QT; ++qt) {
+    const h8 lo = *reinterpret_cast<const h8*>(brow[qt] + k0);
+    const h8 hi = *reinterpret_cast<const h8*>(brow[qt] + k0 + 8);
+    bv[qt][0] = h4{lo[0], lo[1], lo[2], lo[3]};
+    bv[qt][1] = h4{lo[4], lo[5], lo[6], lo[7]};
+    bv[qt][2] = h4{hi[0], hi[1], hi[2], hi[3]};
+    bv[qt][3] = h4{hi[4], hi[5], hi[6], hi[7]};
   }
 }
 
@@ -94,10 +113,14 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], in
 // which is exactly the standard update with an unchanged max.  Otherwise (and in the first
 // chunk, and in chunks holding masked or past-the-end keys) the general update runs.  The
 // row sums come from the PV MFMAs themselves, through an all-ones operand (third d tile).
+//
+// Key order within a chunk: row 4*g + i of S^T tile kt is key 16*g + 4*kt + i (K rows are
+// stored to LDS in that order), so the 16 scores a lane holds per query are the contiguous
+// keys 16*(lane/16) .. +15: its bias, key bias and V^T pieces are single vector loads.
 template <bool BIAS, int QT>
 __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_KC * FA_KLD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vs[2][FA_DP * FA_VLD];
+  // per buffer: K rows [64][FA_KLD], then V^T rows [32][FA_VLD]
+  __shared__ __attribute__((aligned(16))) _Float16 KV[2][FA_KC * FA_KLD + FA_DP * FA_VLD];
   __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
   __shared__ int Kmasked[2];   // chunk has a masked key or a key past Q
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -113,12 +136,14 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   const int b = (int)((lb / p.nqb) % p.B);
   const int h = (int)(lb / ((long long)p.nqb * p.B));
 
+  const int nkc = (p.Q + FA_KC - 1) / FA_KC;
+  const int Qp = nkc * FA_KC;   // keys padded to whole chunks in q, k, v^T, the key bias and bias rows
   const size_t bh = (size_t)b * p.H + h;
-  const _Float16* qh = p.q + bh * p.Q * FA_DP;
-  const _Float16* kh = p.k + bh * p.Q * FA_DP;
-  const _Float16* vh = p.vt + bh * FA_DP * p.Q;
-  const float* kbb = p.kb + (size_t)b * p.Q;
-  const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * p.Q : nullptr;
+  const _Float16* qh = p.q + bh * Qp * FA_DP;
+  const _Float16* kh = p.k + bh * Qp * FA_DP;
+  const _Float16* vh = p.vt + bh * FA_DP * Qp;
+  const float* kbb = p.kb + (size_t)b * Qp;
+  const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * Qp : nullptr;
 
   // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
   int qidx[QT], qc[QT];
@@ -129,75 +154,56 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     qidx[qt] = qb * FA_QPB + (wave * QT + qt) * 16 + r16;
     qc[qt] = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
     qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc[qt] * FA_DP + kq);
-    brow[qt] = BIAS ? bias + (size_t)qc[qt] * p.Q + 4 * g4 : nullptr;
+    brow[qt] = BIAS ? bias + (size_t)qc[qt] * Qp + 16 * g4 : nullptr;
   }
-  const bool bias_vec = (p.Q & 3) == 0;
   const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
 
-  const int nkc = (p.Q + FA_KC - 1) / FA_KC;
-  const bool vecv = (p.Q & 7) == 0;
-  // stage chunk c: K rows [64][32] (one 16-byte piece per thread of the first 256), V^T rows
-  // [32][64], key bias
-  auto kv_load = [&](int c, uint4& kr, uint4& vr, float& kbr) __attribute__((always_inline)) {
-    const int k0 = c * FA_KC;
-    {
-      const int key = tid >> 2, seg = tid & 3, kk = k0 + key;
-      kr = *reinterpret_cast<const uint4*>(kh + (size_t)(kk < p.Q ? kk : 0) * FA_DP + seg * 8);
-    }
-    {
-      const int dd = tid >> 3, seg = tid & 7, kk = k0 + seg * 8;
-      if (vecv) {
-        vr = *reinterpret_cast<const uint4*>(vh + (size_t)dd * p.Q + (kk < p.Q ? kk : 0));
-      } else {
-        uint32_t w[4];
+  // Staging: a chunk is 512 16-byte pieces: piece t < 256 is K row t/4 (dims 8(t%4) .. +8),
+  // piece t >= 256 V^T row (t-256)/8 (keys 8((t-256)%8) .. +8).  Each thread stages NP pieces
+  // and lane l of every wave loads key bias l (wave 0 stores it).  With whole padded chunks
+  // every load is unconditional, so no branch separates a load from its use and the
+  // prefetched chunks stay in flight until they are needed.
+  constexpr int NT = 64 * (8 / QT), NP = 512 / NT;
+  const _Float16* gsrc[NP];
+  int gstep[NP], loff[NP];   // source advance per chunk and LDS offset (elements)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int k1 = kk + 2 * e, k2 = kk + 2 * e + 1;
-          const uint16_t lo = __builtin_bit_cast(uint16_t, vh[(size_t)dd * p.Q + (k1 < p.Q ? k1 : 0)]);
-          const uint16_t hi = __builtin_bit_cast(uint16_t, vh[(size_t)dd * p.Q + (k2 < p.Q ? k2 : 0)]);
-          w[e] = (uint32_t)lo | ((uint32_t)hi << 16);
-        }
-        vr = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    kbr = 0.f;
-    if (tid < FA_KC) {
-      const int kk = k0 + tid;
-      kbr = kk < p.Q ? kbb[kk] : -1e30f;   // keys past Q never contribute
-    }
+  for (int j = 0; j < NP; ++j) {
+    const int t = tid + j * NT, tv = t - 256;
+    const bool isk = t < 256;   // wave-uniform
+    gsrc[j] = isk ? kh + (size_t)(t >> 2) * FA_DP + (t & 3) * 8 : vh + (size_t)(tv >> 3) * Qp + (tv & 7) * 8;
+    gstep[j] = isk ? FA_KC * FA_DP : FA_KC;
+    const int key = t >> 2, krow = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
+    loff[j] = isk ? krow * FA_KLD + (t & 3) * 8 : FA_KC * FA_KLD + (tv >> 3) * FA_VLD + (tv & 7) * 8;
+  }
+  auto kv_load = [&](int c, uint4 (&r)[NP], float& kbr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) r[j] = *reinterpret_cast<const uint4*>(gsrc[j] + (size_t)c * gstep[j]);
+    kbr = kbb[c * FA_KC + lane];
   };
-  auto kv_store = [&](int buf, const uint4& kr, const uint4& vr, float kbr) __attribute__((always_inline)) {
-    {
-      const int key = tid >> 2, seg = tid & 3;
-      *reinterpret_cast<uint4*>(&Ks[buf][key * FA_KLD + seg * 8]) = kr;
-    }
-    {
-      const int dd = tid >> 3, seg = tid & 7;
-      *reinterpret_cast<uint4*>(&Vs[buf][dd * FA_VLD + seg * 8]) = vr;
-    }
+  auto kv_store = [&](int buf, const uint4 (&r)[NP], float kbr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) *reinterpret_cast<uint4*>(&KV[buf][loff[j]]) = r[j];
     if (wave == 0) {
-      Kb[buf][tid] = kbr;
+      Kb[buf][lane] = kbr;
       const bool any = __any(kbr != 0.f);
-      if (tid == 0) Kmasked[buf] = any ? 1 : 0;
+      if (lane == 0) Kmasked[buf] = any ? 1 : 0;
     }
   };
 
-  // loads run two chunks ahead (register set c % 2); chunk c + 1 is written to LDS at the end
-  // of chunk c, into the buffer chunk c - 1 used (every wave passed that chunk's barrier)
-  const bool stager = tid < 256;
-  // two named register sets (set c % 2), chosen with if constexpr so none is ever indexed
-  uint4 kr0, vr0, kr1, vr1;
-  float kb0 = 0.f, kb1 = 0.f;
+  // loads run two chunks ahead (register set c % 2; past the last chunk the last one is
+  // loaded again and never stored); chunk c + 1 is written to LDS at the end of chunk c, into
+  // the buffer chunk c - 1 used (every wave passed that chunk's barrier)
+  uint4 st0[NP], st1[NP];
+  float kb0, kb1;
   h4 bq0[QT][4], bq1[QT][4];   // bias of chunk c in set c % 2; chunk c + 2's is fetched once c's is used
-  if (stager) {
-    kv_load(0, kr0, vr0, kb0);
-    if (nkc > 1) kv_load(1, kr1, vr1, kb1);
-  }
+  const int c1 = nkc > 1 ? 1 : 0;
+  kv_load(0, st0, kb0);
+  kv_load(c1, st1, kb1);
   if (BIAS) {
-    bias_fetch<QT>(brow, p.Q, 0, g4, bias_vec && FA_KC <= p.Q, bq0);
-    if (nkc > 1) bias_fetch<QT>(brow, p.Q, FA_KC, g4, bias_vec && 2 * FA_KC <= p.Q, bq1);
+    bias_fetch<QT>(brow, 0, bq0);
+    bias_fetch<QT>(brow, c1 * FA_KC, bq1);
   }
-  if (stager) kv_store(0, kr0, vr0, kb0);
+  kv_store(0, st0, kb0);
   __syncthreads();
 
   float m_run[QT];
@@ -214,17 +220,16 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       constexpr int rs = decltype(rs_tag)::value;
       const int buf = rs;
       h4 (&bq)[QT][4] = rs == 0 ? bq0 : bq1;
-      if (c + 2 < nkc && stager) {
-        if constexpr (rs == 0) kv_load(c + 2, kr0, vr0, kb0);
-        else kv_load(c + 2, kr1, vr1, kb1);
-      }
+      const int cn = c + 2 < nkc ? c + 2 : nkc - 1;
+      if constexpr (rs == 0) kv_load(cn, st0, kb0);
+      else kv_load(cn, st1, kb1);
       const bool general = c == 0 || Kmasked[buf] != 0;   // wave-uniform
       _Float16 pv[QT][4][4];
       if (general) {
         f4 s[QT][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
+          const h8 kf = *reinterpret_cast<const h8*>(&KV[buf][(kt * 16 + r16) * FA_KLD + kq]);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
         }
@@ -233,12 +238,12 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
           float mx = -1e30f;
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
-            const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][kt * 16 + 4 * g4]);
+            const float4 kb4 = *reinterpret_cast<const float4*>(&Kb[buf][16 * g4 + 4 * kt]);
             const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float x = s[qt][kt][i] + kbv[i];
-              if (BIAS) x += (float)bq[qt][kt][i];
+              if (BIAS) x = bias_add(bq[qt][kt], i, x);
               // clamp (keys past Q carry -1e30 and stay below every real logit)
               x = kbv[i] < -1e29f ? -1e30f : fminf(fmaxf(x, -FA_CLAMP), FA_CLAMP);
               s[qt][kt][i] = x;
@@ -264,10 +269,10 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[qt][kt][i] = BIAS ? (float)bq[qt][kt][i] - m_run[qt] : -m_run[qt];
+            for (int i = 0; i < 4; ++i) s[qt][kt][i] = BIAS ? bias_add(bq[qt][kt], i, -m_run[qt]) : -m_run[qt];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][(kt * 16 + r16) * FA_KLD + kq]);
+          const h8 kf = *reinterpret_cast<const h8*>(&KV[buf][(kt * 16 + r16) * FA_KLD + kq]);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], s[qt][kt]);
         }
@@ -306,18 +311,15 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         }
       }
       // this chunk's bias values are consumed: fetch chunk c + 2's into the slot
-      if (BIAS && c + 2 < nkc) bias_fetch<QT>(brow, p.Q, (c + 2) * FA_KC, g4, bias_vec && (c + 3) * FA_KC <= p.Q, bq);
+      if (BIAS) bias_fetch<QT>(brow, cn * FA_KC, bq);
       // O^T += V^T P^T over two 32-key halves; the ones operand accumulates the row sums
 #pragma unroll
       for (int kh2 = 0; kh2 < 2; ++kh2) {
+        // MFMA k index 8*g4 + j is key 16*g4 + 8*kh2 + j: one 16-byte piece of the V^T row
         h8 vf[2];
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const _Float16* vrow = &Vs[buf][(dt * 16 + r16) * FA_VLD];
-          const h4 lo = *reinterpret_cast<const h4*>(vrow + (2 * kh2) * 16 + 4 * g4);
-          const h4 hi = *reinterpret_cast<const h4*>(vrow + (2 * kh2 + 1) * 16 + 4 * g4);
-          vf[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int dt = 0; dt < 2; ++dt)
+          vf[dt] = *reinterpret_cast<const h8*>(&KV[buf][FA_KC * FA_KLD + (dt * 16 + r16) * FA_VLD + 16 * g4 + 8 * kh2]);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const h8 pf = h8{pv[qt][2 * kh2][0], pv[qt][2 * kh2][1], pv[qt][2 * kh2][2], pv[qt][2 * kh2][3],
@@ -329,10 +331,8 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         }
       }
       if (c + 1 < nkc) {
-        if (stager) {
-          if constexpr (rs == 0) kv_store(buf ^ 1, kr1, vr1, kb1);
-          else kv_store(buf ^ 1, kr0, vr0, kb0);
-        }
+        if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1);
+        else kv_store(buf ^ 1, st0, kb0);
         __syncthreads();
       }
   };
@@ -405,9 +405,11 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     LF_TRY(make_view(w.wb, a.bias_mode == LF_BIAS_SEPARATE ? a.pair_channels : C, H, "pair projectionWeight",
                      &views[nv++]));
 
-  const size_t qkv = (size_t)B * H * Q * FA_DP * sizeof(_Float16);
+  // keys padded to whole 64-key chunks (the flash kernel loads whole chunks)
+  const int Qp = (Q + FA_KC - 1) / FA_KC * FA_KC;
+  const size_t qkv = (size_t)B * H * Qp * FA_DP * sizeof(_Float16);
   const size_t hd = (size_t)rows * HD * sizeof(_Float16);
-  const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Q * sizeof(_Float16);
+  const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Qp * sizeof(_Float16);
   // buffers: q, k, v, g, o, key bias, f16 pair bias, output weights, packed lnproj weights x 2
   void* bufs[9];
 
@@ -451,7 +453,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     pp.ngroups = 5;
   }
 
-  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)rows * sizeof(float), biash, expanded_bytes(views[4]),
+  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)B * Qp * sizeof(float), biash, expanded_bytes(views[4]),
                      std::max(lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb)
                                                                                        : (size_t)0)};
   LF_TRY(workspace(ctx, sizes, bufs, 9));
@@ -461,21 +463,25 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   _Float16* bias16 = (_Float16*)bufs[6];
   WExp wo;
   LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[7], &wo, "attention.expand"));
+  // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
+  // exact 0, which must not meet a non-finite value)
   if (d < FA_DP) {
     for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
+  } else if (Qp != Q) {
+    LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, qkv, ctx->stream), "attention memset"));
   }
-  // f16 bias [h][i][j] from row (i, j); swapped: [h][j][i]
-  const Dst bias_dst = a.swap_bias ? Dst{bias16, DT_F16, Q, 1, Q, 1, (long long)Q * Q, 0}
-                                   : Dst{bias16, DT_F16, Q * Q, 0, 1, 1, (long long)Q * Q, 0};
+  // f16 bias [h][i][j] (row stride Qp) from row (i, j); swapped: [h][j][i]
+  const Dst bias_dst = a.swap_bias ? Dst{bias16, DT_F16, Q, 1, Qp, 1, (long long)Q * Qp, 0}
+                                   : Dst{bias16, DT_F16, Q, Qp, 1, 1, (long long)Q * Qp, 0};
   if (a.bias_mode == LF_BIAS_SEPARATE) {
     pb.g[0].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pb, a.pair_dtype, bufs[8], "attention.pair_bias"));
   }
   {
-    const long long hq = (long long)Q * FA_DP;
+    const long long hq = (long long)Qp * FA_DP;
     pp.g[0].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
     pp.g[1].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    pp.g[2].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Q};
+    pp.g[2].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
     pp.g[3].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
     if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) pp.g[4].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
@@ -484,14 +490,14 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   // 3. key-mask bias, f16 copy of the pair bias
   {
     LaunchScope ls(ctx, "attention.keybias");
-    hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, ctx->stream, a.mask, keyb,
-                       B, Q, a.transpose);
+    hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0, ctx->stream,
+                       a.mask, keyb, B, Q, Qp, a.transpose);
   }
   LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
   // caller-supplied f32 logits are converted (and transposed per head when swapped); the
   // projected biases were written as f16 by lnproj
   if (a.bias_mode == LF_BIAS_LOGITS)
-    LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0, LOG2E));
+    LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0, LOG2E, Q, Qp));
 
   // 4. flash attention
   {

@@ -387,6 +387,18 @@ __device__ __forceinline__ float lanes4_max(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// (float)h + c, with h the f16 in half HI of the dword w, as one mixed-precision FMA
+// (h * 1.0 + c: exact widening, one rounding, the same value as a convert then an add).
+template <int HI>
+__device__ __forceinline__ float f16_add(uint32_t w, float c) {
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(c));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(c));
+  return r;
+}
+
 // LayerNorm of the 16 rows held as values x[j][e] (channel 32j + 8*(lane/16) + e, zero past
 // C) into f16 A fragments.  gamma/beta: 32*KS floats (LDS).  Rows with !ok give zeros.
 template <int KS>

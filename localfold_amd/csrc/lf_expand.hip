@@ -75,22 +75,24 @@ int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* 
 
 // dst = (f16) (scale * src), n elements; with tq > 0 every [tq][tq] plane is transposed.
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* src, _Float16* dst, long long n, int tq,
-                                                         float scale) {
+                                                         float scale, int rowlen, int ld) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     long long s = i;
     if (tq > 0) {
       const long long plane = (long long)tq * tq, pl = i / plane, r = i % plane;
       s = pl * plane + (r % tq) * tq + r / tq;
     }
-    dst[i] = (_Float16)(scale * src[s]);
+    const long long o = ld > 0 ? (i / rowlen) * ld + i % rowlen : i;
+    dst[o] = (_Float16)(scale * src[s]);
   }
 }
 
-int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale) {
+int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale, int rowlen,
+               int ld) {
   LaunchScope ls(ctx, "convert.f16");
   const long long blocks = std::min<long long>((n + 255) / 256, 65536);
   hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)std::max<long long>(blocks, 1)), dim3(256), 0, ctx->stream,
-                     src, dst, n, tq, scale);
+                     src, dst, n, tq, scale, rowlen, ld);
   return check_hip(hipGetLastError(), "f32_to_f16 launch");
 }
 

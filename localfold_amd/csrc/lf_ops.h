@@ -27,8 +27,10 @@ size_t expanded_bytes(const WView& v);
 // row0[m] + (n / W[m]) * 64 + off[m] + n % W[m], pitch kp, padding columns zeroed.
 int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
                   int count, _Float16* dst, int kp, const char* label);
-// dst = (f16) src over n elements; tq > 0 transposes every [tq][tq] plane.
-int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale = 1.f);
+// dst = scale * src as f16; tq > 0 transposes each tq x tq plane; ld > 0 writes rows of rowlen
+// values at a row stride of ld
+int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale = 1.f,
+               int rowlen = 0, int ld = 0);
 
 inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == LF_BF16; }
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }

@@ -60,7 +60,7 @@ def test_msa_column_attention(ctx, blockw, s, n):
     H.assert_close(out, ref, label=f"column {s}x{n}")
 
 
-@pytest.mark.parametrize("n", [24, 37, 70])
+@pytest.mark.parametrize("n", [24, 37, 70, 130])
 @pytest.mark.parametrize("ending", [False, True])
 def test_triangle_attention(ctx, blockw, n, ending):
     from localfold_amd import capi, device as D
