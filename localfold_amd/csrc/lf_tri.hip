@@ -38,6 +38,8 @@ struct TriProjectParams {
   WExp wp[2], wg[2];   // [0] -> a, [1] -> b
   const float *bp[2], *bg[2];
   _Float16* out[2];    // a, b: [H][P]
+  int N;               // length (P = N * N)
+  int kmajor_out;      // store each channel plane transposed: a[h][j][k] for pair (k, j)
 };
 
 struct TriOutputParams {
@@ -631,13 +633,32 @@ constexpr float TRI_NLOG2E = -1.4426950408889634f;
 #define TRI_O_TPW 1
 #endif
 
+// The 16 pairs of a project tile: row r is pair src0 + r * sstride, stored at out0 + r of every
+// channel plane, r < nvalid.  Tile t normally holds pairs 16t .. 16t + 15 in place.  With
+// kmajor_out (the incoming direction) tile t = j * ceil(N/16) + kb holds the pairs (16kb + r, j)
+// and stores them at j * N + 16kb + r: each plane then holds a^T (b^T), so the contraction
+// reads both operands with k contiguous, as in the outgoing direction.
+struct TileGeom {
+  int src0, sstride, out0, nvalid;
+};
+
+__device__ __forceinline__ TileGeom tile_geom(const TriProjectParams& p, int tile) {
+  if (!p.kmajor_out) {
+    const int r0 = tile * 16;
+    return TileGeom{r0, 1, r0, min(16, p.P - r0)};
+  }
+  const int nkb = (p.N + 15) >> 4, j = tile / nkb, kb = tile - j * nkb;
+  return TileGeom{kb * 16 * p.N + j, p.N, j * p.N + kb * 16, min(16, p.N - kb * 16)};
+}
+
 template <int ACT>
 __device__ __forceinline__ void tri_tile_load(FragTile<ACT, 4>& t, float (&m)[4], const TriProjectParams& p, int tile,
                                               int lane) {
-  const int r0 = tile * 16, nv = min(16, p.P - r0), r16 = lane & 15, q4 = (lane >> 4) * 4;
-  frag_load_row(t, p.z, (size_t)(r0 + (r16 < nv ? r16 : 0)), 128, lane);
+  const TileGeom g = tile_geom(p, tile);
+  const int r16 = lane & 15, q4 = (lane >> 4) * 4;
+  frag_load_row(t, p.z, (size_t)g.src0 + (size_t)(r16 < g.nvalid ? r16 : 0) * g.sstride, 128, lane);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) m[i] = q4 + i < nv ? p.mask[r0 + q4 + i] : 0.f;
+  for (int i = 0; i < 4; ++i) m[i] = q4 + i < g.nvalid ? p.mask[g.src0 + (q4 + i) * g.sstride] : 0.f;
 }
 
 template <int ACT, int NWV, int TPW>
@@ -661,8 +682,8 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
   stage_vec(Gs + 128, p.ln_o, 128, 0.f, 128, tid, NT);
 
   const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
-  const int ntiles = (p.P + 15) >> 4, nw = gridDim.x * NWV;
-  const bool vec_store = (p.P & 3) == 0;
+  const int ntiles = p.kmajor_out ? p.N * ((p.N + 15) >> 4) : (p.P + 15) >> 4, nw = gridDim.x * NWV;
+  const bool vec_store = ((p.kmajor_out ? p.N : p.P) & 3) == 0;
   int tile = blockIdx.x * NWV + wave;
   FragTile<ACT, 4> t[TPW];
   float mk[TPW][4];
@@ -674,11 +695,13 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
 
   for (; tile < ntiles; tile += TPW * nw) {
     bool valid[TPW];
-    int row0[TPW];
+    int out0[TPW], nval[TPW];
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
       valid[tt] = tile + tt * nw < ntiles;   // wave-uniform
-      row0[tt] = (valid[tt] ? tile + tt * nw : tile) * 16;
+      const TileGeom g = tile_geom(p, valid[tt] ? tile + tt * nw : tile);
+      out0[tt] = g.out0;
+      nval[tt] = g.nvalid;
     }
     h8 xa[TPW][4];
     if constexpr (TPW == 2) frag_ln_raw2(t[0], t[1], xa[0], xa[1], 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
@@ -731,7 +754,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
 #pragma unroll
       for (int tt = 0; tt < TPW; ++tt) {
         if (tt > 0 && !valid[tt]) break;
-        const int nvalid = min(16, p.P - row0[tt]);
+        const int nvalid = nval[tt];
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) {
           const int h = hh + t4 * 16 + r16;
@@ -740,7 +763,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
           for (int i = 0; i < 4; ++i)
             o[i] = (_Float16)(m[tt][i] * acc[tt][t4][i] *
                               __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(acc[tt][4 + t4][i])));
-          _Float16* d = dst + (size_t)h * p.P + row0[tt] + q4;
+          _Float16* d = dst + (size_t)h * p.P + out0[tt] + q4;
           if (vec_store && q4 + 4 <= nvalid) {
             *reinterpret_cast<h4*>(d) = o;
           } else {
@@ -998,6 +1021,7 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   pp.ln_o = w.ln_in_offset;
   pp.eps = a.epsilon;
   pp.P = P;
+  pp.N = N;
   pp.C = C;
   pp.H = H;
   TriOutputParams op{};
@@ -1035,6 +1059,8 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   WExp ex[6];
   // the 128-wide project kernel takes its gate weights pre-multiplied by -log2(e)
   const bool v2 = C == 128 && H == 128 && N >= 16;
+  // incoming: the 128-wide project kernel stores a and b transposed per channel
+  pp.kmajor_out = v2 && a.direction != LF_OUTGOING;
   const float gate = v2 ? TRI_NLOG2E : 1.f;
   const float scales[6] = {1.f, gate, 1.f, gate, 1.f, gate};
   LF_TRY(expand_weights(ctx, views, 6, bufs + 3, ex,
@@ -1071,7 +1097,7 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
     const int tm = (N + CT_TILE - 1) / CT_TILE;
     dim3 grid((unsigned)(tm * tm * H));
     const bool vec = (N % 8) == 0;
-    if (outgoing) {
+    if (outgoing || pp.kmajor_out) {
       if (vec) hipLaunchKernelGGL((tri_contract_kernel<false, true>), grid, dim3(256), 0, ctx->stream, cp);
       else hipLaunchKernelGGL((tri_contract_kernel<false, false>), grid, dim3(256), 0, ctx->stream, cp);
     } else {
