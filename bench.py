@@ -59,8 +59,8 @@ def cpu_baseline(c2, budget_s=30.0):
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tri_mult_config2_kernel_stats.md")
-TRAFFIC_KERNELS = {"project": ["tri_project_resident_kernel<2>"], "output": ["tri_output_resident_kernel<2>"],
-                   "contract": ["tri_contract_kernel<false, true>", "tri_contract_kernel<true, true>"]}
+# kernel-name prefix of each triangle-multiplication launch kind in the profile's table
+TRAFFIC_KERNELS = {"project": "tri_project", "output": "tri_output", "contract": "tri_contract"}
 
 
 def measured_traffic(kind):
@@ -69,7 +69,8 @@ def measured_traffic(kind):
     try:
         line = next(l for l in open(TRAFFIC_FILE) if l.startswith("traffic_json: "))
         table = json.loads(line[len("traffic_json: "):])["kernels"]
-        vals = [table[k]["traffic_bytes"] for k in TRAFFIC_KERNELS.get(kind, []) if k in table]
+        prefix = TRAFFIC_KERNELS.get(kind)
+        vals = [v["traffic_bytes"] for k, v in table.items() if prefix and k.startswith(prefix)]
         return int(sum(vals) / len(vals)) if vals else None
     except (OSError, StopIteration, ValueError, KeyError):
         return None

@@ -22,6 +22,7 @@
 // cpu/af3/trunk/pairformer.js:213-300 (AF3, both directions, interleaved split).
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "lf_gemm.h"
 #include "lf_ops.h"
@@ -629,9 +630,6 @@ constexpr float TRI_NLOG2E = -1.4426950408889634f;
 #ifndef TRI_O_NWV
 #define TRI_O_NWV 8
 #endif
-#ifndef TRI_O_TPW
-#define TRI_O_TPW 1
-#endif
 
 // The 16 pairs of a project tile: row r is pair src0 + r * sstride, stored at out0 + r of every
 // channel plane, r < nvalid.  Tile t normally holds pairs 16t .. 16t + 15 in place.  With
@@ -777,48 +775,55 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
   }
 }
 
-// Output kernel for c_z = c_hidden = 128.  Each wave handles two 16-pair tiles (tiles w + k*nw
-// two at a time, as in the project kernel): X rows are transposed through a per-wave LDS
-// patch into the B-fragment layout, LN_out(X) and LN_in(z) stay in registers, and the
-// weights (A operand, resident in LDS) meet both tiles per fragment read.  With the weights as
-// the A operand a lane holds four consecutive channels of one pair, so the residual read and
-// the output write are 4-element vectors straight from the accumulators.  The gate weights
-// and bias arrive pre-multiplied by -log2(e): sigmoid = rcp(1 + exp2(acc)).
-constexpr int O2_LD = 136;
+constexpr int O2_LD = 136;   // X patch pitch (halves)
 
+// Xw[r][h] = X[h][row0 + r] for r < 16, element by element (rows past nvalid zero): the
+// path for partial tiles and for P % 8 != 0
 template <int ACT>
-__device__ __forceinline__ void x_transpose(_Float16* Xw, const _Float16* X, int P, int row0, int nvalid, int lane,
-                                            bool vec) {
-  // Xw[r][h] = X[h][row0 + r] for r < 16 (rows past the end zero)
-  if (vec && nvalid == 16) {
-    h8 xv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
-      xv[j] = *reinterpret_cast<const h8*>(X + (size_t)h * P + row0 + seg * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) Xw[(seg * 8 + jj) * O2_LD + h] = xv[j][jj];
-    }
-  } else {
+__device__ __forceinline__ void x_transpose(_Float16* Xw, const _Float16* X, int P, int row0, int nvalid, int lane) {
 #pragma unroll 1
-    for (int idx = lane; idx < 128 * 16; idx += 64) {
-      const int h = idx >> 4, r = idx & 15;
-      const _Float16 v = X[(size_t)h * P + row0 + (r < nvalid ? r : 0)];
-      Xw[r * O2_LD + h] = r < nvalid ? v : (_Float16)0.f;
-    }
+  for (int idx = lane; idx < 128 * 16; idx += 64) {
+    const int h = idx >> 4, r = idx & 15;
+    const _Float16 v = X[(size_t)h * P + row0 + (r < nvalid ? r : 0)];
+    Xw[r * O2_LD + h] = r < nvalid ? v : (_Float16)0.f;
   }
 }
 
-template <int ACT, int NWV, int TPW>
-__global__ __launch_bounds__(64 * NWV) void tri_output_v2_kernel(TriOutputParams p) {
+// x_transpose for a whole tile with P % 8 == 0, in two halves: the 16-byte global loads
+// (issued a tile ahead) and the transposing LDS stores.
+__device__ __forceinline__ void x_fetch(h8 (&xv)[4], const _Float16* X, int P, int row0, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+    xv[j] = *reinterpret_cast<const h8*>(X + (size_t)h * P + row0 + seg * 8);
+  }
+}
+
+__device__ __forceinline__ void x_put(_Float16* Xw, const h8 (&xv)[4], int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = lane + 64 * j, h = idx >> 1, seg = idx & 1;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) Xw[(seg * 8 + jj) * O2_LD + h] = xv[j][jj];
+  }
+}
+
+// Output kernel for c_z = c_hidden = 128, one 16-pair tile per wave step.  The steady-state
+// loop runs whole tiles as straight-line code: the next tile's z rows and X columns are loaded
+// at the top of a step (clamped, never skipped), its X columns are transposed into the wave's
+// other LDS buffer between the second pass's MFMAs and that pass's stores, and the residual
+// comes from the z rows already held.  Every wait on the in-order vector-memory counter then
+// covers loads issued earlier in the same step and none of the stores issued after them.  A
+// partial last tile (P % 16 pairs) runs once after the loop, masked, on the wave owning it.
+// The weights are the MFMA A operand (resident in LDS), so a lane's accumulators hold four
+// consecutive channels of one pair; the gate weights and bias arrive pre-multiplied by
+// -log2(e): sigmoid = rcp(1 + exp2(acc)).
+template <int ACT, int NWV, bool VECX>
+__global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams p) {
   constexpr int NT = 64 * NWV;
   __shared__ __attribute__((aligned(16))) _Float16 Wz[128 * RS_LD];   // [c][h]
   __shared__ __attribute__((aligned(16))) _Float16 Wg[128 * RS_LD];   // [c][k], pre-scaled
-  __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][16 * TPW * O2_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][2][16 * O2_LD];
   __shared__ __attribute__((aligned(16))) float Vs[6 * 128];         // bz, bg', centre-norm s/o, LN_in s/o
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   stage_resident(Wz, p.wz, tid, NT);
@@ -834,53 +839,36 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v2_kernel(TriOutputParams
   __syncthreads();
 
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
-  const int ntiles = (p.P + 15) >> 4, nw = gridDim.x * NWV;
-  const bool vec_x = (p.P & 7) == 0;
-  _Float16* Xw = Xs[wave];
-  for (int tile = blockIdx.x * NWV + wave; tile < ntiles; tile += TPW * nw) {
-    bool valid[TPW];
-    int row0[TPW], nval[TPW];
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      valid[tt] = tile + tt * nw < ntiles;   // wave-uniform
-      row0[tt] = (valid[tt] ? tile + tt * nw : tile) * 16;
-      nval[tt] = min(16, p.P - row0[tt]);
-    }
-    // z rows (LN_in) and the transposed X rows (LN_out)
-    FragTile<ACT, 4> z[TPW];
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      frag_load(z[tt], p.z, (size_t)row0[tt], nval[tt], 128, lane);
-      x_transpose<ACT>(Xw + tt * 16 * O2_LD, p.X, p.P, row0[tt], nval[tt], lane, vec_x);
-    }
-    h8 ax[TPW][4], az[TPW][4];
+  const int nfull = p.P >> 4, nw = gridDim.x * NWV;
+
+  // One tile: LN_out of X (LDS buffer Xc) and LN_in of z (zc), then two passes of 64 output
+  // channels.  A pass stages its f32 update in Xc (the X fragments are in registers by then)
+  // and each lane writes its own pair r16, channels c0 + 32jj + 8*g4 .. +7: the layout of its
+  // z fragment, which holds the residual.  `between` runs after the second pass's MFMAs.
+  auto run_tile = [&](auto full_tag, const FragTile<ACT, 4>& zc, _Float16* Xc, int row0, int nval,
+                      auto&& between) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    h8 ax[4], az[4];
     {
-      FragTile<DT_F16, 4> x[TPW];
+      FragTile<DT_F16, 4> x;
 #pragma unroll
-      for (int tt = 0; tt < TPW; ++tt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[tt].raw[j][0] = *reinterpret_cast<const uint4*>(Xw + (tt * 16 + r16) * O2_LD + 32 * j + kq);
-      if constexpr (TPW == 2) {
-        frag_ln_raw2(x[0], x[1], ax[0], ax[1], 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
-      } else {
-        frag_ln_raw1(x[0], ax[0], 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
-      }
+      for (int j = 0; j < 4; ++j) x.raw[j][0] = *reinterpret_cast<const uint4*>(Xc + r16 * O2_LD + 32 * j + kq);
+      frag_ln_raw1(x, ax, 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
     }
-    if constexpr (TPW == 2) frag_ln_raw2(z[0], z[1], az[0], az[1], 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
-    else frag_ln_raw1(z[0], az[0], 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
-#pragma unroll 1
-    for (int pass = 0; pass < 2; ++pass) {
-      const int c0 = pass * 64;
-      f4 accz[TPW][4], accg[TPW][4];
+    {
+      FragTile<ACT, 4> zl = zc;
+      frag_ln_raw1(zl, az, 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+    }
+    float* Us = reinterpret_cast<float*>(Xc);   // [16 pairs][68] f32 (pitch 68: no bank conflicts)
+    auto pass = [&](auto pass_tag) __attribute__((always_inline)) {
+      constexpr int PS = decltype(pass_tag)::value, c0 = PS * 64;
+      f4 accz[4], accg[4];
 #pragma unroll
       for (int t4 = 0; t4 < 4; ++t4) {
         const float4 bz = *reinterpret_cast<const float4*>(Vs + c0 + t4 * 16 + 4 * g4);
         const float4 bg = *reinterpret_cast<const float4*>(Vs + 128 + c0 + t4 * 16 + 4 * g4);
-#pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-          accz[tt][t4] = f4{bz.x, bz.y, bz.z, bz.w};
-          accg[tt][t4] = f4{bg.x, bg.y, bg.z, bg.w};
-        }
+        accz[t4] = f4{bz.x, bz.y, bz.z, bz.w};
+        accg[t4] = f4{bg.x, bg.y, bg.z, bg.w};
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -891,58 +879,80 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v2_kernel(TriOutputParams
           wg[t4] = *reinterpret_cast<const h8*>(Wg + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq);
         }
 #pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-          if (tt > 0 && !valid[tt]) break;
-#pragma unroll
-          for (int t4 = 0; t4 < 4; ++t4) {
-            accz[tt][t4] = mfma16(wz[t4], ax[tt][j], accz[tt][t4]);
-            accg[tt][t4] = mfma16(wg[t4], az[tt][j], accg[tt][t4]);
-          }
+        for (int t4 = 0; t4 < 4; ++t4) {
+          accz[t4] = mfma16(wz[t4], ax[j], accz[t4]);
+          accg[t4] = mfma16(wg[t4], az[j], accg[t4]);
         }
         __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
       }
-      // stage the pass's update (pairs x 64 channels, f32) in this wave's X patch (its X
-      // fragments are in registers), then write whole 128-byte half-rows: lane -> (pair, 8
-      // channels), the residual read the same way
-      float* Us = reinterpret_cast<float*>(Xw);   // [16*TPW pairs][68] f32 (pitch 68: no bank conflicts)
 #pragma unroll
-      for (int tt = 0; tt < TPW; ++tt) {
-        if (tt > 0 && !valid[tt]) break;
-#pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          float4 v;
-          v.x = accz[tt][t4][0] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][0]));
-          v.y = accz[tt][t4][1] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][1]));
-          v.z = accz[tt][t4][2] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][2]));
-          v.w = accz[tt][t4][3] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[tt][t4][3]));
-          *reinterpret_cast<float4*>(Us + (tt * 16 + r16) * 68 + t4 * 16 + 4 * g4) = v;
-        }
+      for (int t4 = 0; t4 < 4; ++t4) {
+        float4 v;
+        v.x = accz[t4][0] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[t4][0]));
+        v.y = accz[t4][1] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[t4][1]));
+        v.z = accz[t4][2] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[t4][2]));
+        v.w = accz[t4][3] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[t4][3]));
+        *reinterpret_cast<float4*>(Us + r16 * 68 + t4 * 16 + 4 * g4) = v;
       }
+      if constexpr (PS == 1) between();
 #pragma unroll
-      for (int u = 0; u < 2 * TPW; ++u) {
-        const int pr = u * 8 + (lane >> 3), seg = lane & 7;   // pair slot, 8-channel segment
-        const int tt = pr >> 4, r = pr & 15;
-        if (tt > 0 && !valid[tt]) break;
-        if (r >= nval[tt]) continue;
-        const float4 u0 = *reinterpret_cast<const float4*>(Us + pr * 68 + seg * 8);
-        const float4 u1 = *reinterpret_cast<const float4*>(Us + pr * 68 + seg * 8 + 4);
+      for (int jj = 0; jj < 2; ++jj) {
+        const float4 u0 = *reinterpret_cast<const float4*>(Us + r16 * 68 + 32 * jj + 8 * g4);
+        const float4 u1 = *reinterpret_cast<const float4*>(Us + r16 * 68 + 32 * jj + 8 * g4 + 4);
         float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-        const size_t idx = (size_t)(row0[tt] + r) * 128 + c0 + seg * 8;
         if (p.accumulate) {
-          float a4[4], b4[4];
-          ld4v<ACT>(p.z, idx, a4);
-          ld4v<ACT>(p.z, idx + 4, b4);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[i] += a4[i];
-            v[4 + i] += b4[i];
-          }
+          for (int e = 0; e < 8; ++e) v[e] += zc.get(2 * PS + jj, e);
         }
+        const size_t idx = (size_t)(row0 + r16) * 128 + c0 + 32 * jj + 8 * g4;
         const float lo[4] = {v[0], v[1], v[2], v[3]}, hi[4] = {v[4], v[5], v[6], v[7]};
-        st4v<ACT>(p.out, idx, lo);
-        st4v<ACT>(p.out, idx + 4, hi);
+        if (FULL || r16 < nval) {
+          st4v<ACT>(p.out, idx, lo);
+          st4v<ACT>(p.out, idx + 4, hi);
+        }
       }
+    };
+    pass(std::integral_constant<int, 0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    pass(std::integral_constant<int, 1>{});
+  };
+
+  int tile = blockIdx.x * NWV + wave;
+  if (tile < nfull) {
+    FragTile<ACT, 4> zc;
+    frag_load(zc, p.z, (size_t)tile * 16, 16, 128, lane);
+    if constexpr (VECX) {
+      h8 xv[4];
+      x_fetch(xv, p.X, p.P, tile * 16, lane);
+      x_put(Xs[wave][0], xv, lane);
+    } else {
+      x_transpose<ACT>(Xs[wave][0], p.X, p.P, tile * 16, 16, lane);
     }
+    int cur = 0;
+    for (; tile < nfull; tile += nw) {
+      const int nt = tile + nw < nfull ? tile + nw : tile;   // the last step reloads its own tile
+      FragTile<ACT, 4> zn;
+      h8 xn[4];
+      frag_load(zn, p.z, (size_t)nt * 16, 16, 128, lane);
+      if constexpr (VECX) x_fetch(xn, p.X, p.P, nt * 16, lane);
+      _Float16* Xn = Xs[wave][cur ^ 1];
+      run_tile(std::true_type{}, zc, Xs[wave][cur], tile * 16, 16, [&]() __attribute__((always_inline)) {
+        if constexpr (VECX) x_put(Xn, xn, lane);
+        else x_transpose<ACT>(Xn, p.X, p.P, nt * 16, 16, lane);
+      });
+      // take the next rows now (an asm use forces the wait here, within this step, where the
+      // counter wait cannot cover this step's stores), not at their first use next step
+      launder(zn);
+      zc = zn;
+      cur ^= 1;
+    }
+  }
+  if (tile == nfull && nfull * 16 < p.P) {
+    const int row0 = nfull * 16, nval = p.P - row0;
+    FragTile<ACT, 4> zc;
+    frag_load(zc, p.z, (size_t)row0, nval, 128, lane);
+    x_transpose<ACT>(Xs[wave][0], p.X, p.P, row0, nval, lane);
+    run_tile(std::false_type{}, zc, Xs[wave][0], row0, nval, []() {});
   }
 }
 
@@ -973,7 +983,10 @@ static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resid
   if (resident && op.C == 128 && op.H == 128) {
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_O_NWV - 1) / TRI_O_NWV)));
-    hipLaunchKernelGGL((tri_output_v2_kernel<ACT, TRI_O_NWV, TRI_O_TPW>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
+    if ((P & 7) == 0)
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, TRI_O_NWV, true>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
+    else
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, TRI_O_NWV, false>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
     return;
   }
   if (resident) {
