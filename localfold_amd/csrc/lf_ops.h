@@ -38,6 +38,11 @@ inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }
 int tri_mult(lf_context* ctx, const lf_tri_mult_args& a);
 int attention(lf_context* ctx, const lf_attention_args& a);
 int transition(lf_context* ctx, const lf_transition_args& a);
+// fused transition (lf_mlp.hip): c = 128 (ReLU or SwiGLU) or 256 (ReLU), hidden % 32 == 0;
+// views: W1 (gate half), [W1 value half,] W2; packed: mlp_packed_bytes of workspace
+bool mlp_supported(int C, int H, bool swiglu);
+size_t mlp_packed_bytes(int C, int H, bool swiglu);
+int transition_fused(lf_context* ctx, const lf_transition_args& a, const WView* views, void* packed);
 int outer_product_mean(lf_context* ctx, const lf_opm_args& a);
 
 }  // namespace lf

@@ -2,8 +2,9 @@
 // 1080-1085) or x += (swish(h[:H]) * h[H:]) W2 with h = LN(x) W1 (AF3 SwiGLU, blocked split,
 // cpu/af3/trunk/pairformer.js:180-201).
 //
-// Two kernels per row chunk: lnproj (LN + W1 + activation -> f16 hidden) and rowgemm (hidden W2
-// + b2 + residual).  Rows are chunked so the hidden buffer stays within `chunk_bytes`
+// c = 128 / 256 (every AF2/AF3 pair and MSA width) runs fused in one kernel (lf_mlp.hip).
+// Otherwise two kernels per row chunk: lnproj (LN + W1 + activation -> f16 hidden) and rowgemm
+// (hidden W2 + b2 + residual).  Rows are chunked so the hidden buffer stays within `chunk_bytes`
 // (transitionChunkRows, webgpu/kernels/transition.js:411-442, without WebGPU's binding-offset
 // alignment, which HIP does not have).
 #include <algorithm>
@@ -35,6 +36,16 @@ int transition(lf_context* ctx, const lf_transition_args& a) {
     LF_REQUIRE(outs == 2 * Hd, "transition1 must have 2 * hidden outputs (gate half, then value half)");
   }
   LF_TRY(make_view(w.w2, Hd, C, "secondWeight", &views[nv++]));
+
+  // fused path: one kernel, no hidden buffer (vector loads need 16-byte aligned rows and biases)
+  const bool swiglu = a.kind == LF_TRANSITION_SWIGLU;
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  if (mlp_supported(C, Hd, swiglu) && al16(a.act) && al16(a.out) && al16(w.b1) && al16(w.b2)) {
+    size_t sz = mlp_packed_bytes(C, Hd, swiglu);
+    void* packed;
+    LF_TRY(workspace(ctx, &sz, &packed, 1));
+    return transition_fused(ctx, a, views, packed);
+  }
 
   // rows per chunk: all when the f16 hidden buffer fits the budget, else a multiple of 128
   const long long budget = a.chunk_bytes > 0 ? a.chunk_bytes : 32LL * 1024 * 1024;

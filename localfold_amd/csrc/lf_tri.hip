@@ -332,39 +332,7 @@ __global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) 
 
 constexpr int RS_LD = 136;
 
-// Four consecutive activations at element index idx (8-/16-byte aligned).
-template <int ACT>
-__device__ __forceinline__ void ld4v(const void* base, size_t idx, float (&v)[4]) {
-  if constexpr (ACT == DT_F32) {
-    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-  } else if constexpr (ACT == DT_F16) {
-    const h4 q = *reinterpret_cast<const h4*>(static_cast<const _Float16*>(base) + idx);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (float)q[i];
-  } else {
-    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
-    v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
-    v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
-  }
-}
-
-template <int ACT>
-__device__ __forceinline__ void st4v(void* base, size_t idx, const float (&v)[4]) {
-  if constexpr (ACT == DT_F32) {
-    *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if constexpr (ACT == DT_F16) {
-    h4 q;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = (_Float16)v[i];
-    *reinterpret_cast<h4*>(static_cast<_Float16*>(base) + idx) = q;
-  } else {
-    uint2 q;
-    q.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-    q.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + idx) = q;
-  }
-}  // 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
+// 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
 
 __device__ __forceinline__ void stage_resident(_Float16* W, const WExp& e, int tid, int nthreads) {
   const int segs = e.kp >> 3;

@@ -39,6 +39,25 @@ def test_transition_relu(ctx, blockw, rows_shape, which, chunk):
     H.assert_close(out.cpu().numpy(), ref, label=f"{which} {rows_shape} chunk={chunk}")
 
 
+@pytest.mark.parametrize("which,dt", [("pairTransition", "bfloat16"), ("msaTransition", "bfloat16"),
+                                      ("msaTransition", "float16")])
+def test_transition_fused_dtypes(ctx, blockw, which, dt):
+    """16-bit activations, 700 rows (a partial 256-row block); the update alone is compared, so
+    the output rounding is that of the update's magnitude."""
+    import torch
+    from localfold_amd import device as D
+    w = blockw[which]
+    c, hid = w["firstWeight"].shape
+    x = S.Stream(11).values(700 * c, 1.5).reshape(700, c)
+    xt = _dev(ctx, x, getattr(torch, dt))
+    x16 = xt.float().cpu().numpy()
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.transition_weights(dw, w)
+    out = D.transition(ctx, xt, ws, hid)
+    torch.cuda.synchronize()
+    H.assert_close(out.float().cpu().numpy(), ops.transition_af2(x16, w), label=f"{which} {dt}")
+
+
 @pytest.mark.parametrize("c,n", [(128, 40), (384, 50)])
 def test_transition_swiglu(ctx, c, n):
     import torch
