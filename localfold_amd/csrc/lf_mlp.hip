@@ -124,6 +124,7 @@ __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
   __syncthreads();
   h8 xf[2][KS];
   frag_ln_raw2(xt[0], xt[1], xf[0], xf[1], C, Gs, Gs + C, p.eps, p.fast_var, lane);
+  __builtin_amdgcn_sched_barrier(0);   // the raw rows die before the accumulators are born
 
   f4 acc[2][CT];
 #pragma unroll
@@ -224,6 +225,7 @@ __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
         for (int i = 0; i < 4; ++i) v[i] += r[i];
       }
       st4v<ACT>(p.out, idx, v);
+      __builtin_amdgcn_sched_barrier(0);   // one tile's residual in flight at a time
     }
   }
 }

@@ -743,6 +743,107 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
   }
 }
 
+// Project kernel for c_z = c_hidden = 128 when every tile is whole (P % 16 == 0, or N % 16 == 0
+// for the transposed incoming store): the v2 work as straight-line code.  The next tile's rows
+// and mask are loaded at the top of a step (clamped, never skipped), the four passes are
+// unrolled, and the next rows are taken into registers (an asm use forces the wait) after the
+// last pass's MFMAs and before its stores: every wait on the in-order vector-memory counter
+// then covers loads issued earlier in the same step, never the stores that follow them.
+template <int ACT, int NWV>
+__global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectParams p) {
+  constexpr int NT = 64 * NWV;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate', b-proj, b-gate' [h][k]
+  __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
+  __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  stage_resident(Ws, p.wp[0], tid, NT);
+  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, NT);
+  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, NT);
+  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, NT);
+  for (int i = tid; i < 128; i += NT) {
+    Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
+    Bs[128 + i] = p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f;
+    Bs[256 + i] = p.bp[1] ? p.bp[1][i] : 0.f;
+    Bs[384 + i] = p.bg[1] ? TRI_NLOG2E * p.bg[1][i] : 0.f;
+  }
+  stage_vec(Gs, p.ln_s, 128, 1.f, 128, tid, NT);
+  stage_vec(Gs + 128, p.ln_o, 128, 0.f, 128, tid, NT);
+  __syncthreads();
+
+  const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
+  const int ntiles = p.kmajor_out ? p.N * (p.N >> 4) : p.P >> 4, nw = gridDim.x * NWV;
+  auto fetch = [&](int tl, FragTile<ACT, 4>& t, float (&m)[4]) __attribute__((always_inline)) {
+    const TileGeom g = tile_geom(p, tl);
+    frag_load_row(t, p.z, (size_t)g.src0 + (size_t)r16 * g.sstride, 128, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = p.mask[g.src0 + (q4 + i) * g.sstride];
+  };
+  int tile = blockIdx.x * NWV + wave;
+  if (tile >= ntiles) return;
+  FragTile<ACT, 4> tc;
+  float mc[4];
+  fetch(tile, tc, mc);
+  for (; tile < ntiles; tile += nw) {
+    const int out0 = tile_geom(p, tile).out0;
+    h8 xa[4];
+    frag_ln_raw1(tc, xa, 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    const int nt = tile + nw < ntiles ? tile + nw : tile;   // the last step reloads its own tile
+    FragTile<ACT, 4> tn;
+    float mn[4];
+    fetch(nt, tn, mn);
+    auto pass = [&](auto pass_tag) __attribute__((always_inline)) {
+      constexpr int PS = decltype(pass_tag)::value, which = PS >> 1, hh = (PS & 1) * 64;
+      const _Float16* Wp = Ws + (which * 2) * 128 * RS_LD;
+      const _Float16* Wg = Wp + 128 * RS_LD;
+      const float* bp = Bs + which * 256 + hh;
+      const float* bg = bp + 128;
+      f4 acc[8];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const float b0 = bp[t4 * 16 + r16], b1 = bg[t4 * 16 + r16];
+        acc[t4] = f4{b0, b0, b0, b0};
+        acc[4 + t4] = f4{b1, b1, b1, b1};
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h8 wb[8];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          wb[t4] = *reinterpret_cast<const h8*>(Wp + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+          wb[4 + t4] = *reinterpret_cast<const h8*>(Wg + (hh + t4 * 16 + r16) * RS_LD + 32 * j + kq);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] = mfma16(xa[j], wb[u], acc[u]);
+        __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
+      }
+      if constexpr (PS == 3) {
+        launder(tn);
+        asm volatile("" : "+v"(mn[0]), "+v"(mn[1]), "+v"(mn[2]), "+v"(mn[3]));
+      }
+      _Float16* dst = which ? p.out[1] : p.out[0];
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int h = hh + t4 * 16 + r16;
+        h4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = (_Float16)(mc[i] * acc[t4][i] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(acc[4 + t4][i])));
+        *reinterpret_cast<h4*>(dst + (size_t)h * p.P + out0 + q4) = o;
+      }
+    };
+    pass(std::integral_constant<int, 0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    pass(std::integral_constant<int, 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+    pass(std::integral_constant<int, 2>{});
+    __builtin_amdgcn_sched_barrier(0);
+    pass(std::integral_constant<int, 3>{});
+    tc = tn;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mc[i] = mn[i];
+  }
+}
+
 constexpr int O2_LD = 136;   // X patch pitch (halves)
 
 // Xw[r][h] = X[h][row0 + r] for r < 16, element by element (rows past nvalid zero): the
@@ -930,7 +1031,11 @@ static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool res
   if (resident && pp.C == 128 && pp.H == 128) {
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_P_NWV - 1) / TRI_P_NWV)));
-    hipLaunchKernelGGL((tri_project_v2_kernel<ACT, TRI_P_NWV, TRI_P_TPW>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
+    const bool whole = pp.kmajor_out ? pp.N % 16 == 0 : P % 16 == 0;
+    if (whole)
+      hipLaunchKernelGGL((tri_project_v3_kernel<ACT, TRI_P_NWV>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
+    else
+      hipLaunchKernelGGL((tri_project_v2_kernel<ACT, TRI_P_NWV, TRI_P_TPW>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
     return;
   }
   if (resident) {
