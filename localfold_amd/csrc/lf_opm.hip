@@ -119,43 +119,29 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OuterParams p) {
   }
 }
 
-// den[i*N + j] = eps + sum_s m[s][i] m[s][j]: a 32x32 tile per block (16x16 threads of 2x2
-// outputs), the mask staged through LDS 64 sequences at a time; sums run in sequence order.
+// den[i*N + j] = eps + sum_s m[s][i] m[s][j]: a 16x16 tile per block, one output per thread
+// (N = 384 gives 576 blocks), the mask columns staged through LDS 64 sequences at a time
+// (reads of a staged row are broadcasts or conflict-free); sums run in sequence order.
 constexpr int CT_S = 64;
 
 __global__ __launch_bounds__(256) void opm_count_kernel(const float* mask, float* den, int S, int N, float eps) {
-  __shared__ float Mi[CT_S][32], Mj[CT_S][32];
+  __shared__ float Mi[CT_S][16], Mj[CT_S][16];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
-  float acc[2][2] = {};
+  const int i0 = blockIdx.y * 16, j0 = blockIdx.x * 16;
+  float acc = 0.f;
   for (int s0 = 0; s0 < S; s0 += CT_S) {
-    for (int e = tid; e < CT_S * 32; e += 256) {
-      const int ss = e >> 5, c = e & 31, sg = s0 + ss;
+    for (int e = tid; e < CT_S * 16; e += 256) {
+      const int ss = e >> 4, c = e & 15, sg = s0 + ss;
       Mi[ss][c] = (sg < S && i0 + c < N) ? mask[(size_t)sg * N + i0 + c] : 0.f;
       Mj[ss][c] = (sg < S && j0 + c < N) ? mask[(size_t)sg * N + j0 + c] : 0.f;
     }
     __syncthreads();
-#pragma unroll 8
-    for (int ss = 0; ss < CT_S; ++ss) {
-      const float a0 = Mi[ss][ty * 2], a1 = Mi[ss][ty * 2 + 1];
-      const float b0 = Mj[ss][tx * 2], b1 = Mj[ss][tx * 2 + 1];
-      acc[0][0] = fmaf(a0, b0, acc[0][0]);
-      acc[0][1] = fmaf(a0, b1, acc[0][1]);
-      acc[1][0] = fmaf(a1, b0, acc[1][0]);
-      acc[1][1] = fmaf(a1, b1, acc[1][1]);
-    }
+#pragma unroll 16
+    for (int ss = 0; ss < CT_S; ++ss) acc = fmaf(Mi[ss][ty], Mj[ss][tx], acc);
     __syncthreads();
   }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = i0 + ty * 2 + u;
-    if (i >= N) continue;
-#pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      const int j = j0 + tx * 2 + v;
-      if (j < N) den[(size_t)i * N + j] = eps + acc[u][v];
-    }
-  }
+  const int i = i0 + ty, j = j0 + tx;
+  if (i < N && j < N) den[(size_t)i * N + j] = eps + acc;
 }
 
 int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
@@ -208,7 +194,7 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, bufs[5], "opm.project"));
   {
     LaunchScope ls(ctx, "opm.count");
-    hipLaunchKernelGGL(opm_count_kernel, dim3((N + 31) / 32, (N + 31) / 32), dim3(256), 0, ctx->stream, a.mask, den,
+    hipLaunchKernelGGL(opm_count_kernel, dim3((N + 15) / 16, (N + 15) / 16), dim3(256), 0, ctx->stream, a.mask, den,
                        S, N, a.norm_epsilon);
   }
   LF_TRY(check_hip(hipGetLastError(), "opm count launch"));
