@@ -111,6 +111,8 @@ class DeviceWeights:
         shape = list(rec["shape"])
         if len(shape) != 2:
             raise ValueError(f"weights must be 2-D, got shape {shape}")
+        if "layout" in rec:   # a record that names its stored layout (a bundle's [in][out] codes)
+            layout = {"in_out": capi.LF_IN_OUT, "out_in": capi.LF_OUT_IN}[rec["layout"]]
         w = capi.lf_weight()
         w.dtype = _DTYPE_CODE[rec["dtype"]]
         w.layout = layout
@@ -398,7 +400,7 @@ def evoformer_block_args(msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.
     a = capi.lf_evoformer_block_args()
     a.sequences, a.length, a.c_m, a.c_z = s_, n, cm, pair.shape[-1]
     a.c_outer = np.shape(_plain(w["outerProductMean"]["leftWeight"]))[1]
-    a.tri_hidden = np.shape(_plain(w["triangleMultiplicationOutgoing"]["linearAPWeight"]))[0]
+    a.tri_hidden = _out_dim(w["triangleMultiplicationOutgoing"]["linearAPWeight"], out_axis=0)
     a.msa_hidden = np.shape(_plain(w["msaTransition"]["firstWeight"]))[1]
     a.pair_hidden = np.shape(_plain(w["pairTransition"]["firstWeight"]))[1]
     a.msa_dtype, a.msa = act_code(msa), ptr(msa)
@@ -410,6 +412,15 @@ def evoformer_block_args(msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.
 
 def _plain(v):
     return np.zeros(v["shape"]) if isinstance(v, dict) else v
+
+
+def _out_dim(v, out_axis: int) -> int:
+    """Output width of a weight whose arrays are stored with the output on `out_axis`; a record
+    naming its own layout (a bundle's [in][out] codes) says where its output axis is."""
+    shape = np.shape(_plain(v))
+    if isinstance(v, dict) and "layout" in v:
+        out_axis = 1 if v["layout"] == "in_out" else 0
+    return shape[out_axis]
 
 
 def evoformer_block(ctx: Context, msa, pair, msa_mask, pair_mask, wstruct, w: dict, epsilon: float = 1e-5):

@@ -38,6 +38,37 @@ def test_evoformer_block(ctx, s, n):
     H.assert_close(pair.cpu().numpy(), rp, label="evoformer pair")
 
 
+def test_evoformer_block_from_bundle(ctx, tmp_path):
+    """A block whose weights come from an int8 bundle in the reference's manifest + shard layout
+    (stacked haiku, codes uploaded as stored, triangle projections in their [in][out] storage)
+    matches the oracle block run on those weights' decoded values."""
+    import torch
+    from localfold_amd import bundle as B, device as D
+    from oracle import codec
+    w, act = _evo_inputs(3, 28, 5)
+    tensors, section, _ = H.af2_stack_bundle_tensors([w], "int8", 64)
+    store = B.FileTensorStore.open(H.write_bundle(str(tmp_path), tensors, section))
+    wb = B.af2_main_stack_weights(store)[0]
+
+    def decoded(v):
+        if isinstance(v, dict) and "dtype" in v:
+            return codec.decode(v)
+        return {k: decoded(u) for k, u in v.items()} if isinstance(v, dict) else v
+
+    wf = decoded(wb)
+    for key in ("triangleMultiplicationOutgoing", "triangleMultiplicationIncoming"):   # oracle: (out,in)
+        for name in ("linearAPWeight", "linearAGWeight", "linearBPWeight", "linearBGWeight", "linearZWeight", "linearGWeight"):
+            wf[key][name] = wf[key][name].T.copy()
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.evoformer_weights(dw, wb)
+    msa, pair = _dev(ctx, act["msa"]), _dev(ctx, act["pair"])
+    D.evoformer_block(ctx, msa, pair, _dev(ctx, act["msaMask"]), _dev(ctx, act["pairMask"]), ws, wb)
+    torch.cuda.synchronize()
+    rm, rp = blocks.evoformer_block_af2(act["msa"], act["pair"], act["msaMask"], act["pairMask"], wf)
+    H.assert_close(msa.cpu().numpy(), rm, label="bundle block msa")
+    H.assert_close(pair.cpu().numpy(), rp, label="bundle block pair")
+
+
 def test_evoformer_stack_two_blocks(ctx):
     import torch
     from localfold_amd import device as D
