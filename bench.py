@@ -173,13 +173,83 @@ def evoformer_block_config4(ctx, D, synthetic, reps):
             "outputs_finite": finite, "kernels_ms": kern}
 
 
+def evoformer_stack_config4(ctx, D, synthetic, reps):
+    """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
+    pass (1 recycle), 48 distinct int8 weight sets, bf16 activations, through lf_evoformer_stack."""
+    import torch
+    c4 = synthetic.config4_inputs()
+    dev = ctx.device
+    dw = D.DeviceWeights(dev)
+    weights = [c4["weights"]] + [synthetic.quantise_tree(synthetic.config1_inputs(seed=100 + k, n=1)[0], "int8", 64)
+                                 for k in range(47)]
+    ws = [D.evoformer_weights(dw, w) for w in weights]
+    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16)
+    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16)
+    mm = torch.as_tensor(c4["msa_mask"]).to(dev)
+    pm = torch.as_tensor(c4["pair_mask"]).to(dev)
+    msa0, pair0 = msa.clone(), pair.clone()
+    s_, n = c4["msa_mask"].shape
+    del c4
+
+    def stack():
+        msa.copy_(msa0)
+        pair.copy_(pair0)
+        D.evoformer_stack(ctx, msa, pair, mm, pm, ws, weights[0])
+
+    stack()   # grows the workspace once
+    ms = timed(stack, reps)
+    finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
+    gflop = 48 * 1076.5
+    return {"workload": f"BASELINE config 4, the 48-block AF2 Evoformer stack: N_res={n}, N_seq={s_}, c_m=256, "
+                        "c_z=128, 48 distinct int8 weight sets (fp16 scales, groups of 64), bf16 activations, "
+                        "one pass; time includes restoring the inputs (2 device copies, 138 MB)",
+            "ms_per_stack": round(ms, 2), "ms_per_block": round(ms / 48, 3),
+            "tflops": round(gflop / ms, 1), "algorithmic_gflop": gflop, "outputs_finite": finite}
+
+
+def pairformer_block_config5(ctx, D, synthetic, reps):
+    """BASELINE config 5 at one block: an AF3 Pairformer block at N_tokens=1024, c_z=128,
+    c_s=384, int5 weights (fp16 scale and zero, groups of 32), bf16 activations, the last 32
+    tokens padded."""
+    import torch
+    n, cz, cs = 1024, 128, 384
+    w = synthetic.quantise_tree(synthetic.synthetic_pairformer_weights(cz, cs, 4, 16, 24, seed=21), "int5", 32)
+    st = synthetic.Stream(22)
+    dev = ctx.device
+    pair = torch.as_tensor(st.normal(n * n * cz).reshape(n, n, cz)).to(dev).to(torch.bfloat16)
+    single = torch.as_tensor(st.normal(n * cs).reshape(n, cs)).to(dev).to(torch.bfloat16)
+    seq_mask = np.ones(n, np.float32)
+    seq_mask[-32:] = 0
+    sm = torch.as_tensor(seq_mask).to(dev)
+    pm = torch.as_tensor(np.outer(seq_mask, seq_mask).astype(np.float32)).to(dev)
+    dw = D.DeviceWeights(dev)
+    ws = D.pairformer_weights(dw, w)
+    pair0, single0 = pair.clone(), single.clone()
+
+    def block():
+        D.pairformer_block(ctx, pair, single, pm, sm, ws)
+
+    block()
+    pair.copy_(pair0)
+    single.copy_(single0)
+    ms = timed(block, reps)
+    kern = profile_ops(ctx, block, 2)
+    finite = bool(torch.isfinite(pair).all().item() and torch.isfinite(single).all().item())
+    gflop = 2692.0
+    return {"workload": f"BASELINE config 5, one AF3 Pairformer block: N_tokens={n}, c_z={cz}, c_s={cs}, "
+                        "triangle attention 4x32, single attention 16x24, int5 weights (groups of 32), bf16 "
+                        "activations, last 32 tokens padded",
+            "ms_per_block": round(ms, 3), "stack_48_blocks_s_estimate": round(48 * ms / 1e3, 3),
+            "tflops": round(gflop / ms, 1), "algorithmic_gflop": gflop, "outputs_finite": finite, "kernels_ms": kern}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the config 3 / config 4 measurements")
+    ap.add_argument("--no-extras", action="store_true", help="skip the config 3 / 4 / 5 measurements")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy 5 times (the reference "
                          "reading for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -271,6 +341,10 @@ def main():
         extras["triangle_attention"] = triangle_attention_config3(ctx, D, synthetic, 10)
         log("config 4: one Evoformer block ...")
         extras["evoformer_block"] = evoformer_block_config4(ctx, D, synthetic, 5)
+        log("config 4: the 48-block stack ...")
+        extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
+        log("config 5: one Pairformer block ...")
+        extras["pairformer_block"] = pairformer_block_config5(ctx, D, synthetic, 5)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -303,6 +377,8 @@ def main():
         "cpu_baseline": cpu,
         "evoformer_block": extras.get("evoformer_block"),
         "triangle_attention": extras.get("triangle_attention"),
+        "evoformer_stack": extras.get("evoformer_stack"),
+        "pairformer_block": extras.get("pairformer_block"),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -92,10 +92,13 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   stage_vec(Gs, p.ln_s, p.C, 1.f, KP, tid, 512);
   stage_vec(Gs + KP, p.ln_o, p.C, 0.f, KP, tid, 512);
-  const int nchunks = p.nchunks;
+  // blockIdx.y takes a contiguous range of the column chunks (few rows: more blocks)
+  const int per = (p.nchunks + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int ci0 = (int)blockIdx.y * per, ci1 = min(p.nchunks, ci0 + per);
+  if (ci0 >= ci1) return;
   uint4 regs[NREG];
-  chunk_load<KP, NREG>(p, 0, regs, tid);
-  if (wave == 0) build_chunk_tab(Tab[0], p, 0, lane);
+  chunk_load<KP, NREG>(p, ci0, regs, tid);
+  if (wave == 0) build_chunk_tab(Tab[0], p, ci0, lane);
   const int row_block = blockIdx.x * LP_ROWS;
   for (int i = tid; i < p.ngroups * LP_ROWS; i += 512) {
     const int g = i / LP_ROWS, r = i - g * LP_ROWS;
@@ -128,10 +131,11 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
     for (int tt = 0; tt < 2; ++tt) rm[tt] = p.rowmask[srow[tt]];
   }
 
-  for (int ci = 0; ci < nchunks; ++ci) {
-    const _Float16* W = Ws[ci & 1];
-    const ChunkTab& T = Tab[ci & 1];
-    if (ci + 1 < nchunks) chunk_load<KP, NREG>(p, ci + 1, regs, tid);
+  for (int ci = ci0; ci < ci1; ++ci) {
+    const int kb = (ci - ci0) & 1;   // LDS buffer of this chunk
+    const _Float16* W = Ws[kb];
+    const ChunkTab& T = Tab[kb];
+    if (ci + 1 < ci1) chunk_load<KP, NREG>(p, ci + 1, regs, tid);
     f4 acc[2][4];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -149,7 +153,7 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
     }
-    if (wave == 0 && ci + 1 < nchunks) build_chunk_tab(Tab[(ci + 1) & 1], p, ci + 1, lane);
+    if (wave == 0 && ci + 1 < ci1) build_chunk_tab(Tab[kb ^ 1], p, ci + 1, lane);
 
     // wave-uniform by construction; readfirstlane lets the compiler keep them in SGPRs
     const int gi = __builtin_amdgcn_readfirstlane(p.chunk_group[ci]);
@@ -204,8 +208,8 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
         __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
       }
     }
-    if (ci + 1 < nchunks) {
-      chunk_store<KP, NREG>(Ws[(ci + 1) & 1], regs, tid);
+    if (ci + 1 < ci1) {
+      chunk_store<KP, NREG>(Ws[kb ^ 1], regs, tid);
       __syncthreads();
     }
   }
@@ -276,7 +280,11 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
     LF_TRY(expand_packed(ctx, views, W, off, row0, nv, static_cast<_Float16*>(packed), KP,
                        (std::string(label) + ".expand").c_str()));
   const int ks = lnproj_ks(p.C);
-  dim3 grid((p.rows + LP_ROWS - 1) / LP_ROWS);
+  // few row blocks (the single track): split the column chunks over grid.y so about two blocks
+  // per CU run; each re-does the LayerNorm of its rows
+  const int xb = (p.rows + LP_ROWS - 1) / LP_ROWS;
+  const int ysplit = std::max(1, std::min(p.nchunks, (2 * ctx->num_cus) / xb));
+  dim3 grid(xb, ysplit);
   LaunchScope ls(ctx, label);
 #define LF_LP(A, K) hipLaunchKernelGGL((lnproj_kernel<A, K>), grid, dim3(512), 0, ctx->stream, p)
 #define LF_LPK(A)            \
