@@ -17,6 +17,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));   // register words (arrays of it stay in VGPRs)
 
 enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3, DT_I5 = 4 };
 
@@ -280,16 +281,16 @@ __device__ __forceinline__ void lds_ln_inplace(_Float16* X, int ld, int nvalid, 
 template <int ACT, int KS = 4>
 struct FragTile {
   typedef typename Act<ACT>::T T;
-  static constexpr int NV = (int)sizeof(T) * 8 / 16;   // uint4 per 8 elements
-  uint4 raw[KS][NV];
+  static constexpr int NV = (int)sizeof(T) * 8 / 16;   // 16-byte words per 8 elements
+  u32x4 raw[KS][NV];
   // element e (< 8) of k-step j, decoded with shifts (no address-taken locals)
   __device__ __forceinline__ float get(int j, int e) const {
     if constexpr (ACT == DT_F32) {
-      const uint4 q = raw[j][e >> 2];
+      const u32x4 q = raw[j][e >> 2];
       const uint32_t w = (e & 3) == 0 ? q.x : (e & 3) == 1 ? q.y : (e & 3) == 2 ? q.z : q.w;
       return __uint_as_float(w);
     } else {
-      const uint4 q = raw[j][0];
+      const u32x4 q = raw[j][0];
       const uint32_t w = (e >> 1) == 0 ? q.x : (e >> 1) == 1 ? q.y : (e >> 1) == 2 ? q.z : q.w;
       const uint16_t hbits = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
       if constexpr (ACT == DT_BF16) return bf2f(hbits);
@@ -310,7 +311,7 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
     for (int j = 0; j < KS; ++j)
 #pragma unroll
       for (int v = 0; v < FragTile<ACT, KS>::NV; ++v)
-        t.raw[j][v] = *reinterpret_cast<const uint4*>(s + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
+        t.raw[j][v] = *reinterpret_cast<const u32x4*>(s + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
   } else {
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
@@ -322,8 +323,8 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
           const uint32_t bits = __float_as_uint(s[c < C ? c : 0]);
           w[k] = c < C ? bits : 0u;
         }
-        t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
-        t.raw[j][1] = make_uint4(w[4], w[5], w[6], w[7]);
+        t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
+        t.raw[j][1] = u32x4{w[4], w[5], w[6], w[7]};
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -332,7 +333,7 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
           const uint16_t hi = c0 + 1 < C ? __builtin_bit_cast(uint16_t, s[c0 + 1 < C ? c0 + 1 : 0]) : (uint16_t)0;
           w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        t.raw[j][0] = make_uint4(w[0], w[1], w[2], w[3]);
+        t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
       }
     }
   }

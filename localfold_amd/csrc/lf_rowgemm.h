@@ -40,6 +40,11 @@ struct Group {
   const float* bias0; // per output column (nullable)
   const float* bias1;
   Dst dst;
+  int tr;             // set by launch_lnproj: the epilogue runs on the transposed tile (a lane
+                      // holds 4 consecutive rows of one column) for destinations whose rows,
+                      // not columns, are contiguous
+  int vec;            // set by launch_lnproj: every 4-element run a lane stores (4 columns, or
+                      // 4 rows when tr) is contiguous and 8-byte aligned
 };
 
 constexpr int MAX_GROUPS = 6;
@@ -57,8 +62,9 @@ struct LnProjParams {
   int ngroups;
   const _Float16* wpk;    // packed weights (set by launch_lnproj)
   int nchunks;            // set by launch_lnproj: chunk ci covers group chunk_group[ci]'s
-  unsigned char chunk_group[MAX_CHUNKS];   // logical columns from chunk_c0[ci]
-  short chunk_c0[MAX_CHUNKS];
+  int chunk_group[MAX_CHUNKS];   // logical columns from chunk_c0[ci] (ints: kernel-argument
+  int chunk_c0[MAX_CHUNKS];      // loads of them are scalar, so no vector-memory wait)
+  int chunk_fast[MAX_CHUNKS];    // the chunk's columns all exist and its group is vec
 };
 
 struct RowGemmParams {

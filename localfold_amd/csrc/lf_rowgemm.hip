@@ -11,23 +11,23 @@ constexpr int LP_ROWS = 8 * 32;         // 8 waves x 32 rows
 // Loads chunk ci of the packed weights (a contiguous [64][KP] f16 block) into registers
 // (NREG 16-byte words per thread), to be stored into LDS later.
 template <int KP, int NREG>
-__device__ __forceinline__ void chunk_load(const LnProjParams& p, int ci, uint4 (&regs)[NREG], int tid) {
-  const uint4* src = reinterpret_cast<const uint4*>(p.wpk + (size_t)ci * 64 * KP);
+__device__ __forceinline__ void chunk_load(const LnProjParams& p, int ci, u32x4 (&regs)[NREG], int tid) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(p.wpk + (size_t)ci * 64 * KP);
 #pragma unroll
   for (int r = 0; r < NREG; ++r) {
     const int i = tid + r * 512;
-    regs[r] = i < 64 * KP / 8 ? src[i] : make_uint4(0, 0, 0, 0);
+    regs[r] = i < 64 * KP / 8 ? src[i] : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
 template <int KP, int NREG>
-__device__ __forceinline__ void chunk_store(_Float16* Ws, const uint4 (&regs)[NREG], int tid) {
+__device__ __forceinline__ void chunk_store(_Float16* Ws, const u32x4 (&regs)[NREG], int tid) {
   constexpr int SEGS = KP / 8, LDW = KP + 8;
 #pragma unroll
   for (int r = 0; r < NREG; ++r) {
     const int i = tid + r * 512;
     const int n = i / SEGS, seg = i - n * SEGS;
-    if (n < 64) *reinterpret_cast<uint4*>(Ws + n * LDW + seg * 8) = regs[r];
+    if (n < 64) *reinterpret_cast<u32x4*>(Ws + n * LDW + seg * 8) = regs[r];
   }
 }
 
@@ -42,22 +42,39 @@ __device__ __forceinline__ int dst_col32(const Dst& d, int col) {
   return (int)h * (int)d.sH + (int)e * (int)d.sD;
 }
 
-// Per-chunk epilogue table, built by wave 0 for the next chunk while the others work:
-// destination column offsets (-1 past the group's columns) and scaled biases of the chunk's
-// logical columns (64, or 32 gate/value pairs for SwiGLU).
+// Per-chunk epilogue table: destination column offsets (-1 past the group's columns) and
+// scaled biases of the chunk's logical columns (64, or 32 gate/value pairs for SwiGLU).  Every
+// wave loads the next chunk's biases with the weight prefetch (so the one wait for that
+// prefetch covers them) and wave 0 writes the table.
 struct ChunkTab {
   int cofs[64];
   float b0[64];
   float b1[64];
 };
 
-__device__ __forceinline__ void build_chunk_tab(ChunkTab& T, const LnProjParams& p, int ci, int lane) {
-  const Group& G = p.g[__builtin_amdgcn_readfirstlane(p.chunk_group[ci])];
-  const int c = __builtin_amdgcn_readfirstlane(p.chunk_c0[ci]) + lane;
+__device__ __forceinline__ void chunk_tab_load(const LnProjParams& p, int g, int c0, int lane, float& b0, float& b1) {
+  const Group& G = p.g[g];
+  const int c = min(c0 + lane, G.ncols - 1);
+  b0 = G.bias0 ? G.bias0[c] : 0.f;
+  b1 = G.bias1 ? G.bias1[c] : 0.f;
+}
+
+__device__ __forceinline__ void chunk_tab_put(ChunkTab& T, const LnProjParams& p, int g, int c0, int lane, float b0,
+                                              float b1) {
+  const Group& G = p.g[g];
+  const int c = c0 + lane;
   const bool ok = c < G.ncols;
   T.cofs[lane] = ok ? dst_col32(G.dst, c) : -1;
-  T.b0[lane] = ok && G.bias0 ? G.bias0[c] * G.scale : 0.f;
-  T.b1[lane] = ok && G.bias1 ? G.bias1[c] * G.scale : 0.f;
+  T.b0[lane] = ok ? b0 * G.scale : 0.f;
+  T.b1[lane] = ok ? b1 * G.scale : 0.f;
+}
+
+// Round-to-nearest-even f16 of 4 floats (two v_cvt_pk_f16_f32).
+__device__ __forceinline__ h4 pack_h4(const float (&v)[4]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const h2 lo = __builtin_convertvector((f2){v[0], v[1]}, h2);
+  const h2 hi = __builtin_convertvector((f2){v[2], v[3]}, h2);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
 }
 
 // Four consecutive logical columns of one row.  When every lane of the wave has its four
@@ -68,10 +85,7 @@ __device__ __forceinline__ void store4(_Float16* out, int rowpart, int4 co, bool
   const bool vec = row_ok && co.x >= 0 && co.y == co.x + 1 && co.z == co.x + 2 && co.w == co.x + 3 &&
                    ((rowpart + co.x) & 3) == 0;
   if (__all(vec)) {
-    h4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (_Float16)v[i];
-    *reinterpret_cast<h4*>(out + rowpart + co.x) = o;
+    *reinterpret_cast<h4*>(out + rowpart + co.x) = pack_h4(v);
   } else if (row_ok) {
     if (co.x >= 0) out[rowpart + co.x] = (_Float16)v[0];
     if (co.y >= 0) out[rowpart + co.y] = (_Float16)v[1];
@@ -80,14 +94,130 @@ __device__ __forceinline__ void store4(_Float16* out, int rowpart, int4 co, bool
   }
 }
 
+// Four consecutive rows of one logical column (the transposed tile): one vector store when
+// every lane's rows are valid, contiguous and 8-byte aligned in the destination.
+__device__ __forceinline__ void store4t(_Float16* out, int4 rp, int co, int nrow, const float (&v)[4]) {
+  const bool vec = nrow == 4 && co >= 0 && rp.y == rp.x + 1 && rp.z == rp.x + 2 && rp.w == rp.x + 3 &&
+                   ((rp.x + co) & 3) == 0;
+  if (__all(vec)) {
+    *reinterpret_cast<h4*>(out + rp.x + co) = pack_h4(v);
+  } else if (co >= 0) {
+    if (nrow > 0) out[rp.x + co] = (_Float16)v[0];
+    if (nrow > 1) out[rp.y + co] = (_Float16)v[1];
+    if (nrow > 2) out[rp.z + co] = (_Float16)v[2];
+    if (nrow > 3) out[rp.w + co] = (_Float16)v[3];
+  }
+}
+
+// Half a chunk's GEMM for both row tiles: acc[tt][u] is the 16x16 tile of row tile tt and
+// column tile tb + u*ts -- tiles 2th, 2th+1 (adjacent columns, so a half writes whole 64-byte
+// runs of a destination row and no line is left half-written for the other half), or th, th+2
+// for SwiGLU (gate and value).  TR puts the activation rows first (lane: rows 4*g4+i of column
+// r16), else the weight columns.
+template <int KS, bool TR>
+__device__ __forceinline__ void lnproj_mma(f4 (&acc)[2][2], const _Float16* W, const h8 (&xb)[2][KS], int tb, int ts,
+                                           int r16, int kq) {
+  constexpr int LDW = KS * 32 + 8;
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+    h8 w[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      w[u] = *reinterpret_cast<const h8*>(W + ((tb + ts * u) * 16 + r16) * LDW + 32 * j + kq);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        acc[tt][u] = TR ? mfma16(xb[tt][j], w[u], acc[tt][u]) : mfma16(w[u], xb[tt][j], acc[tt][u]);
+    }
+  }
+}
+
+// Half a chunk's epilogue for a wave: y = op(acc * scale + bias) for column tiles 2th and 2th+1
+// (SwiGLU: tile th = gate, th + 2 = value, one output tile), stored as f16.
+// The op and the tile orientation are template parameters, dispatched once per chunk.
+struct EpiArgs {
+  _Float16* out;
+  const int* Rp;        // destination row offsets of the block rows
+  const float* Rm;      // OP_ROWMASK multipliers of the block rows
+  const ChunkTab* T;
+  float scale;
+  int rows_left;        // rows of the block that exist (may exceed LP_ROWS)
+  int wrow;             // the wave's first block row
+  int r16, g4;
+};
+
+template <int OP>
+__device__ __forceinline__ float lnproj_op(float y, float value, float rmul) {
+  if (OP == OP_SWIGLU) return y * sigmoidf_(y) * value;
+  if (OP == OP_SIGMOID) return sigmoidf_(y);
+  if (OP == OP_RELU) return fmaxf(y, 0.f);
+  if (OP == OP_ROWMASK) return y * rmul;
+  return y;
+}
+
+template <int OP, bool TR, bool FAST>
+__device__ __forceinline__ void lnproj_epilogue(const f4 (&acc)[2][2], int th, const EpiArgs& a) {
+  const ChunkTab& T = *a.T;
+  {
+#pragma unroll
+    for (int u = 0; u < (OP == OP_SWIGLU ? 1 : 2); ++u) {
+      const int t = OP == OP_SWIGLU ? th : 2 * th + u;
+      if (TR) {
+        const int col = t * 16 + a.r16, co = T.cofs[col];
+        const float b0 = T.b0[col], b1 = T.b1[col];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int r0 = a.wrow + tt * 16 + 4 * a.g4;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[i] = lnproj_op<OP>(fmaf(acc[tt][u][i], a.scale, b0), fmaf(acc[tt][1][i], a.scale, b1),
+                                 OP == OP_ROWMASK ? a.Rm[r0 + i] : 1.f);
+          if (FAST) *reinterpret_cast<h4*>(a.out + (uint32_t)(a.Rp[r0] + co)) = pack_h4(v);
+          else store4t(a.out, *reinterpret_cast<const int4*>(&a.Rp[r0]), co, min(4, max(0, a.rows_left - r0)), v);
+        }
+      } else {
+        const int cc = t * 16 + 4 * a.g4;
+        const int4 co = *reinterpret_cast<const int4*>(&T.cofs[cc]);
+        const float4 bb = *reinterpret_cast<const float4*>(&T.b0[cc]);
+        const float b0s[4] = {bb.x, bb.y, bb.z, bb.w};
+        float b1s[4] = {0.f, 0.f, 0.f, 0.f};
+        if (OP == OP_SWIGLU) {
+          const float4 bv = *reinterpret_cast<const float4*>(&T.b1[cc]);
+          b1s[0] = bv.x; b1s[1] = bv.y; b1s[2] = bv.z; b1s[3] = bv.w;
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int r = a.wrow + tt * 16 + a.r16;
+          const float rmul = OP == OP_ROWMASK ? a.Rm[r] : 1.f;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[i] = lnproj_op<OP>(fmaf(acc[tt][u][i], a.scale, b0s[i]),
+                                 OP == OP_SWIGLU ? fmaf(acc[tt][1][i], a.scale, b1s[i]) : 0.f, rmul);
+          if (FAST) *reinterpret_cast<h4*>(a.out + (uint32_t)(a.Rp[r] + co.x)) = pack_h4(v);
+          else store4(a.out, a.Rp[r], co, r < a.rows_left, v);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
+    }
+  }
+}
+
+// 512 threads = 8 waves x 32 rows.  With K <= 256 the kernel fits 128 VGPRs, so two blocks
+// share a CU (the LDS holds two): the accumulators cover half a chunk at a time and the two
+// row tiles are LayerNorm'd one after the other.
 template <int ACT, int KS>
-__global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
+__global__ __launch_bounds__(512, 2) void lnproj_kernel(LnProjParams p) {
   constexpr int KP = KS * 32, LDW = KP + 8;
   constexpr int NREG = (64 * KP / 8 + 511) / 512;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[2][64 * LDW];
   __shared__ __attribute__((aligned(16))) float Gs[2 * KP];
   __shared__ __attribute__((aligned(16))) ChunkTab Tab[2];
   __shared__ int Rp[MAX_GROUPS][LP_ROWS];   // destination row offsets per group and block row
+  __shared__ float Rm[LP_ROWS];             // OP_ROWMASK multipliers of the block rows
+  __shared__ int Cg[MAX_CHUNKS], Cc[MAX_CHUNKS], Cf[MAX_CHUNKS];   // chunk -> group, first column, fast
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   stage_vec(Gs, p.ln_s, p.C, 1.f, KP, tid, 512);
@@ -96,122 +226,97 @@ __global__ __launch_bounds__(512) void lnproj_kernel(LnProjParams p) {
   const int per = (p.nchunks + (int)gridDim.y - 1) / (int)gridDim.y;
   const int ci0 = (int)blockIdx.y * per, ci1 = min(p.nchunks, ci0 + per);
   if (ci0 >= ci1) return;
-  uint4 regs[NREG];
+  for (int i = tid; i < p.nchunks; i += 512) {
+    Cg[i] = p.chunk_group[i];
+    Cc[i] = p.chunk_c0[i];
+    Cf[i] = p.chunk_fast[i];
+  }
+  u32x4 regs[NREG];
   chunk_load<KP, NREG>(p, ci0, regs, tid);
-  if (wave == 0) build_chunk_tab(Tab[0], p, ci0, lane);
+  {
+    const int g = __builtin_amdgcn_readfirstlane(p.chunk_group[ci0]);
+    const int c0 = __builtin_amdgcn_readfirstlane(p.chunk_c0[ci0]);
+    float b0, b1;
+    chunk_tab_load(p, g, c0, lane, b0, b1);
+    if (wave == 0) chunk_tab_put(Tab[0], p, g, c0, lane, b0, b1);
+  }
   const int row_block = blockIdx.x * LP_ROWS;
   for (int i = tid; i < p.ngroups * LP_ROWS; i += 512) {
     const int g = i / LP_ROWS, r = i - g * LP_ROWS;
     Rp[g][r] = row_block + r < p.rows ? dst_row32(p.g[g].dst, row_block + r) : 0;
   }
+  if (p.rowmask && tid < LP_ROWS) {
+    const int r = row_block + tid;
+    Rm[tid] = r < p.rows ? p.rowmask[p.rmB > 0 ? (r % p.rmQ) * p.rmB + r / p.rmQ : r] : 0.f;
+  }
 
   // this wave's two 16-row tiles, LayerNorm'd into B fragments
   const int rbase = row_block + wave * 32;
+  auto srow_of = [&](int r) { return p.rmB > 0 ? (r % p.rmQ) * p.rmB + r / p.rmQ : r; };
   h8 xb[2][KS];
-  int srow[2];
-  bool rvalid[2];
+  chunk_store<KP, NREG>(Ws[0], regs, tid);
+  __syncthreads();  // Gs, chunk 0, its table and the row offsets staged
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int myrow = rbase + tt * 16 + r16;
-    rvalid[tt] = myrow < p.rows;
-    const int lrow = rvalid[tt] ? myrow : 0;
-    srow[tt] = p.rmB > 0 ? (lrow % p.rmQ) * p.rmB + lrow / p.rmQ : lrow;
-  }
-  {
-    FragTile<ACT, KS> t0, t1;
-    frag_load_row(t0, p.x, (size_t)srow[0], p.C, lane);
-    frag_load_row(t1, p.x, (size_t)srow[1], p.C, lane);
-    chunk_store<KP, NREG>(Ws[0], regs, tid);
-    __syncthreads();  // Gs, chunk 0, its table and the row offsets staged
-    frag_ln_raw2(t0, t1, xb[0], xb[1], p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
-  }
-  float rm[2] = {1.f, 1.f};
-  if (p.rowmask) {
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) rm[tt] = p.rowmask[srow[tt]];
+    FragTile<ACT, KS> t0;
+    frag_load_row(t0, p.x, (size_t)srow_of(myrow < p.rows ? myrow : 0), p.C, lane);
+    frag_ln_raw1(t0, xb[tt], p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
   }
 
   for (int ci = ci0; ci < ci1; ++ci) {
     const int kb = (ci - ci0) & 1;   // LDS buffer of this chunk
     const _Float16* W = Ws[kb];
     const ChunkTab& T = Tab[kb];
-    if (ci + 1 < ci1) chunk_load<KP, NREG>(p, ci + 1, regs, tid);
-    f4 acc[2][4];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[tt][t] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KS; ++j) {
-      h8 w[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) w[t] = *reinterpret_cast<const h8*>(W + (t * 16 + r16) * LDW + 32 * j + kq);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[0][t] = mfma16(w[t], xb[0][j], acc[0][t]);
-        acc[1][t] = mfma16(w[t], xb[1][j], acc[1][t]);
-      }
-      __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
-    }
-    if (wave == 0 && ci + 1 < ci1) build_chunk_tab(Tab[kb ^ 1], p, ci + 1, lane);
-
+    // unconditional (the last iteration reloads its own chunk): with no branch around the
+    // prefetch the compiler's wait before the LDS store counts only this iteration's stores
+    const int cn = min(ci + 1, ci1 - 1);
+    chunk_load<KP, NREG>(p, cn, regs, tid);
     // wave-uniform by construction; readfirstlane lets the compiler keep them in SGPRs
-    const int gi = __builtin_amdgcn_readfirstlane(p.chunk_group[ci]);
+    const int gn = __builtin_amdgcn_readfirstlane(Cg[cn]), cn0 = __builtin_amdgcn_readfirstlane(Cc[cn]);
+    float tb0, tb1;
+    chunk_tab_load(p, gn, cn0, lane, tb0, tb1);
+    const int gi = __builtin_amdgcn_readfirstlane(Cg[ci]);
     const Group& G = p.g[gi];
+    const bool tr = __builtin_amdgcn_readfirstlane(G.tr) != 0;
+    // whole-block, whole-chunk, vector-aligned: the epilogue stores without checks
+    const bool fast = __builtin_amdgcn_readfirstlane(Cf[ci]) != 0 && p.rows - row_block >= LP_ROWS;
     _Float16* out = static_cast<_Float16*>(G.dst.ptr);
     const float scale = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(G.scale)));
     const int op = __builtin_amdgcn_readfirstlane(G.op);
-    int rowpart[2];
+
+    // per half: the GEMM, then (after half 0) the next chunk into the other LDS buffer -- its
+    // loads are waited for before this chunk's first store, so that wait never covers this
+    // chunk's stores -- then the half's epilogue
+    const EpiArgs ea{out, Rp[gi], Rm, &T, scale, p.rows - row_block, wave * 32, r16, g4};
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) rowpart[tt] = Rp[gi][wave * 32 + tt * 16 + r16];
-    if (op == OP_SWIGLU) {
+    for (int th = 0; th < 2; ++th) {
+      f4 acc[2][2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int cc = t * 16 + 4 * g4;
-        const int4 co = *reinterpret_cast<const int4*>(&T.cofs[cc]);
-        const float4 bg = *reinterpret_cast<const float4*>(&T.b0[cc]);
-        const float4 bv = *reinterpret_cast<const float4*>(&T.b1[cc]);
-        const float bgs[4] = {bg.x, bg.y, bg.z, bg.w}, bvs[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float gt = fmaf(acc[tt][t][i], scale, bgs[i]);
-            const float vl = fmaf(acc[tt][t + 2][i], scale, bvs[i]);
-            v[i] = gt * sigmoidf_(gt) * vl;
-          }
-          store4(out, rowpart[tt], co, rvalid[tt], v);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int tt = 0; tt < 2; ++tt) acc[tt][0] = acc[tt][1] = f4{0.f, 0.f, 0.f, 0.f};
+      const int tb = op == OP_SWIGLU ? th : 2 * th, ts = op == OP_SWIGLU ? 2 : 1;
+      if (tr) lnproj_mma<KS, true>(acc, W, xb, tb, ts, r16, kq);
+      else lnproj_mma<KS, false>(acc, W, xb, tb, ts, r16, kq);
+      if (th == 0) {
+        chunk_store<KP, NREG>(Ws[kb ^ 1], regs, tid);
+        if (wave == 0) chunk_tab_put(Tab[kb ^ 1], p, gn, cn0, lane, tb0, tb1);
       }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int cc = t * 16 + 4 * g4;
-        const int4 co = *reinterpret_cast<const int4*>(&T.cofs[cc]);
-        const float4 bb = *reinterpret_cast<const float4*>(&T.b0[cc]);
-        const float bs[4] = {bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float y = fmaf(acc[tt][t][i], scale, bs[i]);
-            if (op == OP_SIGMOID) y = sigmoidf_(y);
-            else if (op == OP_RELU) y = fmaxf(y, 0.f);
-            else if (op == OP_ROWMASK) y *= rm[tt];
-            v[i] = y;
-          }
-          store4(out, rowpart[tt], co, rvalid[tt], v);
-        }
-        __builtin_amdgcn_sched_barrier(0);   // one column tile's epilogue at a time
+      __builtin_amdgcn_sched_barrier(0);
+#define LF_EPI(OPV)                                                                          \
+  if (fast) tr ? lnproj_epilogue<OPV, true, true>(acc, th, ea) : lnproj_epilogue<OPV, false, true>(acc, th, ea); \
+  else tr ? lnproj_epilogue<OPV, true, false>(acc, th, ea) : lnproj_epilogue<OPV, false, false>(acc, th, ea);
+      switch (op) {
+        case OP_SIGMOID: LF_EPI(OP_SIGMOID) break;
+        case OP_RELU: LF_EPI(OP_RELU) break;
+        case OP_SWIGLU:
+          tr ? lnproj_epilogue<OP_SWIGLU, true, false>(acc, th, ea) : lnproj_epilogue<OP_SWIGLU, false, false>(acc, th, ea);
+          break;
+        case OP_ROWMASK: LF_EPI(OP_ROWMASK) break;
+        default: LF_EPI(OP_STORE) break;
       }
+#undef LF_EPI
     }
-    if (ci + 1 < ci1) {
-      chunk_store<KP, NREG>(Ws[kb ^ 1], regs, tid);
-      __syncthreads();
-    }
+    __syncthreads();
   }
 }
 
@@ -241,6 +346,11 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
                            (long long)((p.g[g].ncols - 1) / d.D) * d.sH +
                            (long long)std::min(p.g[g].ncols - 1, d.D - 1) * d.sD;
     if (span >= (1LL << 31)) return set_error(LF_ERR_INVALID, std::string(label) + ": destination above 2^31 elements");
+    const bool cols_contig = d.D % 4 == 0 && d.sD == 1;
+    const bool rows_contig = d.sN == 1 && d.Q % 4 == 0;
+    p.g[g].tr = !cols_contig && rows_contig;
+    const bool aligned8 = (reinterpret_cast<uintptr_t>(d.ptr) & 7) == 0 && d.sB % 4 == 0 && d.sH % 4 == 0;
+    p.g[g].vec = aligned8 && (p.g[g].tr ? d.sD % 4 == 0 : cols_contig && d.sN % 4 == 0);
   }
   // decode every group's weights into chunk order
   const int KP = 32 * lnproj_ks(p.C);
@@ -272,8 +382,9 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
     for (int c0 = 0; c0 < p.g[g].ncols; c0 += w) {
       if (p.nchunks == MAX_CHUNKS) return set_error(LF_ERR_INVALID, std::string(label) + ": too many output columns");
       if (c0 > 32767) return set_error(LF_ERR_INVALID, std::string(label) + ": group wider than 32767 columns");
-      p.chunk_group[p.nchunks] = (unsigned char)g;
-      p.chunk_c0[p.nchunks++] = (short)c0;
+      p.chunk_group[p.nchunks] = g;
+      p.chunk_fast[p.nchunks] = p.g[g].vec && c0 + w <= p.g[g].ncols;
+      p.chunk_c0[p.nchunks++] = c0;
     }
   }
   if (decode)

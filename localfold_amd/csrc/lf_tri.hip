@@ -921,7 +921,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     {
       FragTile<DT_F16, 4> x;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x.raw[j][0] = *reinterpret_cast<const uint4*>(Xc + r16 * O2_LD + 32 * j + kq);
+      for (int j = 0; j < 4; ++j) x.raw[j][0] = *reinterpret_cast<const u32x4*>(Xc + r16 * O2_LD + 32 * j + kq);
       frag_ln_raw1(x, ax, 128, Vs + 256, Vs + 384, p.eps_x, p.fast_var, lane);
     }
     {
