@@ -205,11 +205,12 @@ __device__ __forceinline__ void lnproj_epilogue(const f4 (&acc)[2][2], int th, c
   }
 }
 
-// 512 threads = 8 waves x 32 rows.  With K <= 256 the kernel fits 128 VGPRs, so two blocks
-// share a CU (the LDS holds two): the accumulators cover half a chunk at a time and the two
-// row tiles are LayerNorm'd one after the other.
+// 512 threads = 8 waves x 32 rows; the accumulators cover half a chunk at a time and the two
+// row tiles are LayerNorm'd one after the other.  With K <= 128 the kernel fits 128 VGPRs, so
+// two blocks share a CU (the LDS holds two); wider rows keep 256 (one block), since at 128 the
+// 64 registers of LayerNorm'd activations push the loop into spills.
 template <int ACT, int KS>
-__global__ __launch_bounds__(512, 2) void lnproj_kernel(LnProjParams p) {
+__global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjParams p) {
   constexpr int KP = KS * 32, LDW = KP + 8;
   constexpr int NREG = (64 * KP / 8 + 511) / 512;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[2][64 * LDW];
