@@ -54,6 +54,10 @@ struct FlashParams {
 // +-1e8 * log2(e).  Mathematically identical to exp(logit - max).
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float FA_CLAMP = 1e8f * LOG2E;
+// The running max is raised only when a chunk's scores exceed it by more than this (log2
+// units): until then p = exp2(x - m) <= 2^FA_RESCALE, well inside f16 range, and the
+// O rescale is skipped.
+constexpr float FA_RESCALE = 8.f;
 
 // kb[b][k] for k < Qp (keys padded to whole chunks): 1e9 log2(e) (mask - 1), and -1e30 past Q
 __global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* kb, int B, int Q, int Qp,
@@ -109,8 +113,9 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], in
 //
 // Online softmax with a lazy running max: after the first chunk, the S accumulators start at
 // bias - m (m = the query's running max), so the MFMA yields x - m directly; when no query's
-// maximum rose (a wave-uniform vote) p = exp2(x - m) needs no subtraction and O no rescale,
-// which is exactly the standard update with an unchanged max.  Otherwise (and in the first
+// maximum rose by more than FA_RESCALE (a wave-uniform vote) p = exp2(x - m) needs no
+// subtraction and O no rescale: the standard update with a stale max m, which only scales
+// numerator and denominator alike.  Otherwise (and in the first
 // chunk, and in chunks holding masked or past-the-end keys) the general update runs.  The
 // row sums come from the PV MFMAs themselves, through an all-ones operand (third d tile).
 //
@@ -157,6 +162,9 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     brow[qt] = BIAS ? bias + (size_t)qc[qt] * Qp + 16 * g4 : nullptr;
   }
   const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
+  // identity A operand of a 16x16x16 MFMA: lane supplies I[r16][4*g4 + j]
+  const h4 ident = h4{(_Float16)(r16 == 4 * g4), (_Float16)(r16 == 4 * g4 + 1), (_Float16)(r16 == 4 * g4 + 2),
+                      (_Float16)(r16 == 4 * g4 + 3)};
 
   // Staging: a chunk is 512 16-byte pieces: piece t < 256 is K row t/4 (dims 8(t%4) .. +8),
   // piece t >= 256 V^T row (t-256)/8 (keys 8((t-256)%8) .. +8).  Each thread stages NP pieces
@@ -262,14 +270,15 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
           for (int dt = 0; dt < 3; ++dt) o[dt][qt] = o[dt][qt] * corr;
         }
       } else {
-        // S accumulators start at bias - m, so the MFMA yields x - m
+        // S accumulators start at bias - m, so the MFMA yields x - m; the bias lands through an
+        // identity MFMA (D = I B + C, B = the lane's bias h4 in the accumulator layout)
         f4 s[QT][4];
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
+        for (int qt = 0; qt < QT; ++qt) {
+          const f4 negm = f4{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[qt][kt][i] = BIAS ? bias_add(bq[qt][kt], i, -m_run[qt]) : -m_run[qt];
+          for (int kt = 0; kt < 4; ++kt) s[qt][kt] = BIAS ? mfma16k16(ident, bq[qt][kt], negm) : negm;
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
           const h8 kf = *reinterpret_cast<const h8*>(&KV[buf][(kt * 16 + r16) * FA_KLD + kq]);
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) v = fmaxf(v, s[qt][kt][i]);
           mx[qt] = v;
-          rose |= v > 0.f;
+          rose |= v > FA_RESCALE;
         }
         if (!__any(rose)) {
 #pragma unroll

@@ -103,6 +103,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 
+// 16x16x16 f16 MFMA: lane l supplies A[l%16][4(l/16)+j] and B[4(l/16)+j][l%16], j < 4.
+__device__ __forceinline__ f4 mfma16k16(h4 a, h4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
