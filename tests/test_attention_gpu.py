@@ -48,6 +48,24 @@ def test_msa_row_attention_pair_bias(ctx, blockw, s, n):
     H.assert_close(out, ref, label=f"row {s}x{n}")
 
 
+def test_row_attention_keys_over_one_stage(ctx, blockw):
+    """600 keys (padded to 640): the kernel stages 512 keys in LDS at a time, so the second
+    stage (128 keys, the last ones masked) runs after a block-wide reload."""
+    from localfold_amd import capi, device as D
+    s, n = 2, 600
+    act = S.synthetic_activations(s, n, 256, 128, seed=6)
+    mask = np.ones((s, n), np.float32)
+    mask[:, -40:] = 0
+    mask[1, 100:130] = 0
+    row = blockw["msaRowAttention"]
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, row["attention"], row["pairBias"])
+    out, _, _ = _run(ctx, act["msa"], mask, ws, 8, False, capi.LF_BIAS_SEPARATE, act["pair"])
+    pb = dict(row["pairBias"], source="separate", activations=act["pair"])
+    ref = ops.attention_af2(act["msa"], mask, row["attention"], 8, False, pb)
+    H.assert_close(out, ref, label=f"row {s}x{n}")
+
+
 @pytest.mark.parametrize("s,n", [(5, 40), (33, 17)])
 def test_msa_column_attention(ctx, blockw, s, n):
     from localfold_amd import device as D
