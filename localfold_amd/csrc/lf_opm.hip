@@ -6,7 +6,8 @@
 //   lnproj    LN(msa) -> l, r stored [i][a][s] (sequence-contiguous: the contraction's K axis)
 //   count     den[i*N + j] = norm_eps + sum_s m_si m_sj
 //   outer     O[(i,j)][a*c + b] = sum_s l[i][a][s] r[j][b][s]: one NT GEMM of (N*c) x (N*c) x S on
-//             MFMA, 128x128 tiles, written pair-major f16 (the next GEMM's rows)
+//             MFMA, 256x256 tiles (128x128 when N*c is not a multiple of 256), written
+//             pair-major f16 (the next GEMM's rows)
 //   rowgemm   O W_out + b, / den, + pair residual
 #include <algorithm>
 #include <cmath>
@@ -55,47 +56,88 @@ __device__ __forceinline__ void ot_store(_Float16* Sm, const OtRegs& r, int tid)
 }
 
 // One 128x128 tile per block (4 waves of 64x64).  The 1-D grid is remapped so that each XCD
-// (block ids are dealt round-robin over 8) walks a contiguous band of row tiles, keeping
-// those L rows in its L2.  R is the MFMA A operand, so a lane holds four consecutive b of one
-// (i, a) row: 8-byte stores into the pair-major output.
+// (block ids are dealt round-robin over 8) owns a contiguous band of row tiles; when the band
+// is whole rows it is walked column by column, so the band's L tiles stay in the XCD's L2 and
+// each R tile is read from memory once per XCD, not once per row tile.  R is the MFMA A operand, so a lane holds four
+// consecutive b of one (i, a) row: 8-byte stores into the pair-major output.
+// FULL: N*co a multiple of 128 and S of 64, so every fetch is a whole in-range 16-byte load
+// from a per-thread base pointer.
+template <bool FULL>
 __global__ __launch_bounds__(256) void opm_outer_kernel(OuterParams p) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[OT * OT_LD];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[OT * OT_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][OT * OT_LD];   // double-buffered K steps
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][OT * OT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = p.N * p.co, tm = (M + OT - 1) / OT;
   const int total = (int)gridDim.x, per = total >> 3;
   int lin = (int)blockIdx.x;
-  if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
-  const int m0 = (lin / tm) * OT, n0 = (lin % tm) * OT;
+  int mt, nt;
+  if (lin < per * 8) {
+    const int x = lin & 7, q = lin >> 3;   // XCD x owns tiles [x*per, (x+1)*per) of row-major order
+    if (per % tm == 0) {                   // whole row tiles: walk the band column-major
+      const int rows = per / tm;
+      mt = x * rows + q % rows;
+      nt = q / rows;
+    } else {
+      const int t = x * per + q;
+      mt = t / tm;
+      nt = t % tm;
+    }
+  } else {
+    mt = lin / tm;
+    nt = lin % tm;
+  }
+  const int m0 = mt * OT, n0 = nt * OT;
   const bool vec = (p.S & 7) == 0;
   f4 acc[4][4];
   zero_acc(acc);
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   OtRegs ra, rb;
-  ot_fetch(ra, p.L, M, p.S, m0, 0, tid, vec);
-  ot_fetch(rb, p.R, M, p.S, n0, 0, tid, vec);
-  for (int k0 = 0; k0 < p.S; k0 += OT_BK) {
-    __syncthreads();
-    ot_store(As, ra, tid);
-    ot_store(Bs, rb, tid);
-    __syncthreads();
-    if (k0 + OT_BK < p.S) {
-      ot_fetch(ra, p.L, M, p.S, m0, k0 + OT_BK, tid, vec);
-      ot_fetch(rb, p.R, M, p.S, n0, k0 + OT_BK, tid, vec);
+  // FULL: thread tid loads rows (tid >> 3) + 32*it of each tile, k pieces (tid & 7)*8 .. +8
+  const _Float16* pa = p.L + (size_t)(m0 + (tid >> 3)) * p.S + (tid & 7) * 8;
+  const _Float16* pb = p.R + (size_t)(n0 + (tid >> 3)) * p.S + (tid & 7) * 8;
+  const size_t rstep = (size_t)32 * p.S;
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+    if constexpr (FULL) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        ra.v[it] = *reinterpret_cast<const h8*>(pa + it * rstep + k0);
+        rb.v[it] = *reinterpret_cast<const h8*>(pb + it * rstep + k0);
+      }
+    } else {
+      ot_fetch(ra, p.L, M, p.S, m0, k0, tid, vec);
+      ot_fetch(rb, p.R, M, p.S, n0, k0, tid, vec);
     }
+  };
+  // one barrier per K step: the next step's tiles are fetched before this step's MFMAs and
+  // written to the other buffer after them (every wave passed the barrier that ended that
+  // buffer's last use)
+  fetch(0);
+  ot_store(As[0], ra, tid);
+  ot_store(Bs[0], rb, tid);
+  __syncthreads();
+  for (int k0 = 0, kb = 0; k0 < p.S; k0 += OT_BK, kb ^= 1) {
+    const bool more = k0 + OT_BK < p.S;
+    if (more) fetch(k0 + OT_BK);
+    const _Float16* Ak = As[kb];
+    const _Float16* Bk = Bs[kb];
 #pragma unroll
     for (int kk = 0; kk < OT_BK; kk += 32) {
       h8 a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const h8*>(As + (wm * 64 + i * 16 + r16) * OT_LD + kk + kq);
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const h8*>(Ak + (wm * 64 + i * 16 + r16) * OT_LD + kk + kq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(Bs + (wn * 64 + j * 16 + r16) * OT_LD + kk + kq);
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(Bk + (wn * 64 + j * 16 + r16) * OT_LD + kk + kq);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(b[j], a[i], acc[i][j]);
     }
+    if (more) {
+      ot_store(As[kb ^ 1], ra, tid);
+      ot_store(Bs[kb ^ 1], rb, tid);
+    }
+    __syncthreads();
   }
   // acc[i][j][u]: row m = m0 + wm*64 + 16i + r16, columns n = n0 + wn*64 + 16j + 4g4 + u
   const unsigned co = (unsigned)p.co;
@@ -115,6 +157,111 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OuterParams p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) o[u] = (_Float16)acc[i][j][u];
       *reinterpret_cast<h4*>(p.O + rowpart + (long long)nj * cc + nb) = o;
+    }
+  }
+}
+
+// The outer-product GEMM with 256x256 tiles for whole tiles (N*co a multiple of 256, S of
+// 64): half the L2-to-CU operand traffic per flop of the 128x128 kernel, which the L2 latency
+// at the bytes a CU keeps in flight otherwise bounds.  512 threads = 8 waves of 128x64
+// (2 in m x 4 in n); K steps of 64 double-buffered in LDS (147 KB, one block per CU), the next
+// step fetched into registers during the current one's MFMAs.  Same XCD band order as above.
+constexpr int OB = 256;
+constexpr size_t OB_SMEM = (size_t)2 * 2 * OB * OT_LD * sizeof(_Float16);   // 147,456 bytes
+__global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 obs[];   // [2][A 256 x OT_LD | B 256 x OT_LD]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+  const int M = p.N * p.co, tm = M / OB;
+  const int total = (int)gridDim.x, per = total >> 3;
+  int lin = (int)blockIdx.x, mt, nt;
+  if (lin < per * 8) {
+    const int x = lin & 7, q = lin >> 3;
+    if (per % tm == 0) {
+      const int rows = per / tm;
+      mt = x * rows + q % rows;
+      nt = q / rows;
+    } else {
+      const int t = x * per + q;
+      mt = t / tm;
+      nt = t % tm;
+    }
+  } else {
+    mt = lin / tm;
+    nt = lin % tm;
+  }
+  const int m0 = mt * OB, n0 = nt * OB;
+  constexpr int STAGE = 2 * OB * OT_LD;
+  // thread tid loads rows (tid >> 3) + 64*it of each tile, k pieces (tid & 7)*8 .. +8
+  const _Float16* pa = p.L + (size_t)(m0 + (tid >> 3)) * p.S + (tid & 7) * 8;
+  const _Float16* pb = p.R + (size_t)(n0 + (tid >> 3)) * p.S + (tid & 7) * 8;
+  const size_t rstep = (size_t)64 * p.S;
+  h8 ra[4], rb[4];
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      ra[it] = *reinterpret_cast<const h8*>(pa + it * rstep + k0);
+      rb[it] = *reinterpret_cast<const h8*>(pb + it * rstep + k0);
+    }
+  };
+  auto put = [&](int buf) __attribute__((always_inline)) {
+    _Float16* A = obs + buf * STAGE;
+    _Float16* B = A + OB * OT_LD;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = (tid >> 3) + 64 * it, c = (tid & 7) * 8;
+      *reinterpret_cast<h8*>(A + r * OT_LD + c) = ra[it];
+      *reinterpret_cast<h8*>(B + r * OT_LD + c) = rb[it];
+    }
+  };
+  f4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int k0 = 0, kb = 0; k0 < p.S; k0 += OT_BK, kb ^= 1) {
+    const bool more = k0 + OT_BK < p.S;
+    if (more) fetch(k0 + OT_BK);
+    const _Float16* A = obs + kb * STAGE;
+    const _Float16* B = A + OB * OT_LD;
+#pragma unroll
+    for (int kk = 0; kk < OT_BK; kk += 32) {
+      h8 a[8], b[4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const h8*>(A + (wm * 128 + i * 16 + r16) * OT_LD + kk + kq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(B + (wn * 64 + j * 16 + r16) * OT_LD + kk + kq);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(b[j], a[i], acc[i][j]);
+    }
+    if (more) put(kb ^ 1);
+    __syncthreads();
+  }
+  // acc[i][j][u]: row m = m0 + wm*128 + 16i + r16, columns n = n0 + wn*64 + 16j + 4g4 + u
+  const unsigned co = (unsigned)p.co;
+  const long long cc = (long long)p.co * p.co;
+  long long colpart[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned n = (unsigned)(n0 + wn * 64 + j * 16 + 4 * g4), nj = n / co, nb = n - nj * co;
+    colpart[j] = (long long)nj * cc + nb;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const unsigned m = (unsigned)(m0 + wm * 128 + i * 16 + r16), mi = m / co, ma = m - mi * co;
+    const long long rowpart = (long long)mi * p.N * cc + (long long)ma * p.co;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h4 o;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[u] = (_Float16)acc[i][j][u];
+      *reinterpret_cast<h4*>(p.O + rowpart + colpart[j]) = o;
     }
   }
 }
@@ -142,6 +289,13 @@ __global__ __launch_bounds__(256) void opm_count_kernel(const float* mask, float
   }
   const int i = i0 + ty, j = j0 + tx;
   if (i < N && j < N) den[(size_t)i * N + j] = eps + acc;
+}
+
+// The big kernel's dynamic LDS (above the 64 KB default) is opted into once per process.
+static bool big_smem_ok(lf_context*) {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(opm_outer_big_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)OB_SMEM) == hipSuccess;
+  return ok;
 }
 
 int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
@@ -202,7 +356,14 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
     OuterParams op{L, R, O, N, co, S};
     const int tm = (N * co + OT - 1) / OT;
     LaunchScope ls(ctx, "opm.outer");
-    hipLaunchKernelGGL(opm_outer_kernel, dim3((unsigned)(tm * tm)), dim3(256), 0, ctx->stream, op);
+    const bool full = (N * co) % OT == 0 && S % OT_BK == 0;
+    const int tb = N * co / OB;
+    if ((N * co) % OB == 0 && S % OT_BK == 0 && big_smem_ok(ctx)) {
+      hipLaunchKernelGGL(opm_outer_big_kernel, dim3((unsigned)(tb * tb)), dim3(512), OB_SMEM, ctx->stream, op);
+    } else if (full)
+      hipLaunchKernelGGL(opm_outer_kernel<true>, dim3((unsigned)(tm * tm)), dim3(256), 0, ctx->stream, op);
+    else
+      hipLaunchKernelGGL(opm_outer_kernel<false>, dim3((unsigned)(tm * tm)), dim3(256), 0, ctx->stream, op);
   }
   LF_TRY(check_hip(hipGetLastError(), "opm outer launch"));
   {  // (O W_out + b) / den + residual

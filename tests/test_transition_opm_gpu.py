@@ -75,7 +75,7 @@ def test_transition_swiglu(ctx, c, n):
     H.assert_close(xt.cpu().numpy(), ref, label=f"swiglu {c}")
 
 
-@pytest.mark.parametrize("s,n", [(1, 16), (5, 37), (16, 64)])
+@pytest.mark.parametrize("s,n", [(1, 16), (5, 37), (16, 64), (64, 96), (128, 64)])
 def test_opm_af2(ctx, blockw, s, n):
     import torch
     from localfold_amd import device as D
