@@ -410,6 +410,36 @@ __device__ __forceinline__ void ld4v(const void* base, size_t idx, float (&v)[4]
   }
 }
 
+// Four activations as their storage words: loaded early, taken into registers (touch) at a
+// chosen point, converted when used.
+template <int ACT>
+struct Raw4v {
+  typedef uint2 T;
+  __device__ static T load(const void* base, size_t idx) {
+    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
+  }
+  __device__ static void touch(T& q) { asm volatile("" : "+v"(q.x), "+v"(q.y)); }
+  __device__ static void unpack(const T& q, float (&v)[4]) {
+    if constexpr (ACT == DT_F16) {
+      const h4 h = __builtin_bit_cast(h4, q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (float)h[i];
+    } else {
+      v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
+      v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct Raw4v<DT_F32> {
+  typedef float4 T;
+  __device__ static T load(const void* base, size_t idx) {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+  }
+  __device__ static void touch(T& q) { asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
+  __device__ static void unpack(const T& q, float (&v)[4]) { v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w; }
+};
+
 template <int ACT>
 __device__ __forceinline__ void st4v(void* base, size_t idx, const float (&v)[4]) {
   if constexpr (ACT == DT_F32) {

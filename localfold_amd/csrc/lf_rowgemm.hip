@@ -439,33 +439,6 @@ __device__ __forceinline__ void ld4(const void* base, int idx, float (&v)[4]) {
   }
 }
 
-// Four activations as their storage words (loaded early, converted when used).
-template <int DACT>
-struct Raw4 {
-  typedef uint2 T;
-  __device__ static T load(const void* base, int idx) {
-    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
-  }
-  __device__ static void touch(T& q) { asm volatile("" : "+v"(q.x), "+v"(q.y)); }
-  __device__ static void unpack(const T& q, float (&v)[4]) {
-    if constexpr (DACT == DT_F16) {
-      const h4 h = __builtin_bit_cast(h4, q);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (float)h[i];
-    } else {
-      v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
-      v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
-    }
-  }
-};
-template <>
-struct Raw4<DT_F32> {
-  typedef float4 T;
-  __device__ static T load(const void* base, int idx) { return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx); }
-  __device__ static void touch(T& q) { asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
-  __device__ static void unpack(const T& q, float (&v)[4]) { v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w; }
-};
-
 template <int DACT>
 __device__ __forceinline__ void st4(void* base, int idx, const float (&v)[4]) {
   if constexpr (DACT == DT_F32) {
@@ -579,7 +552,7 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
   // counter completes in order, so a load issued after stores would wait for them as well.
   int rowpart[2];
   float den[2];
-  typename Raw4<DACT>::T rr[2][NT];
+  typename Raw4v<DACT>::T rr[2][NT];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int row = rvalid[tt] ? rbase + tt * 16 + r16 : 0;
@@ -591,7 +564,7 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int c = min(col0 + wc * 16 * NT + t * 16 + 4 * g4, p.N - 4);   // clamped: never skipped
-        rr[tt][t] = Raw4<DACT>::load(p.resid, rowpart[tt] + c);
+        rr[tt][t] = Raw4v<DACT>::load(p.resid, rowpart[tt] + c);
       }
     }
   }
@@ -602,7 +575,7 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
     asm volatile("" : "+v"(den[tt]));
     if (p.resid) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) Raw4<DACT>::touch(rr[tt][t]);
+      for (int t = 0; t < NT; ++t) Raw4v<DACT>::touch(rr[tt][t]);
     }
   }
 #pragma unroll
@@ -625,7 +598,7 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
       }
       if (p.resid) {
         float r[4];
-        Raw4<DACT>::unpack(rr[tt][t], r);
+        Raw4v<DACT>::unpack(rr[tt][t], r);
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] += r[i];
       }
