@@ -224,6 +224,35 @@ typedef struct {
  * AF3 outerProductMean (cpu/af3/trunk/msa.js:72-155). */
 int lf_outer_product_mean(lf_context* ctx, const lf_opm_args* args);
 
+/* ---- global column attention (AF2 extra-MSA stack) ---------------------------------- */
+
+typedef struct {
+  const float *norm_scale, *norm_offset;  /* queryNormScale / queryNormOffset */
+  lf_weight wq;             /* [C x H*d] */
+  lf_weight wk, wv;         /* [C x d]: one key/value head shared by every query head */
+  lf_weight wg;             /* [C x H*d] */
+  const float* g_bias;      /* [H*d] */
+  lf_weight wo;             /* [H*d x C] */
+  const float* o_bias;      /* [C], optional */
+} lf_global_attention_weights;
+
+typedef struct {
+  int sequences, length, channels, heads;
+  int head_dim;             /* 0: channels / heads */
+  int act_dtype;
+  const void* act;          /* [S, N, C] */
+  const float* mask;        /* [S, N] */
+  void* out;                /* [S, N, C], act_dtype; may alias act when accumulate */
+  int accumulate;
+  float epsilon;            /* layer norm, 1e-5 */
+  const lf_global_attention_weights* w;
+} lf_global_attention_args;
+
+/* Replaces encodeGlobalAttention (webgpu/af2/evoformer/block.js:953-1030) and its kernels
+ * (block.js:88-400): per residue column, attention of the masked-mean query over the
+ * sequences (a masked sequence's logit is -1e9), gated per sequence, projected out. */
+int lf_global_column_attention(lf_context* ctx, const lf_global_attention_args* args);
+
 /* ---- blocks --------------------------------------------------------------------------- */
 
 typedef struct {
@@ -254,6 +283,24 @@ int lf_evoformer_block(lf_context* ctx, const lf_evoformer_block_args* args);
 
 /* Replaces EvoformerStackGpu.run (webgpu/af2/evoformer/stack.js:44-160): `blocks` blocks in order. */
 int lf_evoformer_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_evoformer_weights* blocks,
+                       int block_count);
+
+/* The extra-MSA block's weights: the Evoformer block's (column_attention and column_heads
+ * unused) with the global column attention in its place. */
+typedef struct {
+  lf_evoformer_weights base;
+  lf_global_attention_weights column_global;
+  int column_global_heads;
+} lf_extra_msa_weights;
+
+/* Replaces encodeExtraMsaBlock (webgpu/af2/evoformer/block.js:1715-1744): row attention with
+ * pair bias, global column attention, MSA transition, then the pair steps of
+ * encodeEvoformerPairBlock (block.js:1663-1713).  args->w is not read. */
+int lf_extra_msa_block(lf_context* ctx, const lf_evoformer_block_args* args, const lf_extra_msa_weights* w);
+
+/* Replaces ExtraMsaStackGpu.run (webgpu/af2/evoformer/stack.js:249-330): `block_count`
+ * extra-MSA blocks in order on the same msa and pair. */
+int lf_extra_msa_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_extra_msa_weights* blocks,
                        int block_count);
 
 typedef struct {

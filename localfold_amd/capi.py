@@ -85,6 +85,17 @@ class lf_opm_args(C.Structure):
                 ("epsilon", C.c_float), ("norm_epsilon", C.c_float), ("w", C.POINTER(lf_opm_weights))]
 
 
+class lf_global_attention_weights(C.Structure):
+    _fields_ = [("norm_scale", P), ("norm_offset", P), ("wq", lf_weight), ("wk", lf_weight), ("wv", lf_weight),
+                ("wg", lf_weight), ("g_bias", P), ("wo", lf_weight), ("o_bias", P)]
+
+
+class lf_global_attention_args(C.Structure):
+    _fields_ = [("sequences", C.c_int), ("length", C.c_int), ("channels", C.c_int), ("heads", C.c_int),
+                ("head_dim", C.c_int), ("act_dtype", C.c_int), ("act", P), ("mask", P), ("out", P),
+                ("accumulate", C.c_int), ("epsilon", C.c_float), ("w", C.POINTER(lf_global_attention_weights))]
+
+
 class lf_evoformer_weights(C.Structure):
     _fields_ = [("row_attention", lf_attention_weights), ("row_heads", C.c_int),
                 ("column_attention", lf_attention_weights), ("column_heads", C.c_int),
@@ -101,6 +112,11 @@ class lf_evoformer_block_args(C.Structure):
                 ("msa_dtype", C.c_int), ("msa", P), ("pair_dtype", C.c_int), ("pair", P),
                 ("msa_mask", P), ("pair_mask", P), ("epsilon", C.c_float),
                 ("w", C.POINTER(lf_evoformer_weights))]
+
+
+class lf_extra_msa_weights(C.Structure):
+    _fields_ = [("base", lf_evoformer_weights), ("column_global", lf_global_attention_weights),
+                ("column_global_heads", C.c_int)]
 
 
 class lf_pairformer_weights(C.Structure):
@@ -141,7 +157,10 @@ PROTOTYPES = [
     ("lf_attention", C.c_int, [P, C.POINTER(lf_attention_args)]),
     ("lf_transition", C.c_int, [P, C.POINTER(lf_transition_args)]),
     ("lf_outer_product_mean", C.c_int, [P, C.POINTER(lf_opm_args)]),
+    ("lf_global_column_attention", C.c_int, [P, C.POINTER(lf_global_attention_args)]),
     ("lf_evoformer_block", C.c_int, [P, C.POINTER(lf_evoformer_block_args)]),
+    ("lf_extra_msa_block", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights)]),
+    ("lf_extra_msa_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights), C.c_int]),
     ("lf_evoformer_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
     ("lf_pairformer_block", C.c_int, [P, C.POINTER(lf_pairformer_block_args)]),
 ]

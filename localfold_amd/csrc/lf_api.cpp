@@ -266,6 +266,9 @@ inline int impl_lf_tri_mult(lf_context* c, const lf_tri_mult_args& a) { return t
 inline int impl_lf_attention(lf_context* c, const lf_attention_args& a) { return attention(c, a); }
 inline int impl_lf_transition(lf_context* c, const lf_transition_args& a) { return transition(c, a); }
 inline int impl_lf_outer_product_mean(lf_context* c, const lf_opm_args& a) { return outer_product_mean(c, a); }
+inline int impl_lf_global_column_attention(lf_context* c, const lf_global_attention_args& a) {
+  return global_attention(c, a);
+}
 }  // namespace lf
 
 extern "C" {
@@ -273,4 +276,5 @@ LF_ENTRY(lf_tri_mult, lf_tri_mult_args)
 LF_ENTRY(lf_attention, lf_attention_args)
 LF_ENTRY(lf_transition, lf_transition_args)
 LF_ENTRY(lf_outer_product_mean, lf_opm_args)
+LF_ENTRY(lf_global_column_attention, lf_global_attention_args)
 }

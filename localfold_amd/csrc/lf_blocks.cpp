@@ -10,7 +10,10 @@
 
 namespace lf {
 
-static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, const lf_evoformer_weights& w) {
+// The Evoformer block; with `global` the extra-MSA block (encodeExtraMsaBlock,
+// webgpu/af2/evoformer/block.js:1715-1744), whose step 2 is the global column attention.
+static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, const lf_evoformer_weights& w,
+                           const lf_global_attention_weights* global = nullptr, int global_heads = 0) {
   LF_REQUIRE(a.sequences > 0 && a.length > 0 && a.c_m > 0 && a.c_z > 0, "evoformer block dimensions must be positive");
   LF_REQUIRE(a.msa && a.pair && a.msa_mask && a.pair_mask, "evoformer block: NULL activation or mask");
   const float eps = a.epsilon > 0.f ? a.epsilon : 1e-5f;
@@ -36,7 +39,22 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     StageScope stage(ctx, "row_attention");
     LF_TRY(attention(ctx, x));
   }
-  {  // 2. MSA column attention
+  if (global) {  // 2. global column attention (extra-MSA block)
+    lf_global_attention_args x{};
+    x.sequences = a.sequences;
+    x.length = a.length;
+    x.channels = a.c_m;
+    x.heads = global_heads;
+    x.act_dtype = a.msa_dtype;
+    x.act = a.msa;
+    x.mask = a.msa_mask;
+    x.out = a.msa;
+    x.accumulate = 1;
+    x.epsilon = eps;
+    x.w = global;
+    StageScope stage(ctx, "global_column_attention");
+    LF_TRY(global_attention(ctx, x));
+  } else {  // 2. MSA column attention
     lf_attention_args x{};
     x.batch = a.length;
     x.queries = a.sequences;
@@ -273,6 +291,22 @@ int lf_evoformer_stack(lf_context* ctx, const lf_evoformer_block_args* args, con
   if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_stack: negative block count");
   hipSetDevice(ctx->device);
   for (int i = 0; i < block_count; ++i) LF_TRY(lf::evoformer_block(ctx, *args, blocks[i]));
+  return LF_OK;
+}
+
+int lf_extra_msa_block(lf_context* ctx, const lf_evoformer_block_args* args, const lf_extra_msa_weights* w) {
+  if (!ctx || !args || !w) return lf::set_error(LF_ERR_INVALID, "lf_extra_msa_block: NULL argument");
+  hipSetDevice(ctx->device);
+  return lf::evoformer_block(ctx, *args, w->base, &w->column_global, w->column_global_heads);
+}
+
+int lf_extra_msa_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_extra_msa_weights* blocks,
+                       int block_count) {
+  if (!ctx || !args || (!blocks && block_count > 0)) return lf::set_error(LF_ERR_INVALID, "lf_extra_msa_stack: NULL argument");
+  if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_extra_msa_stack: negative block count");
+  hipSetDevice(ctx->device);
+  for (int b = 0; b < block_count; ++b)
+    LF_TRY(lf::evoformer_block(ctx, *args, blocks[b].base, &blocks[b].column_global, blocks[b].column_global_heads));
   return LF_OK;
 }
 

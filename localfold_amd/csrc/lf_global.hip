@@ -1,0 +1,209 @@
+// Global column attention of the AF2 extra-MSA stack: encodeGlobalAttention
+// (webgpu/af2/evoformer/block.js:953-1030) and its kernels (block.js:88-400).  Per residue
+// column i, over the sequences s, with x = LN(msa):
+//   k_si = x_si Wk, v_si = x_si Wv (one head of width d shared by every query head),
+//   q_ih = (sum_s m_si x_si / (1e-10 + sum_s m_si)) Wq_h / sqrt(d),
+//   a_ih = sum_s softmax_s(q_ih . k_si, -1e9 where m_si = 0) v_si,
+//   update_si = (sigmoid(x_si Wg + bg) * a_i) Wo + bo.
+//
+// Kernels:
+//   lnproj   LN(msa) -> qm = m * (x Wq) [N][S][H*d], k, v [N][S][d] (column-contiguous), gate
+//            sigmoid(x Wg + bg) [S*N][H*d]; the mean of qm over s is q (the projection is
+//            linear, so projecting then averaging equals the reference's average then project)
+//   column   one block per column: the mask count, q, an online softmax over the sequences
+//            (each thread a stride of sequences, merged over lanes and waves), then the gate
+//            rows of the column multiplied in place by a_i
+//   rowgemm  gate Wo + bo, + residual
+#include <algorithm>
+#include <cmath>
+
+#include "lf_rowgemm.h"
+
+namespace lf {
+
+constexpr int GA_MAXHD = 64;   // heads * head_dim supported by the column kernel
+constexpr int GA_NT = 256;
+
+struct GlobalColumnParams {
+  const _Float16 *qm, *k, *v;   // [N][S][Hd], [N][S][d], [N][S][d]
+  _Float16* gate;               // [S*N][Hd], multiplied in place by the column's attended values
+  const float* mask;            // [S][N]
+  int S, N, H, d;
+  float scale;                  // 1/sqrt(d)
+};
+
+// Merges an online-softmax state (m, l, acc) with another one.
+template <int D>
+__device__ __forceinline__ void sm_merge(float& m, float& l, float (&acc)[D], float m2, float l2, const float (&acc2)[D]) {
+  const float mx = fmaxf(m, m2);
+  const float a = __expf(m - mx), b = __expf(m2 - mx);
+  l = l * a + l2 * b;
+#pragma unroll
+  for (int e = 0; e < D; ++e) acc[e] = acc[e] * a + acc2[e] * b;
+  m = mx;
+}
+
+template <int D>
+__global__ __launch_bounds__(GA_NT) void global_column_kernel(GlobalColumnParams p) {
+  __shared__ float part[4][GA_MAXHD];
+  __shared__ float qs[GA_MAXHD];
+  __shared__ float wstate[4][GA_MAXHD / 1 + 16];   // per wave: acc [H*D], then max [H], sum [H]
+  __shared__ float att[GA_MAXHD];
+  __shared__ float cnt[4];
+  const int i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = p.S, N = p.N, H = p.H, Hd = H * D;
+
+  // the column's mask count
+  float c = 0.f;
+  for (int s = tid; s < S; s += GA_NT) c += p.mask[(size_t)s * N + i];
+  c = wave_sum(c);
+  if (lane == 0) cnt[wave] = c;
+  // q: the masked mean of qm over the sequences, four sequence phases per output
+  for (int e = tid; e < 4 * Hd; e += GA_NT) {
+    const int hd = e % Hd, ph = e / Hd;
+    float t = 0.f;
+    for (int s = ph; s < S; s += 4) t += (float)p.qm[((size_t)i * S + s) * Hd + hd];
+    part[ph][hd] = t;
+  }
+  __syncthreads();
+  const float den = 1e-10f + cnt[0] + cnt[1] + cnt[2] + cnt[3];
+  for (int hd = tid; hd < Hd; hd += GA_NT)
+    qs[hd] = (part[0][hd] + part[1][hd] + part[2][hd] + part[3][hd]) / den * p.scale;
+  __syncthreads();
+
+  // online softmax over this thread's sequences, per head
+  for (int h = 0; h < H; ++h) {
+    float q[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) q[e] = qs[h * D + e];
+    float m = -1e30f, l = 0.f, acc[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) acc[e] = 0.f;
+    for (int s = tid; s < S; s += GA_NT) {
+      const _Float16* kr = p.k + ((size_t)i * S + s) * D;
+      const _Float16* vr = p.v + ((size_t)i * S + s) * D;
+      float logit = 0.f;
+#pragma unroll
+      for (int e = 0; e < D; ++e) logit += q[e] * (float)kr[e];
+      if (p.mask[(size_t)s * N + i] == 0.f) logit = -1e9f;
+      const float mx = fmaxf(m, logit);
+      const float a = __expf(m - mx), w = __expf(logit - mx);
+      l = l * a + w;
+#pragma unroll
+      for (int e = 0; e < D; ++e) acc[e] = acc[e] * a + w * (float)vr[e];
+      m = mx;
+    }
+    // merge over the wave's lanes
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      float acc2[D];
+#pragma unroll
+      for (int e = 0; e < D; ++e) acc2[e] = __shfl_xor(acc[e], o, WAVE);
+      sm_merge<D>(m, l, acc, __shfl_xor(m, o, WAVE), __shfl_xor(l, o, WAVE), acc2);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int e = 0; e < D; ++e) wstate[wave][h * D + e] = acc[e];
+      wstate[wave][Hd + h] = m;
+      wstate[wave][Hd + 8 + h] = l;
+    }
+  }
+  __syncthreads();
+  // merge the four waves: thread hd < Hd finishes one attended value
+  for (int hd = tid; hd < Hd; hd += GA_NT) {
+    const int h = hd / D;
+    float m = wstate[0][Hd + h], l = wstate[0][Hd + 8 + h], a = wstate[0][hd];
+    for (int w2 = 1; w2 < 4; ++w2) {
+      const float m2 = wstate[w2][Hd + h], l2 = wstate[w2][Hd + 8 + h], a2 = wstate[w2][hd];
+      const float mx = fmaxf(m, m2), x1 = __expf(m - mx), x2 = __expf(m2 - mx);
+      l = l * x1 + l2 * x2;
+      a = a * x1 + a2 * x2;
+      m = mx;
+    }
+    att[hd] = a / l;
+  }
+  __syncthreads();
+  // gate rows of this column times the attended values, in place
+  for (int e = tid; e < S * Hd; e += GA_NT) {
+    const int s = e / Hd, hd = e - s * Hd;
+    _Float16* g = p.gate + ((size_t)s * N + i) * Hd + hd;
+    *g = (_Float16)((float)*g * att[hd]);
+  }
+}
+
+int global_attention(lf_context* ctx, const lf_global_attention_args& a) {
+  LF_REQUIRE(a.w != nullptr, "global column attention: weights are NULL");
+  LF_REQUIRE(a.sequences > 0 && a.length > 0 && a.channels > 0 && a.heads > 0,
+             "global column attention dimensions must be positive");
+  LF_REQUIRE(act_dtype_ok(a.act_dtype), "global column attention: act_dtype must be f32, f16 or bf16");
+  LF_REQUIRE(a.act && a.mask && a.out, "global column attention: act, mask and out must be device pointers");
+  LF_REQUIRE(a.channels <= 384 && a.channels % 4 == 0, "global column attention: channels must be a multiple of 4, <= 384");
+  if (a.head_dim == 0)
+    LF_REQUIRE(a.channels % a.heads == 0, "global column attention: channels must be a multiple of heads when head_dim is 0");
+  const int S = a.sequences, N = a.length, C = a.channels, H = a.heads;
+  const int d = a.head_dim > 0 ? a.head_dim : C / H, Hd = H * d;
+  LF_REQUIRE(d == 8 || d == 16 || d == 32, "global column attention: head dimension must be 8, 16 or 32");
+  LF_REQUIRE(Hd <= GA_MAXHD && H <= 8, "global column attention: heads * head_dim must be <= 64 and heads <= 8");
+  LF_REQUIRE(a.epsilon > 0.f && std::isfinite(a.epsilon), "global column attention: epsilon must be finite and positive");
+  const long long rows = (long long)S * N;
+  LF_REQUIRE(rows * std::max(Hd, C) < (1LL << 31), "global column attention: too many rows");
+  const lf_global_attention_weights& w = *a.w;
+
+  WView views[5];
+  LF_TRY(make_view(w.wq, C, Hd, "queryWeight", &views[0]));
+  LF_TRY(make_view(w.wk, C, d, "keyWeight", &views[1]));
+  LF_TRY(make_view(w.wv, C, d, "valueWeight", &views[2]));
+  LF_TRY(make_view(w.wg, C, Hd, "gatingWeight", &views[3]));
+  LF_TRY(make_view(w.wo, Hd, C, "outputWeight", &views[4]));
+
+  LnProjParams pp{};
+  pp.x = a.act;
+  pp.rows = (int)rows;
+  pp.C = C;
+  pp.ln_s = w.norm_scale;
+  pp.ln_o = w.norm_offset;
+  pp.eps = a.epsilon;
+  pp.rowmask = a.mask;   // storage row s*N + i is mask[s][i]
+  pp.g[0] = Group{views[0], WView{}, Hd, OP_ROWMASK, 1.f, nullptr, nullptr, Dst{}};
+  pp.g[1] = Group{views[1], WView{}, d, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  pp.g[2] = Group{views[2], WView{}, d, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  pp.g[3] = Group{views[3], WView{}, Hd, OP_SIGMOID, 1.f, w.g_bias, nullptr, Dst{}};
+  pp.ngroups = 4;
+
+  const size_t qb = (size_t)rows * Hd * sizeof(_Float16), kb = (size_t)rows * d * sizeof(_Float16);
+  size_t sizes[6] = {qb, kb, kb, qb, expanded_bytes(views[4]), lnproj_packed_bytes(pp)};
+  void* bufs[6];
+  LF_TRY(workspace(ctx, sizes, bufs, 6));
+  _Float16 *QM = (_Float16*)bufs[0], *K = (_Float16*)bufs[1], *V = (_Float16*)bufs[2], *G = (_Float16*)bufs[3];
+  // logical row r = s*N + i (the storage row); column-contiguous [i][s][.] for qm, k, v
+  pp.g[0].dst = Dst{QM, DT_F16, N, (long long)Hd, (long long)S * Hd, Hd, 0, 1};
+  pp.g[1].dst = Dst{K, DT_F16, N, (long long)d, (long long)S * d, d, 0, 1};
+  pp.g[2].dst = Dst{V, DT_F16, N, (long long)d, (long long)S * d, d, 0, 1};
+  pp.g[3].dst = dst_rowmajor(G, DT_F16, (int)rows, Hd);
+  LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[5], "global.project"));
+
+  GlobalColumnParams gp{QM, K, V, G, a.mask, S, N, H, d, 1.f / std::sqrt((float)d)};
+  {
+    LaunchScope ls(ctx, "global.column");
+    if (d == 8) hipLaunchKernelGGL(global_column_kernel<8>, dim3(N), dim3(GA_NT), 0, ctx->stream, gp);
+    else if (d == 16) hipLaunchKernelGGL(global_column_kernel<16>, dim3(N), dim3(GA_NT), 0, ctx->stream, gp);
+    else hipLaunchKernelGGL(global_column_kernel<32>, dim3(N), dim3(GA_NT), 0, ctx->stream, gp);
+  }
+  LF_TRY(check_hip(hipGetLastError(), "global column launch"));
+
+  WExp wo;
+  LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[4], &wo, "global.expand"));
+  RowGemmParams rp{};
+  rp.A = G;
+  rp.rows = (int)rows;
+  rp.K = Hd;
+  rp.N = C;
+  rp.w = wo;
+  rp.bias = w.o_bias;
+  rp.op = OP_STORE;
+  rp.resid = a.accumulate ? a.act : nullptr;
+  rp.dst = dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+  return launch_rowgemm(ctx, rp, "global.output");
+}
+
+}  // namespace lf

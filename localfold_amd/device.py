@@ -367,6 +367,39 @@ def outer_product_mean(ctx: Context, msa: torch.Tensor, mask: torch.Tensor, wstr
     return out
 
 
+def global_attention_weights(dw: DeviceWeights, w: dict) -> capi.lf_global_attention_weights:
+    """Global column attention (`encodeGlobalAttention`, `webgpu/af2/evoformer/block.js:963-980`):
+    queryNorm, queryWeight [C, H*d], keyWeight / valueWeight [C, d], gatingWeight [C, H*d] +
+    gatingBias, outputWeight [H*d, C] + outputBias, all (in,out)."""
+    s = capi.lf_global_attention_weights()
+    s.norm_scale, s.norm_offset = dw.vec(w["queryNormScale"]), dw.vec(w["queryNormOffset"])
+    s.wq = dw.weight(w["queryWeight"], capi.LF_IN_OUT)
+    s.wk = dw.weight(w["keyWeight"], capi.LF_IN_OUT)
+    s.wv = dw.weight(w["valueWeight"], capi.LF_IN_OUT)
+    s.wg = dw.weight(w["gatingWeight"], capi.LF_IN_OUT)
+    s.g_bias = dw.vec(w["gatingBias"])
+    s.wo = dw.weight(w["outputWeight"], capi.LF_IN_OUT)
+    s.o_bias = dw.vec(w.get("outputBias"))
+    return s
+
+
+def global_column_attention(ctx: Context, msa: torch.Tensor, mask: torch.Tensor,
+                            wstruct: capi.lf_global_attention_weights, heads: int, out: torch.Tensor = None,
+                            accumulate: bool = False, head_dim: int = 0, epsilon: float = 1e-5) -> torch.Tensor:
+    """msa [S, N, C], mask [S, N]: the update (or msa + update with accumulate) into `out`."""
+    s_, n, c = msa.shape
+    if out is None:
+        out = torch.empty_like(msa)
+    a = capi.lf_global_attention_args()
+    a.sequences, a.length, a.channels, a.heads, a.head_dim = s_, n, c, heads, head_dim
+    a.act_dtype, a.act, a.mask, a.out = act_code(msa), ptr(msa), ptr(mask), ptr(out)
+    a.accumulate = int(accumulate)
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_global_column_attention(ctx.handle, C.byref(a)))
+    return out
+
+
 # ---------------------------------------------------------------------------------------
 # Blocks
 # ---------------------------------------------------------------------------------------
@@ -378,9 +411,10 @@ def evoformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_evoformer_weights:
     row = w["msaRowAttention"]
     s.row_attention = attention_weights_af2(dw, row["attention"], row["pairBias"])
     s.row_heads = row["heads"]
-    col = w["msaColumnAttention"]
-    s.column_attention = attention_weights_af2(dw, col["attention"])
-    s.column_heads = col["heads"]
+    col = w.get("msaColumnAttention")   # absent in an extra-MSA block (global attention instead)
+    if col is not None:
+        s.column_attention = attention_weights_af2(dw, col["attention"])
+        s.column_heads = col["heads"]
     s.msa_transition = transition_weights(dw, w["msaTransition"])
     s.outer_product_mean = opm_weights(dw, w["outerProductMean"])
     s.tri_out = tri_mult_weights(dw, w["triangleMultiplicationOutgoing"])
@@ -435,6 +469,29 @@ def evoformer_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: 
     a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w0, epsilon)
     arr = (capi.lf_evoformer_weights * len(wstructs))(*wstructs)
     check(ctx.lib.lf_evoformer_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
+
+
+def extra_msa_weights(dw: DeviceWeights, w: dict) -> capi.lf_extra_msa_weights:
+    """An extra-MSA block's weights: the Evoformer structure with `msaColumnGlobalAttention`."""
+    s = capi.lf_extra_msa_weights()
+    s.base = evoformer_weights(dw, w)
+    g = w["msaColumnGlobalAttention"]
+    s.column_global = global_attention_weights(dw, g["attention"])
+    s.column_global_heads = g["heads"]
+    return s
+
+
+def extra_msa_block(ctx: Context, msa, pair, msa_mask, pair_mask, wstruct, w: dict, epsilon: float = 1e-5):
+    """One AF2 extra-MSA block (`encodeExtraMsaBlock`), msa and pair updated in place."""
+    a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w, epsilon)
+    check(ctx.lib.lf_extra_msa_block(ctx.handle, C.byref(a), C.byref(wstruct)))
+
+
+def extra_msa_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: dict, epsilon: float = 1e-5):
+    """`len(wstructs)` extra-MSA blocks in order (ExtraMsaStackGpu.run), in place."""
+    a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w0, epsilon)
+    arr = (capi.lf_extra_msa_weights * len(wstructs))(*wstructs)
+    check(ctx.lib.lf_extra_msa_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
 
 
 def pairformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_pairformer_weights:

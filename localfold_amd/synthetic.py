@@ -187,6 +187,39 @@ def synthetic_block_weights(c_m: int, c_z: int, c_outer: int, heads_msa: int, he
     return w
 
 
+def synthetic_global_attention_weights(c_m: int, heads: int, seed: int = 5) -> dict:
+    """Global column attention weights in the layout `encodeGlobalAttention` uploads
+    (`webgpu/af2/evoformer/block.js:963-980`): queryWeight [C, H*d], key/value [C, d] with
+    d = C / heads, gating [C, H*d] + bias, output [H*d, C] + bias, all (in,out)."""
+    s = Stream(seed)
+    noise = s.values
+    d = c_m // heads
+    r = 1.0 / np.sqrt(c_m)
+    return {"heads": heads, "attention": {
+        "queryNormScale": noise(c_m, 0.2, 1),
+        "queryNormOffset": noise(c_m, 0.1),
+        "queryWeight": noise(c_m * heads * d, r).reshape(c_m, heads * d),
+        "keyWeight": noise(c_m * d, r).reshape(c_m, d),
+        "valueWeight": noise(c_m * d, r).reshape(c_m, d),
+        "gatingWeight": noise(c_m * heads * d, r).reshape(c_m, heads * d),
+        "gatingBias": noise(heads * d, 0.1, 1),
+        "outputWeight": noise(heads * d * c_m, 1 / np.sqrt(heads * d)).reshape(heads * d, c_m),
+        "outputBias": noise(c_m, 0.05),
+    }}
+
+
+def synthetic_extra_msa_block_weights(c_m: int = 64, c_z: int = 128, c_outer: int = 32, heads_msa: int = 8,
+                                      heads_pair: int = 4, tri_hidden: int = 128, msa_hidden: int = 256,
+                                      pair_hidden: int = 512, seed: int = 11) -> dict:
+    """An AF2 extra-MSA block (`encodeExtraMsaBlock`, `webgpu/af2/evoformer/block.js:1715-1744`):
+    the main block's weights with `msaColumnGlobalAttention` in place of `msaColumnAttention`
+    (AF2 extra MSA: c_m 64, 8 heads of 8)."""
+    w = synthetic_block_weights(c_m, c_z, c_outer, heads_msa, heads_pair, tri_hidden, msa_hidden, pair_hidden, seed)
+    del w["msaColumnAttention"]
+    w["msaColumnGlobalAttention"] = synthetic_global_attention_weights(c_m, heads_msa, seed + 1000)
+    return w
+
+
 def synthetic_activations(sequences: int, length: int, c_m: int, c_z: int, seed: int = 9) -> dict:
     """`syntheticActivations` (`tools/gpu/af2-synthetic-block.js:141-162`)."""
     s = Stream(seed)

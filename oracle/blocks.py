@@ -28,6 +28,25 @@ def evoformer_block_af2(msa, pair, msa_mask, pair_mask, w, eps=1e-5):
     # column attention: batch = residues, queries = sequences, transposed storage [S, N, C]
     msa = _add(msa, ops.attention_af2(msa, msa_mask, col["attention"], col["heads"], True, None, eps))
     msa = _add(msa, ops.transition_af2(msa, w["msaTransition"], eps))
+    return msa, _pair_steps(msa, pair, msa_mask, pair_mask, w, eps)
+
+
+def extra_msa_block_af2(msa, pair, msa_mask, pair_mask, w, eps=1e-5):
+    """One AF2 extra-MSA block (`encodeExtraMsaBlock`, `webgpu/af2/evoformer/block.js:1715-1744`):
+    the Evoformer block with the column attention replaced by global column attention
+    (`w["msaColumnGlobalAttention"]`), then `encodeEvoformerPairBlock` (`:1663-1713`).
+    Returns (msa, pair)."""
+    row = w["msaRowAttention"]
+    pb = dict(row["pairBias"], source="separate", activations=pair)
+    msa = _add(msa, ops.attention_af2(msa, msa_mask, row["attention"], row["heads"], False, pb, eps))
+    g = w["msaColumnGlobalAttention"]
+    msa = _add(msa, ops.global_column_attention_af2(msa, msa_mask, g["attention"], g["heads"], eps))
+    msa = _add(msa, ops.transition_af2(msa, w["msaTransition"], eps))
+    return msa, _pair_steps(msa, pair, msa_mask, pair_mask, w, eps)
+
+
+def _pair_steps(msa, pair, msa_mask, pair_mask, w, eps):
+    """OPM, triangle multiplication out/in, triangle attention start/end, pair transition."""
     pair = _add(pair, ops.outer_product_mean_af2(msa, msa_mask, w["outerProductMean"], eps))
     pair = _add(pair, ops.tri_mult_af2(pair, pair_mask, w["triangleMultiplicationOutgoing"], "outgoing", eps))
     pair = _add(pair, ops.tri_mult_af2(pair, pair_mask, w["triangleMultiplicationIncoming"], "incoming", eps))
@@ -37,8 +56,7 @@ def evoformer_block_af2(msa, pair, msa_mask, pair_mask, w, eps=1e-5):
     en = w["triangleAttentionEnding"]
     pair = _add(pair, ops.attention_af2(pair, pair_mask, en["attention"], en["heads"], True,
                                         dict(en["pairBias"], source="normalized-input"), eps))
-    pair = _add(pair, ops.transition_af2(pair, w["pairTransition"], eps))
-    return msa, pair
+    return _add(pair, ops.transition_af2(pair, w["pairTransition"], eps))
 
 
 def pairformer_block_af3(pair, single, pair_mask, seq_mask, w, swap_transposed_bias=False,

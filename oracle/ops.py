@@ -281,6 +281,43 @@ def single_attention_af3(single, pair_logits, seq_mask, w, eps=1e-5):
     return linear(o, w["outputProjection"])
 
 
+def global_column_attention_af2(msa, mask, w, heads, eps=1e-5):
+    """AF2 extra-MSA global column attention, the semantics of `encodeGlobalAttention`
+    (`webgpu/af2/evoformer/block.js:953-1030`) and its kernels (`:88-400`).  Per residue
+    column i, over the sequences s:
+
+      x = LN(msa) with queryNorm (two-pass, eps);
+      k_si = x_si Wk, v_si = x_si Wv        (one shared head of width d, `:101-146`);
+      q_ih = (sum_s m_si x_si / (1e-10 + sum_s m_si)) Wq_h / sqrt(d)      (`:166-226`);
+      logit_sih = q_ih . k_si, replaced by -1e9 where m_si = 0; softmax over s   (`:240-300`);
+      o_sih = sigmoid(x_si Wg + bg)_h * sum_s softmax v_s              (`:329-400`);
+      update_si = o_si Wo + bo.
+    Weights (in,out): queryWeight [C, H*d], keyWeight/valueWeight [C, d], gatingWeight
+    [C, H*d], gatingBias [H*d], outputWeight [H*d, C], outputBias [C]; d = len(gatingBias)/heads.
+    Every intermediate buffer is rounded to float32 as the reference stores it.
+    Returns the msa update [S, N, C].
+    """
+    s_, n, c = msa.shape
+    d = len(w["gatingBias"]) // heads
+    x = layer_norm(msa, w["queryNormScale"], w["queryNormOffset"], eps)
+    m = np.asarray(mask, F64)
+    keys = np.asarray(linear(x, w["keyWeight"]), F64)            # [S, N, d]
+    values = np.asarray(linear(x, w["valueWeight"]), F64)
+    den = 1e-10 + m.sum(0)                                       # [N]
+    means = _f32((np.asarray(x, F64) * m[..., None]).sum(0) / den[:, None])   # [N, C]
+    q = np.asarray(_f32(np.asarray(means, F64) @ np.asarray(w["queryWeight"], F64).reshape(c, heads * d)
+                        / np.sqrt(d)), F64).reshape(n, heads, d)
+    logits = np.einsum("nhd,snd->nhs", q, keys)
+    logits = np.where((m.T == 0)[:, None, :], -1e9, logits)
+    logits = logits - logits.max(-1, keepdims=True)
+    p = np.exp(logits)
+    p = p / p.sum(-1, keepdims=True)
+    attended = np.asarray(_f32(np.einsum("nhs,snd->nhd", p, values)), F64).reshape(n, heads * d)
+    gate = sigmoid(np.asarray(linear(x, w["gatingWeight"], w["gatingBias"]), F64))
+    gated = _f32(gate * attended[None])
+    return linear(gated, w["outputWeight"], w["outputBias"])
+
+
 # ---------------------------------------------------------------------------------------
 # Outer product mean and transitions
 # ---------------------------------------------------------------------------------------
