@@ -173,6 +173,39 @@ def evoformer_block_config4(ctx, D, synthetic, reps):
             "outputs_finite": finite, "kernels_ms": kern}
 
 
+def extra_msa_block_n384(ctx, D, synthetic, reps):
+    """One AF2 extra-MSA block (global column attention) at N_res=384 with 1024 extra sequences
+    (AF2 monomer's max_extra_msa), c_m=64, c_z=128, int8 weights, bf16 activations."""
+    import torch
+    n, s_, cm, cz = 384, 1024, 64, 128
+    dev = ctx.device
+    w = synthetic.quantise_tree(synthetic.synthetic_extra_msa_block_weights(
+        c_m=cm, c_z=cz, c_outer=32, heads_msa=8, heads_pair=4, tri_hidden=128, msa_hidden=4 * cm,
+        pair_hidden=4 * cz), "int8", 64)
+    dw = D.DeviceWeights(dev)
+    ws = D.extra_msa_weights(dw, w)
+    g = torch.Generator(device=dev).manual_seed(12)
+    msa = torch.randn(s_, n, cm, device=dev, generator=g).to(torch.bfloat16)
+    pair = torch.randn(n, n, cz, device=dev, generator=g).to(torch.bfloat16)
+    mm = (torch.rand(s_, n, device=dev, generator=g) > 0.2).float()
+    pm = torch.ones(n, n, device=dev)
+    msa0, pair0 = msa.clone(), pair.clone()
+
+    def block():
+        D.extra_msa_block(ctx, msa, pair, mm, pm, ws, w)
+
+    block()
+    msa.copy_(msa0)
+    pair.copy_(pair0)
+    ms = timed(block, reps)
+    kern = profile_ops(ctx, block, 2)
+    finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
+    return {"workload": f"one AF2 extra-MSA block: N_res={n}, N_extra_seq={s_}, c_m={cm}, c_z={cz}, row attention "
+                        "8x8 with pair bias, global column attention 8x8, int8 weights (fp16 scales, groups of 64), "
+                        "bf16 activations, 20% of MSA positions masked; synthetic",
+            "ms_per_block": round(ms, 3), "outputs_finite": finite, "kernels_ms": kern}
+
+
 def evoformer_stack_config4(ctx, D, synthetic, reps):
     """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
     pass (1 recycle), 48 distinct int8 weight sets, bf16 activations, through lf_evoformer_stack."""
@@ -343,6 +376,8 @@ def main():
         extras["evoformer_block"] = evoformer_block_config4(ctx, D, synthetic, 5)
         log("config 4: the 48-block stack ...")
         extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
+        log("extra-MSA block ...")
+        extras["extra_msa_block"] = extra_msa_block_n384(ctx, D, synthetic, 5)
         log("config 5: one Pairformer block ...")
         extras["pairformer_block"] = pairformer_block_config5(ctx, D, synthetic, 5)
 
@@ -379,6 +414,7 @@ def main():
         "triangle_attention": extras.get("triangle_attention"),
         "evoformer_stack": extras.get("evoformer_stack"),
         "pairformer_block": extras.get("pairformer_block"),
+        "extra_msa_block": extras.get("extra_msa_block"),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -32,7 +32,8 @@ struct GlobalColumnParams {
   float scale;                  // 1/sqrt(d)
 };
 
-// Merges an online-softmax state (m, l, acc) with another one.
+// Merges an online-softmax state (m, l, acc) with another one (exp of -1e30-scale gaps is 0,
+// so an empty state merges away).
 template <int D>
 __device__ __forceinline__ void sm_merge(float& m, float& l, float (&acc)[D], float m2, float l2, const float (&acc2)[D]) {
   const float mx = fmaxf(m, m2);
@@ -45,89 +46,122 @@ __device__ __forceinline__ void sm_merge(float& m, float& l, float (&acc)[D], fl
 
 template <int D>
 __global__ __launch_bounds__(GA_NT) void global_column_kernel(GlobalColumnParams p) {
-  __shared__ float part[4][GA_MAXHD];
+  constexpr int HMAX = GA_MAXHD / D;            // heads this head width allows
+  __shared__ float part[32][GA_MAXHD];          // query partial sums: 32 row groups
   __shared__ float qs[GA_MAXHD];
-  __shared__ float wstate[4][GA_MAXHD / 1 + 16];   // per wave: acc [H*D], then max [H], sum [H]
+  __shared__ float wstate[4][GA_MAXHD + 2 * HMAX];   // per wave: acc [H*D], max [H], sum [H]
   __shared__ float att[GA_MAXHD];
   __shared__ float cnt[4];
   const int i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int S = p.S, N = p.N, H = p.H, Hd = H * D;
+  const int S = p.S, N = p.N, H = p.H, Hd = H * D, pr = Hd / 8;   // 16-byte pieces per row
 
   // the column's mask count
   float c = 0.f;
   for (int s = tid; s < S; s += GA_NT) c += p.mask[(size_t)s * N + i];
   c = wave_sum(c);
   if (lane == 0) cnt[wave] = c;
-  // q: the masked mean of qm over the sequences, four sequence phases per output
-  for (int e = tid; e < 4 * Hd; e += GA_NT) {
-    const int hd = e % Hd, ph = e / Hd;
-    float t = 0.f;
-    for (int s = ph; s < S; s += 4) t += (float)p.qm[((size_t)i * S + s) * Hd + hd];
-    part[ph][hd] = t;
+  // q: sum over the sequences of qm (16-byte pieces: thread -> piece tid % pr of rows tid / pr + k*rg)
+  {
+    const int rg = min(32, GA_NT / pr), piece = tid % pr, r0 = tid / pr;   // row groups (<= 32 stored)
+    float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r0 < rg)
+      for (int s = r0; s < S; s += rg) {
+        const h8 v = *reinterpret_cast<const h8*>(p.qm + ((size_t)i * S + s) * Hd + piece * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] += (float)v[e];
+      }
+    if (r0 < 32) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[r0][piece * 8 + e] = r0 < rg ? t[e] : 0.f;
+    }
   }
   __syncthreads();
   const float den = 1e-10f + cnt[0] + cnt[1] + cnt[2] + cnt[3];
-  for (int hd = tid; hd < Hd; hd += GA_NT)
-    qs[hd] = (part[0][hd] + part[1][hd] + part[2][hd] + part[3][hd]) / den * p.scale;
+  const int rg = min(32, GA_NT / pr);
+  for (int hd = tid; hd < Hd; hd += GA_NT) {
+    float t = 0.f;
+    for (int r = 0; r < rg; ++r) t += part[r][hd];
+    qs[hd] = t / den * p.scale;
+  }
   __syncthreads();
 
-  // online softmax over this thread's sequences, per head
-  for (int h = 0; h < H; ++h) {
-    float q[D];
+  // online softmax over this thread's sequences, every head at once (k, v loaded once a sequence)
+  float m[HMAX], l[HMAX], acc[HMAX][D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) q[e] = qs[h * D + e];
-    float m = -1e30f, l = 0.f, acc[D];
+  for (int h = 0; h < HMAX; ++h) {
+    m[h] = -1e30f;
+    l[h] = 0.f;
 #pragma unroll
-    for (int e = 0; e < D; ++e) acc[e] = 0.f;
-    for (int s = tid; s < S; s += GA_NT) {
-      const _Float16* kr = p.k + ((size_t)i * S + s) * D;
-      const _Float16* vr = p.v + ((size_t)i * S + s) * D;
+    for (int e = 0; e < D; ++e) acc[h][e] = 0.f;
+  }
+  for (int s = tid; s < S; s += GA_NT) {
+    float kv[D], vv[D];
+#pragma unroll
+    for (int e8 = 0; e8 < D; e8 += 8) {
+      const h8 kk = *reinterpret_cast<const h8*>(p.k + ((size_t)i * S + s) * D + e8);
+      const h8 vx = *reinterpret_cast<const h8*>(p.v + ((size_t)i * S + s) * D + e8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kv[e8 + e] = (float)kk[e];
+        vv[e8 + e] = (float)vx[e];
+      }
+    }
+    const bool masked = p.mask[(size_t)s * N + i] == 0.f;
+#pragma unroll
+    for (int h = 0; h < HMAX; ++h) {
+      if (h >= H) break;
       float logit = 0.f;
 #pragma unroll
-      for (int e = 0; e < D; ++e) logit += q[e] * (float)kr[e];
-      if (p.mask[(size_t)s * N + i] == 0.f) logit = -1e9f;
-      const float mx = fmaxf(m, logit);
-      const float a = __expf(m - mx), w = __expf(logit - mx);
-      l = l * a + w;
+      for (int e = 0; e < D; ++e) logit += qs[h * D + e] * kv[e];
+      if (masked) logit = -1e9f;
+      const float mx = fmaxf(m[h], logit);
+      const float a = __expf(m[h] - mx), w = __expf(logit - mx);
+      l[h] = l[h] * a + w;
 #pragma unroll
-      for (int e = 0; e < D; ++e) acc[e] = acc[e] * a + w * (float)vr[e];
-      m = mx;
+      for (int e = 0; e < D; ++e) acc[h][e] = acc[h][e] * a + w * vv[e];
+      m[h] = mx;
     }
-    // merge over the wave's lanes
+  }
+  // merge over the wave's lanes, then the four waves through LDS
+#pragma unroll
+  for (int h = 0; h < HMAX; ++h) {
+    if (h >= H) break;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       float acc2[D];
 #pragma unroll
-      for (int e = 0; e < D; ++e) acc2[e] = __shfl_xor(acc[e], o, WAVE);
-      sm_merge<D>(m, l, acc, __shfl_xor(m, o, WAVE), __shfl_xor(l, o, WAVE), acc2);
+      for (int e = 0; e < D; ++e) acc2[e] = __shfl_xor(acc[h][e], o, WAVE);
+      sm_merge<D>(m[h], l[h], acc[h], __shfl_xor(m[h], o, WAVE), __shfl_xor(l[h], o, WAVE), acc2);
     }
     if (lane == 0) {
 #pragma unroll
-      for (int e = 0; e < D; ++e) wstate[wave][h * D + e] = acc[e];
-      wstate[wave][Hd + h] = m;
-      wstate[wave][Hd + 8 + h] = l;
+      for (int e = 0; e < D; ++e) wstate[wave][h * D + e] = acc[h][e];
+      wstate[wave][Hd + h] = m[h];
+      wstate[wave][Hd + HMAX + h] = l[h];
     }
   }
   __syncthreads();
-  // merge the four waves: thread hd < Hd finishes one attended value
   for (int hd = tid; hd < Hd; hd += GA_NT) {
     const int h = hd / D;
-    float m = wstate[0][Hd + h], l = wstate[0][Hd + 8 + h], a = wstate[0][hd];
+    float mm = wstate[0][Hd + h], ll = wstate[0][Hd + HMAX + h], a = wstate[0][hd];
     for (int w2 = 1; w2 < 4; ++w2) {
-      const float m2 = wstate[w2][Hd + h], l2 = wstate[w2][Hd + 8 + h], a2 = wstate[w2][hd];
-      const float mx = fmaxf(m, m2), x1 = __expf(m - mx), x2 = __expf(m2 - mx);
-      l = l * x1 + l2 * x2;
+      const float m2 = wstate[w2][Hd + h], l2 = wstate[w2][Hd + HMAX + h], a2 = wstate[w2][hd];
+      const float mx = fmaxf(mm, m2), x1 = __expf(mm - mx), x2 = __expf(m2 - mx);
+      ll = ll * x1 + l2 * x2;
       a = a * x1 + a2 * x2;
-      m = mx;
+      mm = mx;
     }
-    att[hd] = a / l;
+    att[hd] = a / ll;
   }
   __syncthreads();
-  // gate rows of this column times the attended values, in place
-  for (int e = tid; e < S * Hd; e += GA_NT) {
-    const int s = e / Hd, hd = e - s * Hd;
-    _Float16* g = p.gate + ((size_t)s * N + i) * Hd + hd;
-    *g = (_Float16)((float)*g * att[hd]);
+  // gate rows of this column times the attended values, in place, 16 bytes at a time
+  for (int e = tid; e < S * pr; e += GA_NT) {
+    const int s = e / pr, piece = e - s * pr;
+    h8* g = reinterpret_cast<h8*>(p.gate + ((size_t)s * N + i) * Hd + piece * 8);
+    h8 v = *g;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = (_Float16)((float)v[u] * att[piece * 8 + u]);
+    *g = v;
   }
 }
 
