@@ -549,8 +549,10 @@ lf_evoformer_weights evo_weights(napi_env env, napi_value w) {
   lf_evoformer_weights e{};
   e.row_attention = att_weights(env, prop(env, w, "rowAttention"));
   e.row_heads = get_int(env, w, "rowHeads");
-  e.column_attention = att_weights(env, prop(env, w, "columnAttention"));
-  e.column_heads = get_int(env, w, "columnHeads");
+  if (has(env, w, "columnAttention")) {   // absent in an extra-MSA block
+    e.column_attention = att_weights(env, prop(env, w, "columnAttention"));
+    e.column_heads = get_int(env, w, "columnHeads");
+  }
   e.msa_transition = tr_weights(env, prop(env, w, "msaTransition"));
   e.outer_product_mean = opm_w(env, prop(env, w, "outerProductMean"));
   e.tri_out = tri_weights(env, prop(env, w, "triOut"));
@@ -563,11 +565,44 @@ lf_evoformer_weights evo_weights(napi_env env, napi_value w) {
   return e;
 }
 
-// evoformerStack(ctx, args, [blockWeights...]) - one block when the array has length 1
-napi_value EvoformerStack(napi_env env, napi_callback_info info) {
-  napi_value argv[3];
-  if (!get_args(env, info, 3, argv)) return nullptr;
+lf_global_attention_weights glob_weights(napi_env env, napi_value w) {
+  lf_global_attention_weights t{};
+  t.norm_scale = get_vec(env, w, "normScale");
+  t.norm_offset = get_vec(env, w, "normOffset");
+  t.wq = get_weight(env, w, "wq");
+  t.wk = get_weight(env, w, "wk");
+  t.wv = get_weight(env, w, "wv");
+  t.wg = get_weight(env, w, "wg");
+  t.g_bias = get_vec(env, w, "gBias");
+  t.wo = get_weight(env, w, "wo");
+  t.o_bias = get_vec(env, w, "oBias");
+  return t;
+}
+
+napi_value GlobalColumnAttention(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return nullptr;
   napi_value o = argv[1];
+  lf_global_attention_weights w = glob_weights(env, prop(env, o, "weights"));
+  lf_global_attention_args a{};
+  a.sequences = get_int(env, o, "sequences");
+  a.length = get_int(env, o, "length");
+  a.channels = get_int(env, o, "channels");
+  a.heads = get_int(env, o, "heads");
+  a.head_dim = get_int(env, o, "headDim");
+  a.act_dtype = get_int(env, o, "actDtype");
+  a.act = get_dev(env, o, "act");
+  a.mask = static_cast<const float*>(get_dev(env, o, "mask"));
+  a.out = get_dev(env, o, "out");
+  a.accumulate = get_int(env, o, "accumulate");
+  a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
+  a.w = &w;
+  int rc = lf_global_column_attention(as_ctx(env, argv[0]), &a);
+  if (rc != LF_OK) return throw_lf(env, rc, "lf_global_column_attention");
+  return undefined_value(env);
+}
+
+lf_evoformer_block_args evo_args(napi_env env, napi_value o) {
   lf_evoformer_block_args a{};
   a.sequences = get_int(env, o, "sequences");
   a.length = get_int(env, o, "length");
@@ -584,6 +619,14 @@ napi_value EvoformerStack(napi_env env, napi_callback_info info) {
   a.msa_mask = static_cast<const float*>(get_dev(env, o, "msaMask"));
   a.pair_mask = static_cast<const float*>(get_dev(env, o, "pairMask"));
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
+  return a;
+}
+
+// evoformerStack(ctx, args, [blockWeights...]) - one block when the array has length 1
+napi_value EvoformerStack(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return nullptr;
+  lf_evoformer_block_args a = evo_args(env, argv[1]);
   uint32_t n = 0;
   napi_get_array_length(env, argv[2], &n);
   lf_evoformer_weights* ws = new lf_evoformer_weights[n > 0 ? n : 1];
@@ -595,6 +638,27 @@ napi_value EvoformerStack(napi_env env, napi_callback_info info) {
   int rc = lf_evoformer_stack(as_ctx(env, argv[0]), &a, ws, (int)n);
   delete[] ws;
   if (rc != LF_OK) return throw_lf(env, rc, "lf_evoformer_stack");
+  return undefined_value(env);
+}
+
+// extraMsaStack(ctx, args, [blockWeights...]): Evoformer block weights with columnGlobal
+napi_value ExtraMsaStack(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return nullptr;
+  lf_evoformer_block_args a = evo_args(env, argv[1]);
+  uint32_t n = 0;
+  napi_get_array_length(env, argv[2], &n);
+  lf_extra_msa_weights* ws = new lf_extra_msa_weights[n > 0 ? n : 1];
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, argv[2], i, &e);
+    ws[i].base = evo_weights(env, e);
+    ws[i].column_global = glob_weights(env, prop(env, e, "columnGlobal"));
+    ws[i].column_global_heads = get_int(env, e, "columnGlobalHeads");
+  }
+  int rc = lf_extra_msa_stack(as_ctx(env, argv[0]), &a, ws, (int)n);
+  delete[] ws;
+  if (rc != LF_OK) return throw_lf(env, rc, "lf_extra_msa_stack");
   return undefined_value(env);
 }
 
@@ -647,7 +711,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"memoryStats", MemoryStats}, {"profileEnable", ProfileEnable}, {"profileRead", ProfileRead},
       {"version", Version}, {"triMult", TriMult}, {"attention", Attention}, {"transition", Transition},
       {"outerProductMean", OuterProductMean}, {"evoformerStack", EvoformerStack},
-      {"pairformerBlock", PairformerBlock},
+      {"pairformerBlock", PairformerBlock}, {"globalColumnAttention", GlobalColumnAttention},
+      {"extraMsaStack", ExtraMsaStack},
   };
   for (const auto& f : fns) {
     napi_value v;

@@ -465,16 +465,16 @@ OuterProductMeanGpu.prototype.run = function run(input) {
 
 function evoformerBlockWeights(up, w, dims) {
   const row = w.msaRowAttention;
-  const col = w.msaColumnAttention;
+  const col = w.msaColumnAttention;   // absent in an extra-MSA block
   const st = w.triangleAttentionStarting;
   const en = w.triangleAttentionEnding;
-  return {
+  const out = {
     rowAttention: attentionWeights(up, row.attention, dims.cM, dims.cM,
       { source: 'separate', channels: dims.cZ, layerNormScale: row.pairBias.layerNormScale,
         layerNormOffset: row.pairBias.layerNormOffset, projectionWeight: row.pairBias.projectionWeight }, row.heads),
     rowHeads: row.heads,
-    columnAttention: attentionWeights(up, col.attention, dims.cM, dims.cM, null, col.heads),
-    columnHeads: col.heads,
+    columnAttention: col ? attentionWeights(up, col.attention, dims.cM, dims.cM, null, col.heads) : undefined,
+    columnHeads: col ? col.heads : 0,
     msaTransition: transitionWeights(up, w.msaTransition, dims.cM, dims.msaHidden),
     outerProductMean: opmWeights(up, w.outerProductMean, dims.cM, dims.cOuter, dims.cZ),
     triOut: triangleWeights(up, w.triangleMultiplicationOutgoing, dims.cZ, dims.triangleHidden),
@@ -487,6 +487,9 @@ function evoformerBlockWeights(up, w, dims) {
     triAttEndHeads: en.heads,
     pairTransition: transitionWeights(up, w.pairTransition, dims.cZ, dims.pairHidden),
   };
+  if (!col) delete out.columnAttention;
+  return out;
+
 }
 
 function blockDims(input, w) {
@@ -534,6 +537,62 @@ EvoformerBlockGpu.prototype.run = function run(input) {
 function EvoformerStackGpu(device) { this.device = device; }
 EvoformerStackGpu.prototype.run = function run(input) {
   return runEvoformer(this.device, input, input.blocks);
+};
+
+// ---- AF2 extra-MSA stack ------------------------------------------------------------
+
+// Global column attention weights (webgpu/af2/evoformer/block.js:963-980), all (in,out):
+// queryWeight [cM, H*d], keyWeight / valueWeight [cM, d], gating [cM, H*d] + bias, output
+// [H*d, cM] + bias, with d = gatingBias.length / heads.
+function globalAttentionWeights(up, g, cM) {
+  const a = g.attention;
+  const hd = a.gatingBias.length;
+  const d = hd / g.heads;
+  return {
+    normScale: up.vec(a.queryNormScale), normOffset: up.vec(a.queryNormOffset),
+    wq: up.weight(a.queryWeight, 'in_out', cM, hd), wk: up.weight(a.keyWeight, 'in_out', cM, d),
+    wv: up.weight(a.valueWeight, 'in_out', cM, d), wg: up.weight(a.gatingWeight, 'in_out', cM, hd),
+    gBias: up.vec(a.gatingBias), wo: up.weight(a.outputWeight, 'in_out', hd, cM), oBias: up.vec(a.outputBias),
+  };
+}
+
+// webgpu/af2/evoformer/stack.js:249-330: run(input) with input.blockWeights, each an
+// Evoformer block's weights with msaColumnGlobalAttention in place of msaColumnAttention
+// (encodeExtraMsaBlock, block.js:1715-1744); returns {msa, pair, elapsedMilliseconds, memory}.
+function ExtraMsaStackGpu(device) { this.device = device; }
+ExtraMsaStackGpu.prototype.run = function run(input) {
+  const device = this.device;
+  return new Promise(function execute(resolve) {
+    const blocks = input.blockWeights;
+    if (!Array.isArray(blocks) || blocks.length === 0) throw new RangeError('blockWeights must be a non-empty array');
+    const dims = blockDims(input, blocks[0]);
+    const up = new Uploads(device);
+    const start = performance.now();
+    const ws = blocks.map(function each(w) {
+      return resident(device, w, function build(wu) {
+        const e = evoformerBlockWeights(wu, w, dims);
+        e.columnGlobal = globalAttentionWeights(wu, w.msaColumnGlobalAttention, dims.cM);
+        e.columnGlobalHeads = w.msaColumnGlobalAttention.heads;
+        return e;
+      });
+    });
+    const msaElements = input.sequences * input.length * input.cM;
+    const pairElements = input.length * input.length * input.cZ;
+    expectLength('msa', input.msa, msaElements);
+    expectLength('pair', input.pair, pairElements);
+    const msa = up.vec(input.msa);
+    const pair = up.vec(input.pair);
+    device.addon.extraMsaStack(device.ctx, {
+      sequences: input.sequences, length: input.length, cM: dims.cM, cZ: dims.cZ, cOuter: dims.cOuter,
+      triangleHidden: dims.triangleHidden, msaHidden: dims.msaHidden, pairHidden: dims.pairHidden,
+      msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair,
+      msaMask: up.vec(input.msaMask), pairMask: up.vec(input.pairMask), epsilon: 1e-5,
+    }, ws);
+    const r = finish(device, up, [{ buffer: msa, elements: msaElements }, { buffer: pair, elements: pairElements }],
+      start);
+    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels });
+  });
 };
 
 // ---- AF3 pairformer stack ------------------------------------------------------------
@@ -682,6 +741,7 @@ module.exports = {
   OuterProductMeanGpu: OuterProductMeanGpu,
   EvoformerBlockGpu: EvoformerBlockGpu,
   EvoformerStackGpu: EvoformerStackGpu,
+  ExtraMsaStackGpu: ExtraMsaStackGpu,
   Af3PairformerStackGpu: Af3PairformerStackGpu,
   validateTriangleInput: validateTriangleInput,
   validateAttentionInput: validateAttentionInput,

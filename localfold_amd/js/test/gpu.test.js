@@ -86,6 +86,11 @@ async function main() {
   report('evoformer block msa', lf.errorMetrics(evOut.msa, ev.expectedMsa), { mean: 2e-3, max: 2e-2 });
   report('evoformer block pair', lf.errorMetrics(evOut.pair, ev.expectedPair), { mean: 2e-3, max: 2e-2 });
 
+  const ex = revive(JSON.parse(fs.readFileSync(path.join(dir, 'extra.json'), 'utf8')));
+  const exOut = await new lf.ExtraMsaStackGpu(device).run(ex.input);
+  report('extra-MSA stack msa', lf.errorMetrics(exOut.msa, ex.expectedMsa), { mean: 2e-3, max: 2e-2 });
+  report('extra-MSA stack pair', lf.errorMetrics(exOut.pair, ex.expectedPair), { mean: 2e-3, max: 2e-2 });
+
   const pf = revive(JSON.parse(fs.readFileSync(path.join(dir, 'pairformer.json'), 'utf8')));
   const pfOut = await new lf.Af3PairformerStackGpu(device).run(pf.state, pf.blocks, { swapTransposedBias: false });
   report('pairformer pair', lf.errorMetrics(pfOut.pair, pf.expectedPair), { mean: 2e-3, max: 2e-2 });

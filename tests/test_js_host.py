@@ -119,6 +119,19 @@ def test_js_gpu_suite(tmp_path):
           "expectedMsa": rm, "expectedPair": rp}
     (tmp_path / "evoformer.json").write_text(json.dumps(_dump_tree(ev, tmp_path, "evo")))
 
+    # ExtraMsaStackGpu: two extra-MSA blocks (webgpu/af2/evoformer/stack.js:249-330, input.blockWeights)
+    xws = [S.synthetic_extra_msa_block_weights(c_m=64, c_z=32, c_outer=8, heads_msa=8, heads_pair=2, tri_hidden=32,
+                                               msa_hidden=256, pair_hidden=128, seed=s_) for s_ in (31, 32)]
+    xa = S.synthetic_activations(5, 14, 64, 32, seed=33)
+    xm, xp = xa["msa"], xa["pair"]
+    for xw in xws:
+        xm, xp = blocks.extra_msa_block_af2(xm, xp, xa["msaMask"], xa["pairMask"], xw)
+    ex = {"input": {"msa": xa["msa"], "pair": xa["pair"], "msaMask": xa["msaMask"], "pairMask": xa["pairMask"],
+                    "sequences": 5, "length": 14, "cM": 64, "cZ": 32, "cOuter": 8, "triangleHidden": 32,
+                    "blockWeights": xws},
+          "expectedMsa": xm, "expectedPair": xp}
+    (tmp_path / "extra.json").write_text(json.dumps(_dump_tree(ex, tmp_path, "ex")))
+
     # Af3PairformerStackGpu: two blocks
     n, cz, cs = 24, 128, 384
     pws = [S.synthetic_pairformer_weights(cz, cs, 4, 16, 24, seed=s_) for s_ in (21, 22)]
