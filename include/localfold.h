@@ -329,6 +329,61 @@ typedef struct {
  * in pairformerBlock order (cpu/af3/trunk/pairformer.js:495-541). */
 int lf_pairformer_block(lf_context* ctx, const lf_pairformer_block_args* args);
 
+/* ---- AF3 MSA module ------------------------------------------------------------------- */
+
+/* Pair-weighted averaging weights (`msaAttention1`, cpu/af3/trunk/msa.js:157-219), no biases. */
+typedef struct {
+  const float *act_norm_scale, *act_norm_offset;    /* [cM] */
+  const float *pair_norm_scale, *pair_norm_offset;  /* [cZ] */
+  lf_weight pair_logits;                            /* [cZ x H] */
+  lf_weight wv, wg;                                 /* [cM x H*d] (vProjection, gatingQuery) */
+  lf_weight wo;                                     /* [H*d x cM] (outputProjection) */
+} lf_pair_averaging_weights;
+
+typedef struct {
+  int sequences, tokens, c_m, c_z, heads, head_dim;
+  int msa_dtype;
+  const void* msa;          /* [S, N, cM] */
+  const float* msa_mask;    /* [S, N]; the key mask is its maximum over the sequences */
+  int pair_dtype;
+  const void* pair;         /* [N, N, cZ] */
+  void* out;                /* [S, N, cM], msa_dtype; may alias msa when accumulate */
+  int accumulate;
+  float epsilon;            /* layer norms (fast variance), 1e-5 */
+  const lf_pair_averaging_weights* w;
+} lf_pair_averaging_args;
+
+/* Replaces msaAttention (cpu/af3/trunk/msa.js:157-219): softmax over keys j of
+ * LN(pair_ij) . pairLogits[:, h] + 1e9 (max_s mask[s, j] - 1), shared by every sequence,
+ * averages x vProjection; gated by sigmoid(x gatingQuery), then outputProjection. */
+int lf_msa_pair_weighted_averaging(lf_context* ctx, const lf_pair_averaging_args* args);
+
+typedef struct {
+  lf_opm_weights outer_product_mean;  int c_outer;   /* AF3 outer product mean */
+  lf_pair_averaging_weights msa_attention;  int msa_heads, msa_head_dim;
+  lf_transition_weights msa_transition;              /* SwiGLU, hidden 4 cM */
+  lf_pairformer_weights pair;                        /* pair steps; the single fields are not read */
+} lf_msa_module_weights;
+
+typedef struct {
+  int sequences, tokens, c_m, c_z;
+  int msa_update_before_opm;     /* 0: AF3 (OPM of the incoming msa first); 1: OpenDDE / Boltz-2 */
+  int swap_transposed_bias, divide_by_length;
+  int msa_dtype; void* msa;      /* [S, N, cM] in place */
+  int pair_dtype; void* pair;    /* [N, N, cZ] in place */
+  const float* msa_mask;         /* [S, N] */
+  const float* pair_mask;        /* [N, N] */
+  long long transition_chunk_bytes;
+  float epsilon;
+  const lf_msa_module_weights* w;
+} lf_msa_block_args;
+
+/* Replaces msaBlock (cpu/af3/trunk/msa.js:233-287): outer product mean into the pair and the
+ * MSA update (pair-weighted averaging, SwiGLU transition) in the dialect's order, then the
+ * pair steps of a pair-only pairformer block (triangle multiplications, grid attentions,
+ * pair transition). */
+int lf_msa_module_block(lf_context* ctx, const lf_msa_block_args* args);
+
 #ifdef __cplusplus
 }
 #endif

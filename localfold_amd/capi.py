@@ -137,6 +137,32 @@ class lf_pairformer_block_args(C.Structure):
                 ("epsilon", C.c_float), ("w", C.POINTER(lf_pairformer_weights))]
 
 
+class lf_pair_averaging_weights(C.Structure):
+    _fields_ = [("act_norm_scale", P), ("act_norm_offset", P), ("pair_norm_scale", P), ("pair_norm_offset", P),
+                ("pair_logits", lf_weight), ("wv", lf_weight), ("wg", lf_weight), ("wo", lf_weight)]
+
+
+class lf_pair_averaging_args(C.Structure):
+    _fields_ = [("sequences", C.c_int), ("tokens", C.c_int), ("c_m", C.c_int), ("c_z", C.c_int),
+                ("heads", C.c_int), ("head_dim", C.c_int), ("msa_dtype", C.c_int), ("msa", P), ("msa_mask", P),
+                ("pair_dtype", C.c_int), ("pair", P), ("out", P), ("accumulate", C.c_int),
+                ("epsilon", C.c_float), ("w", C.POINTER(lf_pair_averaging_weights))]
+
+
+class lf_msa_module_weights(C.Structure):
+    _fields_ = [("outer_product_mean", lf_opm_weights), ("c_outer", C.c_int),
+                ("msa_attention", lf_pair_averaging_weights), ("msa_heads", C.c_int), ("msa_head_dim", C.c_int),
+                ("msa_transition", lf_transition_weights), ("pair", lf_pairformer_weights)]
+
+
+class lf_msa_block_args(C.Structure):
+    _fields_ = [("sequences", C.c_int), ("tokens", C.c_int), ("c_m", C.c_int), ("c_z", C.c_int),
+                ("msa_update_before_opm", C.c_int), ("swap_transposed_bias", C.c_int),
+                ("divide_by_length", C.c_int), ("msa_dtype", C.c_int), ("msa", P), ("pair_dtype", C.c_int),
+                ("pair", P), ("msa_mask", P), ("pair_mask", P), ("transition_chunk_bytes", C.c_longlong),
+                ("epsilon", C.c_float), ("w", C.POINTER(lf_msa_module_weights))]
+
+
 # (name, restype, argtypes) for every function include/localfold.h declares.
 PROTOTYPES = [
     ("lf_context_create", P, [C.c_int]),
@@ -163,6 +189,8 @@ PROTOTYPES = [
     ("lf_extra_msa_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights), C.c_int]),
     ("lf_evoformer_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
     ("lf_pairformer_block", C.c_int, [P, C.POINTER(lf_pairformer_block_args)]),
+    ("lf_msa_pair_weighted_averaging", C.c_int, [P, C.POINTER(lf_pair_averaging_args)]),
+    ("lf_msa_module_block", C.c_int, [P, C.POINTER(lf_msa_block_args)]),
 ]
 
 _lib = None

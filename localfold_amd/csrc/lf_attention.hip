@@ -42,7 +42,8 @@ constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
 struct FlashParams {
   const _Float16 *q, *k, *vt, *g;
   _Float16* o;
-  const float* kb;        // [B][Q]
+  const float* kb;        // [B][Qp] at a row stride of kb_stride (0: one row shared by every b)
+  long long kb_stride;
   const _Float16* bias;   // [H][Q][Q] or null
   int B, H, Q, d, HD;
   int nqb;                // query blocks per (b, h)
@@ -71,6 +72,20 @@ __global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* 
   }
   const float m = mask[transpose ? (long long)k * B + b : (long long)b * Q + k];
   kb[i] = (1e9f * LOG2E) * (m - 1.0f);
+}
+
+// One key-bias row shared by every batch row, from the mask's maximum over the batch
+// (AF3 pair-weighted averaging: a token any sequence covers is a key for every sequence)
+__global__ __launch_bounds__(256) void keymax_kernel(const float* mask, float* kb, int B, int Q, int Qp) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= Qp) return;
+  if (k >= Q) {
+    kb[k] = -1e30f;
+    return;
+  }
+  float m = 0.f;
+  for (int b = 0; b < B; ++b) m = fmaxf(m, mask[(long long)b * Q + k]);
+  kb[k] = (1e9f * LOG2E) * (m - 1.0f);
 }
 
 // (float)v[i] + c in one instruction (i is a constant once the caller's loop is unrolled)
@@ -147,7 +162,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   const _Float16* qh = p.q + bh * Qp * FA_DP;
   const _Float16* kh = p.k + bh * Qp * FA_DP;
   const _Float16* vh = p.vt + bh * FA_DP * Qp;
-  const float* kbb = p.kb + (size_t)b * Qp;
+  const float* kbb = p.kb + b * p.kb_stride;
   const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * Qp : nullptr;
 
   // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
@@ -375,7 +390,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   }
 }
 
-int attention(lf_context* ctx, const lf_attention_args& a) {
+int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shared_key_mask) {
   LF_REQUIRE(a.w != nullptr, "attention: weights are NULL");
   LF_REQUIRE(a.batch > 0 && a.queries > 0 && a.channels > 0 && a.heads > 0,
              "attention dimensions must be positive");
@@ -403,9 +418,11 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   LF_REQUIRE(rows < (1LL << 31), "attention: too many rows");
 
   WView views[6];
-  int nv = 0;
-  LF_TRY(make_view(w.wq, C, HD, "queryWeight", &views[nv++]));
-  LF_TRY(make_view(w.wk, C, HD, "keyWeight", &views[nv++]));
+  int nv = 2;
+  if (!no_qk) {
+    LF_TRY(make_view(w.wq, C, HD, "queryWeight", &views[0]));
+    LF_TRY(make_view(w.wk, C, HD, "keyWeight", &views[1]));
+  }
   LF_TRY(make_view(w.wv, C, HD, "valueWeight", &views[nv++]));
   LF_TRY(make_view(w.wg, C, HD, "gatingWeight", &views[nv++]));
   LF_TRY(make_view(w.wo, HD, C, "outputWeight", &views[nv++]));
@@ -452,17 +469,25 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   pp.ln_o = w.norm_offset;
   pp.eps = a.epsilon;
   pp.fast_var = a.fast_variance;
-  pp.g[0] = Group{views[0], WView{}, HD, OP_STORE, LOG2E / std::sqrt((float)d), w.q_bias, nullptr, Dst{}};
-  pp.g[1] = Group{views[1], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
-  pp.g[2] = Group{views[2], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
-  pp.g[3] = Group{views[3], WView{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, Dst{}};
-  pp.ngroups = 4;
+  // group slots: q, k (absent when no_qk: every logit is the bias alone), v, g, bias
+  int gq = -1, gk = -1, gv, gg, gbias = -1;
+  pp.ngroups = 0;
+  if (!no_qk) {
+    gq = pp.ngroups++;
+    pp.g[gq] = Group{views[0], WView{}, HD, OP_STORE, LOG2E / std::sqrt((float)d), w.q_bias, nullptr, Dst{}};
+    gk = pp.ngroups++;
+    pp.g[gk] = Group{views[1], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  }
+  gv = pp.ngroups++;
+  pp.g[gv] = Group{views[2], WView{}, HD, OP_STORE, 1.f, nullptr, nullptr, Dst{}};
+  gg = pp.ngroups++;
+  pp.g[gg] = Group{views[3], WView{}, HD, OP_SIGMOID, 1.f, w.g_bias, nullptr, Dst{}};
   if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) {
-    pp.g[4] = Group{views[5], WView{}, H, OP_STORE, LOG2E, nullptr, nullptr, Dst{}};
-    pp.ngroups = 5;
+    gbias = pp.ngroups++;
+    pp.g[gbias] = Group{views[5], WView{}, H, OP_STORE, LOG2E, nullptr, nullptr, Dst{}};
   }
 
-  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)B * Qp * sizeof(float), biash, expanded_bytes(views[4]),
+  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)(shared_key_mask ? 1 : B) * Qp * sizeof(float), biash, expanded_bytes(views[4]),
                      std::max(lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb)
                                                                                        : (size_t)0)};
   LF_TRY(workspace(ctx, sizes, bufs, 9));
@@ -474,7 +499,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[7], &wo, "attention.expand"));
   // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
   // exact 0, which must not meet a non-finite value)
-  if (d < FA_DP) {
+  if (d < FA_DP || no_qk) {
     for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
   } else if (Qp != Q) {
     LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, qkv, ctx->stream), "attention memset"));
@@ -488,19 +513,23 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
   }
   {
     const long long hq = (long long)Qp * FA_DP;
-    pp.g[0].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    pp.g[1].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    pp.g[2].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
-    pp.g[3].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
-    if (a.bias_mode == LF_BIAS_NORMALIZED_INPUT) pp.g[4].dst = bias_dst;
+    if (gq >= 0) pp.g[gq].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    pp.g[gv].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
+    pp.g[gg].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
+    if (gbias >= 0) pp.g[gbias].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
   }
 
   // 3. key-mask bias, f16 copy of the pair bias
   {
     LaunchScope ls(ctx, "attention.keybias");
-    hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0, ctx->stream,
-                       a.mask, keyb, B, Q, Qp, a.transpose);
+    if (shared_key_mask)
+      hipLaunchKernelGGL(keymax_kernel, dim3((unsigned)((Qp + 255) / 256)), dim3(256), 0, ctx->stream, a.mask, keyb,
+                         B, Q, Qp);
+    else
+      hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0,
+                         ctx->stream, a.mask, keyb, B, Q, Qp, a.transpose);
   }
   LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
   // caller-supplied f32 logits are converted (and transposed per head when swapped); the
@@ -517,6 +546,7 @@ int attention(lf_context* ctx, const lf_attention_args& a) {
     fp.g = gb;
     fp.o = ob;
     fp.kb = keyb;
+    fp.kb_stride = shared_key_mask ? 0 : Qp;
     fp.bias = a.bias_mode == LF_BIAS_NONE ? nullptr : bias16;
     fp.B = B;
     fp.H = H;

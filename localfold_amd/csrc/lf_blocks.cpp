@@ -3,6 +3,7 @@
 //   Evoformer order: webgpu/af2/evoformer/block.js:1536-1629 (encodeEvoformerBlock)
 //   Stack:           webgpu/af2/evoformer/stack.js:44-160
 //   Pairformer:      cpu/af3/trunk/pairformer.js:495-541 (pairformerBlock)
+//   AF3 MSA module:  cpu/af3/trunk/msa.js:157-287 (msaAttention, msaBlock)
 #include <cmath>
 
 #include "lf_context.h"
@@ -275,9 +276,149 @@ static int pairformer_block(lf_context* ctx, const lf_pairformer_block_args& a) 
   return LF_OK;
 }
 
+// AF3 pair-weighted averaging (msaAttention, cpu/af3/trunk/msa.js:157-219) as gated attention
+// whose logits are the pair bias alone (no queries, no keys) over one key mask shared by every
+// sequence, the mask's maximum over the sequences (:177-186).  Both layer norms use the fast
+// variance (cpu/af3/trunk/pairformer.js:70-87); there are no biases.
+static int pair_weighted_averaging(lf_context* ctx, const lf_pair_averaging_args& a) {
+  LF_REQUIRE(a.w != nullptr, "pair-weighted averaging: weights are NULL");
+  LF_REQUIRE(a.sequences > 0 && a.tokens > 0 && a.c_m > 0 && a.c_z > 0 && a.heads > 0 && a.head_dim > 0,
+             "pair-weighted averaging dimensions must be positive");
+  LF_REQUIRE(a.msa && a.msa_mask && a.pair && a.out, "pair-weighted averaging: NULL msa, mask, pair or out");
+  const lf_pair_averaging_weights& w = *a.w;
+  lf_attention_weights aw{};
+  aw.norm_scale = w.act_norm_scale;
+  aw.norm_offset = w.act_norm_offset;
+  aw.wv = w.wv;
+  aw.wg = w.wg;
+  aw.wo = w.wo;
+  aw.pair_norm_scale = w.pair_norm_scale;
+  aw.pair_norm_offset = w.pair_norm_offset;
+  aw.wb = w.pair_logits;
+  lf_attention_args x{};
+  x.batch = a.sequences;
+  x.queries = a.tokens;
+  x.channels = a.c_m;
+  x.heads = a.heads;
+  x.head_dim = a.head_dim;
+  x.act_dtype = a.msa_dtype;
+  x.act = a.msa;
+  x.mask = a.msa_mask;
+  x.out = a.out;
+  x.accumulate = a.accumulate;
+  x.fast_variance = 1;
+  x.bias_mode = LF_BIAS_SEPARATE;
+  x.pair_dtype = a.pair_dtype;
+  x.pair = a.pair;
+  x.pair_channels = a.c_z;
+  x.epsilon = a.epsilon > 0.f ? a.epsilon : 1e-5f;
+  x.w = &aw;
+  return attention(ctx, x, /*no_qk=*/true, /*shared_key_mask=*/true);
+}
+
+// One AF3 MSA-module block (msaBlock, cpu/af3/trunk/msa.js:233-287).
+static int msa_module_block(lf_context* ctx, const lf_msa_block_args& a) {
+  LF_REQUIRE(a.w != nullptr, "msa module block: weights are NULL");
+  LF_REQUIRE(a.sequences > 0 && a.tokens > 0 && a.c_m > 0 && a.c_z > 0, "msa module block dimensions must be positive");
+  LF_REQUIRE(a.msa && a.pair && a.msa_mask && a.pair_mask, "msa module block: NULL activation or mask");
+  const lf_msa_module_weights& w = *a.w;
+  const float eps = a.epsilon > 0.f ? a.epsilon : 1e-5f;
+  const long long chunk = a.transition_chunk_bytes > 0 ? a.transition_chunk_bytes : (1LL << 30);
+  auto opm = [&]() -> int {
+    lf_opm_args x{};
+    x.sequences = a.sequences;
+    x.length = a.tokens;
+    x.c_m = a.c_m;
+    x.c_outer = w.c_outer;
+    x.c_z = a.c_z;
+    x.msa_dtype = a.msa_dtype;
+    x.msa = a.msa;
+    x.mask = a.msa_mask;
+    x.pair_dtype = a.pair_dtype;
+    x.pair_in = a.pair;
+    x.out = a.pair;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.epsilon = eps;
+    x.norm_epsilon = 1e-3f;
+    x.w = &w.outer_product_mean;
+    StageScope stage(ctx, "outer_product_mean");
+    return outer_product_mean(ctx, x);
+  };
+  // the MSA update: the averaging and the transition move together (msa.js:259-263)
+  auto update = [&]() -> int {
+    {
+      lf_pair_averaging_args x{};
+      x.sequences = a.sequences;
+      x.tokens = a.tokens;
+      x.c_m = a.c_m;
+      x.c_z = a.c_z;
+      x.heads = w.msa_heads;
+      x.head_dim = w.msa_head_dim;
+      x.msa_dtype = a.msa_dtype;
+      x.msa = a.msa;
+      x.msa_mask = a.msa_mask;
+      x.pair_dtype = a.pair_dtype;
+      x.pair = a.pair;
+      x.out = a.msa;
+      x.accumulate = 1;
+      x.epsilon = eps;
+      x.w = &w.msa_attention;
+      StageScope stage(ctx, "pair_weighted_averaging");
+      LF_TRY(pair_weighted_averaging(ctx, x));
+    }
+    lf_transition_args x{};
+    x.kind = LF_TRANSITION_SWIGLU;
+    x.rows = a.sequences * a.tokens;
+    x.channels = a.c_m;
+    x.hidden = 4 * a.c_m;
+    x.act_dtype = a.msa_dtype;
+    x.act = a.msa;
+    x.out = a.msa;
+    x.accumulate = 1;
+    x.fast_variance = 1;
+    x.chunk_bytes = chunk;
+    x.epsilon = eps;
+    x.w = &w.msa_transition;
+    StageScope stage(ctx, "msa_transition");
+    return transition(ctx, x);
+  };
+  if (a.msa_update_before_opm) {
+    LF_TRY(update());
+    LF_TRY(opm());
+  } else {
+    LF_TRY(opm());
+    LF_TRY(update());
+  }
+  lf_pairformer_block_args p{};
+  p.tokens = a.tokens;
+  p.c_z = a.c_z;
+  p.swap_transposed_bias = a.swap_transposed_bias;
+  p.divide_by_length = a.divide_by_length;
+  p.pair_dtype = a.pair_dtype;
+  p.pair = a.pair;
+  p.pair_mask = a.pair_mask;
+  p.transition_chunk_bytes = a.transition_chunk_bytes;
+  p.epsilon = eps;
+  p.w = &w.pair;
+  return pairformer_block(ctx, p);
+}
+
 }  // namespace lf
 
 extern "C" {
+
+int lf_msa_pair_weighted_averaging(lf_context* ctx, const lf_pair_averaging_args* args) {
+  if (!ctx || !args) return lf::set_error(LF_ERR_INVALID, "lf_msa_pair_weighted_averaging: NULL argument");
+  hipSetDevice(ctx->device);
+  return lf::pair_weighted_averaging(ctx, *args);
+}
+
+int lf_msa_module_block(lf_context* ctx, const lf_msa_block_args* args) {
+  if (!ctx || !args) return lf::set_error(LF_ERR_INVALID, "lf_msa_module_block: NULL argument");
+  hipSetDevice(ctx->device);
+  return lf::msa_module_block(ctx, *args);
+}
 
 int lf_evoformer_block(lf_context* ctx, const lf_evoformer_block_args* args) {
   if (!ctx || !args || !args->w) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_block: NULL argument");

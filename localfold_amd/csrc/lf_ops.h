@@ -36,7 +36,9 @@ inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == 
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }
 
 int tri_mult(lf_context* ctx, const lf_tri_mult_args& a);
-int attention(lf_context* ctx, const lf_attention_args& a);
+// no_qk: every logit is the bias alone (AF3 pair-weighted averaging; wq/wk are not read);
+// shared_key_mask: one key mask for every batch row, the maximum of a.mask over the batch
+int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk = false, bool shared_key_mask = false);
 int transition(lf_context* ctx, const lf_transition_args& a);
 // fused transition (lf_mlp.hip): c = 128 (ReLU or SwiGLU) or 256 (ReLU), hidden % 32 == 0;
 // views: W1 (gate half), [W1 value half,] W2; packed: mlp_packed_bytes of workspace

@@ -527,3 +527,71 @@ def pairformer_block(ctx: Context, pair, single, pair_mask, seq_mask, wstruct, s
     a.epsilon = epsilon
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_pairformer_block(ctx.handle, C.byref(a)))
+
+
+def pair_averaging_weights(dw: DeviceWeights, w: dict) -> capi.lf_pair_averaging_weights:
+    """AF3 `msaAttention1` (`cpu/af3/trunk/msa.js:157-219`): actNorm / pairNorm, pairLogits
+    [cZ, H], vProjection / gatingQuery [cM, H*d], outputProjection [H*d, cM], all (in,out)."""
+    s = capi.lf_pair_averaging_weights()
+    s.act_norm_scale, s.act_norm_offset = dw.vec(w["actNormScale"]), dw.vec(w["actNormOffset"])
+    s.pair_norm_scale, s.pair_norm_offset = dw.vec(w["pairNormScale"]), dw.vec(w["pairNormOffset"])
+    s.pair_logits = dw.weight(w["pairLogits"], capi.LF_IN_OUT)
+    s.wv = dw.weight(w["vProjection"], capi.LF_IN_OUT)
+    s.wg = dw.weight(w["gatingQuery"], capi.LF_IN_OUT)
+    s.wo = dw.weight(w["outputProjection"], capi.LF_IN_OUT)
+    return s
+
+
+def msa_pair_weighted_averaging(ctx: Context, msa: torch.Tensor, mask: torch.Tensor, pair: torch.Tensor,
+                                wstruct: capi.lf_pair_averaging_weights, heads: int, head_dim: int,
+                                out: torch.Tensor = None, accumulate: bool = False,
+                                epsilon: float = 1e-5) -> torch.Tensor:
+    """msa [S, N, cM], mask [S, N], pair [N, N, cZ]: the update (or msa + update) into `out`."""
+    s_, n, c = msa.shape
+    if out is None:
+        out = torch.empty_like(msa)
+    a = capi.lf_pair_averaging_args()
+    a.sequences, a.tokens, a.c_m, a.c_z = s_, n, c, pair.shape[-1]
+    a.heads, a.head_dim = heads, head_dim
+    a.msa_dtype, a.msa, a.msa_mask = act_code(msa), ptr(msa), ptr(mask)
+    a.pair_dtype, a.pair, a.out = act_code(pair), ptr(pair), ptr(out)
+    a.accumulate = int(accumulate)
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_msa_pair_weighted_averaging(ctx.handle, C.byref(a)))
+    return out
+
+
+def msa_module_weights(dw: DeviceWeights, w: dict) -> capi.lf_msa_module_weights:
+    """One AF3 MSA-module block (`msaBlock`, `cpu/af3/trunk/msa.js:233-287`): outerProductMean,
+    msaAttention1, msaTransition and the pair weights of a pairformer block."""
+    s = capi.lf_msa_module_weights()
+    s.outer_product_mean = opm_weights(dw, w["outerProductMean"], capi.LF_AF3)
+    s.c_outer = np.asarray(w["outerProductMean"]["leftProjection"]).shape[1]
+    s.msa_attention = pair_averaging_weights(dw, w["msaAttention1"])
+    s.msa_heads, s.msa_head_dim = w["msaAttention1"]["heads"], w["msaAttention1"]["dimension"]
+    s.msa_transition = transition_weights(dw, w["msaTransition"], capi.LF_TRANSITION_SWIGLU)
+    p = s.pair
+    p.tri_out = tri_mult_weights(dw, w["triangleMultiplicationOutgoing"], capi.LF_AF3)
+    p.tri_in = tri_mult_weights(dw, w["triangleMultiplicationIncoming"], capi.LF_AF3)
+    p.att_start = attention_weights_af3_grid(dw, w["pairAttention1"])
+    p.att_end = attention_weights_af3_grid(dw, w["pairAttention2"])
+    p.pair_heads = w["pairAttention1"]["heads"]
+    p.pair_transition = transition_weights(dw, w["pairTransition"], capi.LF_TRANSITION_SWIGLU)
+    return s
+
+
+def msa_module_block(ctx: Context, msa, pair, msa_mask, pair_mask, wstruct, msa_update_before_opm: bool,
+                     swap_transposed_bias=False, divide_by_length=False, transition_chunk_bytes=0, epsilon=1e-5):
+    """One AF3 MSA-module block, msa and pair updated in place."""
+    a = capi.lf_msa_block_args()
+    a.sequences, a.tokens, a.c_m = msa.shape
+    a.c_z = pair.shape[-1]
+    a.msa_update_before_opm = int(msa_update_before_opm)
+    a.swap_transposed_bias, a.divide_by_length = int(swap_transposed_bias), int(divide_by_length)
+    a.msa_dtype, a.msa, a.pair_dtype, a.pair = act_code(msa), ptr(msa), act_code(pair), ptr(pair)
+    a.msa_mask, a.pair_mask = ptr(msa_mask), ptr(pair_mask)
+    a.transition_chunk_bytes = transition_chunk_bytes
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_msa_module_block(ctx.handle, C.byref(a)))

@@ -445,6 +445,35 @@ def synthetic_pairformer_weights(c_z, c_s, heads_pair, heads_single, dim_single,
     return w
 
 
+def synthetic_msa_module_weights(c_m: int = 64, c_z: int = 128, heads: int = 8, dim: int = 8,
+                                 heads_pair: int = 4, c_outer: int = 32, seed: int = 13, factor: int = 4) -> dict:
+    """Random-init AF3 MSA-module block weights (`msaBlock`, `cpu/af3/trunk/msa.js:233-287`): the
+    pair-only pairformer block's, plus `msaAttention1` (`msaAttention`, `:157-219`), the SwiGLU
+    `msaTransition` and the AF3 `outerProductMean` (`:72-155`); all (in,out), N(0, 1/fan_in)."""
+    w = synthetic_pairformer_weights(c_z, 32, heads_pair, 2, 16, seed=seed, factor=factor)
+    for key in ("singlePairLogitsNormScale", "singlePairLogitsNormOffset", "singlePairLogitsProjection",
+                "singleAttention", "singleTransition"):
+        del w[key]
+    st = Stream(seed + 1000)
+
+    def lin(i, o):
+        return st.normal(i * o, 1.0 / np.sqrt(i)).reshape(i, o)
+
+    hw = heads * dim
+    w["msaAttention1"] = {"heads": heads, "dimension": dim,
+                          "actNormScale": st.values(c_m, 0.2, 1), "actNormOffset": st.values(c_m, 0.1),
+                          "pairNormScale": st.values(c_z, 0.2, 1), "pairNormOffset": st.values(c_z, 0.1),
+                          "pairLogits": lin(c_z, heads), "vProjection": lin(c_m, hw),
+                          "gatingQuery": lin(c_m, hw), "outputProjection": lin(hw, c_m)}
+    w["msaTransition"] = {"inputLayerNormScale": st.values(c_m, 0.2, 1), "inputLayerNormOffset": st.values(c_m, 0.1),
+                          "transition1": lin(c_m, 2 * factor * c_m), "transition2": lin(factor * c_m, c_m)}
+    w["outerProductMean"] = {"layerNormInputScale": st.values(c_m, 0.2, 1), "layerNormInputOffset": st.values(c_m, 0.1),
+                             "leftProjection": lin(c_m, c_outer), "rightProjection": lin(c_m, c_outer),
+                             "outputW": st.normal(c_outer * c_outer * c_z, 1.0 / c_outer).reshape(c_outer * c_outer, c_z),
+                             "outputB": st.values(c_z, 0.05)}
+    return w
+
+
 def config3_attention_weights(c: int, heads: int, seed: int) -> dict:
     """BASELINE config 3 triangle-attention weights: N(0, 1/fan_in) masters, LN scale ~1."""
     s = Stream(seed)

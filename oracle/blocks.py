@@ -83,3 +83,26 @@ def pairformer_block_af3(pair, single, pair_mask, seq_mask, w, swap_transposed_b
     single = _add(single, ops.transition_af3(single, w["singleTransition"], eps=eps))
     assert logits.shape == (heads, n, n)
     return pair, single
+
+
+def msa_block_af3(msa, pair, msa_mask, pair_mask, w, msa_update_before_opm, swap_transposed_bias=False,
+                  divide_by_length=False, eps=1e-5):
+    """One AF3 MSA-module block, `msaBlock` (`cpu/af3/trunk/msa.js:233-287`): the outer product
+    mean into the pair and the MSA update (pair-weighted averaging, then the SwiGLU transition)
+    in the dialect's order, then the pair steps of a pair-only pairformer block.
+    Returns (msa, pair)."""
+    def opm(m, p):
+        return _add(p, ops.outer_product_mean_af3(m, msa_mask, w["outerProductMean"], eps))
+
+    def update(m, p):
+        m = _add(m, ops.msa_pair_weighted_averaging_af3(m, msa_mask, p, w["msaAttention1"], eps))
+        return _add(m, ops.transition_af3(m, w["msaTransition"], eps=eps))
+
+    if msa_update_before_opm:
+        msa = update(msa, pair)
+        pair = opm(msa, pair)
+    else:
+        pair = opm(msa, pair)
+        msa = update(msa, pair)
+    pair, _ = pairformer_block_af3(pair, None, pair_mask, None, w, swap_transposed_bias, divide_by_length, eps)
+    return msa, pair

@@ -318,6 +318,29 @@ def global_column_attention_af2(msa, mask, w, heads, eps=1e-5):
     return linear(gated, w["outputWeight"], w["outputBias"])
 
 
+def msa_pair_weighted_averaging_af3(msa, mask, pair, w, eps=1e-5):
+    """AF3 MSA pair-weighted averaging, `msaAttention` (`cpu/af3/trunk/msa.js:157-219`):
+    fast-variance LN of the msa (actNorm) and of the pair (pairNorm); logits
+    LN(pair) . pairLogits [cZ, H] (no bias); the key mask is the maximum of the MSA mask over
+    the sequences (`:177-186`), added as 1e9 (keyMask - 1); softmax over j per (h, i), shared by
+    every sequence; averaged = softmax . (x vProjection), times sigmoid(x gatingQuery), then
+    outputProjection.  All weights (in,out), no biases.  Returns the msa update [S, N, C]."""
+    s_, n, c = msa.shape
+    heads, d = w["heads"], w["dimension"]
+    x = layer_norm(msa, w["actNormScale"], w["actNormOffset"], eps, fast_variance=True)
+    pn = layer_norm(pair, w["pairNormScale"], w["pairNormOffset"], eps, fast_variance=True)
+    flat = np.asarray(linear(pn, w["pairLogits"]), F64)                # [N, N, H]
+    key_mask = np.asarray(mask, F64).max(0)                           # [N]
+    logits = flat.transpose(2, 0, 1) + 1e9 * (key_mask[None, None, :] - 1.0)
+    logits = logits - logits.max(-1, keepdims=True)
+    p = np.exp(logits)
+    p = np.asarray(_f32(p / p.sum(-1, keepdims=True)), F64)          # [H, N, N]
+    values = np.asarray(linear(x, w["vProjection"]), F64).reshape(s_, n, heads, d)
+    averaged = np.einsum("hij,sjhd->sihd", p, values).reshape(s_, n, heads * d)
+    gate = sigmoid(np.asarray(linear(x, w["gatingQuery"]), F64))
+    return linear(_f32(averaged * gate), w["outputProjection"])
+
+
 # ---------------------------------------------------------------------------------------
 # Outer product mean and transitions
 # ---------------------------------------------------------------------------------------

@@ -1,0 +1,174 @@
+"""AF3 MSA module: pair-weighted averaging (`msaAttention`, cpu/af3/trunk/msa.js:157-219) and
+the MSA-module block (`msaBlock`, :233-287).
+
+CPU: the oracle against what the reference's semantics fix (one token, uniform logits, the
+key mask as the maximum over the sequences, a token no sequence covers is the same as a
+deleted token, sequences do not mix, both block orderings move both outputs as
+test/opendde-branches.test.js:135-230 asserts, and equal ones when the outer product's output
+is zero).  GPU: the C ABI against the oracle."""
+import numpy as np
+import pytest
+
+from localfold_amd import synthetic as S
+from oracle import blocks, ops
+from tests import helpers as H
+
+
+def _avg_inputs(s, n, cm, cz, heads, dim, seed):
+    w = S.synthetic_msa_module_weights(c_m=cm, c_z=cz, heads=heads, dim=dim, heads_pair=2, c_outer=8,
+                                       seed=seed)["msaAttention1"]
+    st = S.Stream(seed + 7)
+    msa = st.normal(s * n * cm).reshape(s, n, cm).astype(np.float32)
+    pair = st.normal(n * n * cz).reshape(n, n, cz).astype(np.float32)
+    mask = np.ones((s, n), np.float32)
+    return w, msa, pair, mask
+
+
+def _values_gate(msa, w):
+    x = np.asarray(ops.layer_norm(msa, w["actNormScale"], w["actNormOffset"], 1e-5, fast_variance=True), np.float64)
+    return x @ w["vProjection"], ops.sigmoid(x @ w["gatingQuery"])
+
+
+def test_oracle_single_token_closed_form():
+    """One token: every softmax is 1, the update is (v * sigmoid(g)) Wo whatever the pair."""
+    w, msa, pair, mask = _avg_inputs(4, 1, 32, 16, 4, 8, 1)
+    got = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    v, g = _values_gate(msa, w)
+    np.testing.assert_allclose(got, (v * g) @ w["outputProjection"], rtol=2e-5, atol=2e-5)
+    got2 = ops.msa_pair_weighted_averaging_af3(msa, mask, pair * 3 + 1, w)
+    np.testing.assert_allclose(got2, got, rtol=1e-6, atol=1e-6)
+
+
+def test_oracle_zero_logits_average_the_covered_tokens():
+    """pairLogits = 0: each head averages the values of the tokens some sequence covers,
+    uniformly; a token masked in only some sequences still counts (maximum over sequences)."""
+    w, msa, pair, mask = _avg_inputs(3, 6, 32, 16, 4, 8, 2)
+    w = dict(w, pairLogits=np.zeros_like(w["pairLogits"]))
+    mask[:, 4] = 0          # no sequence covers token 4
+    mask[0, 1] = 0          # token 1 is covered by sequences 1 and 2
+    got = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    v, g = _values_gate(msa, w)
+    keep = [0, 1, 2, 3, 5]
+    mean = v[:, keep].mean(1, keepdims=True)                      # [S, 1, H*d]
+    np.testing.assert_allclose(got, (mean * g) @ w["outputProjection"], rtol=2e-5, atol=2e-5)
+
+
+def test_oracle_uncovered_token_equals_deleted_token():
+    """A token no sequence covers is out of every softmax: the other tokens' updates equal
+    those of the problem with that token's msa column and pair row and column deleted."""
+    w, msa, pair, mask = _avg_inputs(3, 7, 32, 16, 4, 8, 3)
+    mask[:, 2] = 0
+    mask[1, 5] = 0
+    got = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    keep = [0, 1, 3, 4, 5, 6]
+    ref = ops.msa_pair_weighted_averaging_af3(msa[:, keep], mask[:, keep], pair[keep][:, keep], w)
+    np.testing.assert_allclose(got[:, keep], ref, rtol=2e-5, atol=2e-5)
+
+
+def test_oracle_sequences_do_not_mix():
+    """The weights come from the pair alone: a sequence's update depends on its own row only,
+    so permuting sequences permutes updates and changing one row leaves the others."""
+    w, msa, pair, mask = _avg_inputs(5, 6, 32, 16, 4, 8, 4)
+    a = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    perm = np.array([2, 4, 0, 1, 3])
+    b = ops.msa_pair_weighted_averaging_af3(msa[perm], mask[perm], pair, w)
+    np.testing.assert_allclose(b, a[perm], rtol=1e-6, atol=1e-6)
+    msa2 = msa.copy()
+    msa2[3] = S.Stream(99).normal(6 * 32).reshape(6, 32)
+    c = ops.msa_pair_weighted_averaging_af3(msa2, mask, pair, w)
+    np.testing.assert_allclose(c[[0, 1, 2, 4]], a[[0, 1, 2, 4]], rtol=1e-6, atol=1e-6)
+
+
+def _block_inputs(s, n, seed, cm=32, cz=16):
+    w = S.synthetic_msa_module_weights(c_m=cm, c_z=cz, heads=4, dim=8, heads_pair=2, c_outer=8, seed=seed)
+    act = S.synthetic_activations(s, n, cm, cz, seed=seed + 50)
+    return w, act
+
+
+def test_oracle_block_orderings_differ():
+    """Both orderings over one set of weights move both the msa and the pair
+    (test/opendde-branches.test.js:213-224)."""
+    w, act = _block_inputs(3, 5, 5)
+    a = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w, False)
+    b = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w, True)
+    for x, y in zip(a, b):
+        assert np.sqrt(np.mean((x - y) ** 2)) / np.sqrt(np.mean(x ** 2)) > 1e-6
+
+
+def test_oracle_block_orderings_agree_without_outer_product():
+    """With the outer product's output zeroed the two orderings are one function, and with the
+    MSA update's outputs zeroed as well the msa passes through and the pair is the pair-only
+    pairformer block's."""
+    w, act = _block_inputs(3, 5, 6)
+    opm = dict(w["outerProductMean"], outputW=np.zeros_like(w["outerProductMean"]["outputW"]),
+               outputB=np.zeros_like(w["outerProductMean"]["outputB"]))
+    w0 = dict(w, outerProductMean=opm)
+    a = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w0, False)
+    b = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w0, True)
+    for x, y in zip(a, b):
+        np.testing.assert_allclose(x, y, rtol=1e-6, atol=1e-6)
+    att = dict(w["msaAttention1"], outputProjection=np.zeros_like(w["msaAttention1"]["outputProjection"]))
+    tr = dict(w["msaTransition"], transition2=np.zeros_like(w["msaTransition"]["transition2"]))
+    w1 = dict(w0, msaAttention1=att, msaTransition=tr)
+    m, p = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w1, False)
+    np.testing.assert_array_equal(m, act["msa"])
+    rp, _ = blocks.pairformer_block_af3(act["pair"], None, act["pairMask"], None, w1)
+    np.testing.assert_allclose(p, rp, rtol=1e-6, atol=1e-6)
+
+
+def _dev(ctx, x, dt=None):
+    import torch
+    t = torch.as_tensor(np.ascontiguousarray(x)).to(ctx.device)
+    return t.to(dt) if dt is not None else t
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("s,n,cm,cz,heads,dim,dt", [(4, 9, 32, 16, 4, 8, "float32"),
+                                                    (40, 70, 64, 128, 8, 8, "bfloat16"),
+                                                    (7, 130, 64, 32, 2, 32, "float16"),
+                                                    (3, 5, 16, 16, 2, 4, "float32")])
+def test_pair_weighted_averaging(ctx, s, n, cm, cz, heads, dim, dt):
+    """The op (update only) against the oracle; ragged token counts (keys past one 64-key
+    chunk), a token masked in some sequences, a token no sequence covers."""
+    import torch
+    from localfold_amd import device as D
+    w, msa, pair, mask = _avg_inputs(s, n, cm, cz, heads, dim, s + n)
+    mask[0, 1] = 0
+    mask[:, n - 2] = 0
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.pair_averaging_weights(dw, w)
+    x, p = _dev(ctx, msa, getattr(torch, dt)), _dev(ctx, pair, getattr(torch, dt))
+    out = D.msa_pair_weighted_averaging(ctx, x, _dev(ctx, mask), p, ws, heads, dim)
+    torch.cuda.synchronize()
+    ref = ops.msa_pair_weighted_averaging_af3(x.float().cpu().numpy(), mask, p.float().cpu().numpy(), w)
+    H.assert_close(out.float().cpu().numpy(), ref, label=f"pwa {s}x{n} {dt}")
+
+
+@pytest.mark.gpu
+def test_pair_weighted_averaging_in_place(ctx):
+    import torch
+    from localfold_amd import device as D
+    w, msa, pair, mask = _avg_inputs(6, 20, 64, 32, 8, 8, 11)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.pair_averaging_weights(dw, w)
+    x = _dev(ctx, msa)
+    D.msa_pair_weighted_averaging(ctx, x, _dev(ctx, mask), _dev(ctx, pair), ws, 8, 8, out=x, accumulate=True)
+    torch.cuda.synchronize()
+    ref = msa.astype(np.float64) + ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    H.assert_close(x.cpu().numpy(), ref, label="pwa in place")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("s,n,before", [(5, 12, False), (5, 12, True), (33, 40, False)])
+def test_msa_module_block(ctx, s, n, before):
+    import torch
+    from localfold_amd import device as D
+    w, act = _block_inputs(s, n, 7 + n, cm=64, cz=32)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.msa_module_weights(dw, w)
+    msa, pair = _dev(ctx, act["msa"]), _dev(ctx, act["pair"])
+    D.msa_module_block(ctx, msa, pair, _dev(ctx, act["msaMask"]), _dev(ctx, act["pairMask"]), ws, before)
+    torch.cuda.synchronize()
+    rm, rp = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w, before)
+    H.assert_close(msa.cpu().numpy(), rm, label=f"msa module msa before={before}")
+    H.assert_close(pair.cpu().numpy(), rp, label=f"msa module pair before={before}")
