@@ -206,6 +206,38 @@ def extra_msa_block_n384(ctx, D, synthetic, reps):
             "ms_per_block": round(ms, 3), "outputs_finite": finite, "kernels_ms": kern}
 
 
+def msa_module_block_n384(ctx, D, synthetic, reps):
+    """One AF3 MSA-module block (msaBlock, AF3 ordering) at N_tokens=384 with 1024 MSA rows,
+    c_m=64, c_z=128, pair-weighted averaging 8x8, c_outer=32, int8 weights, bf16 activations."""
+    import torch
+    n, s_, cm, cz = 384, 1024, 64, 128
+    dev = ctx.device
+    w = synthetic.quantise_tree(synthetic.synthetic_msa_module_weights(
+        c_m=cm, c_z=cz, heads=8, dim=8, heads_pair=4, c_outer=32), "int8", 64)
+    dw = D.DeviceWeights(dev)
+    ws = D.msa_module_weights(dw, w)
+    g = torch.Generator(device=dev).manual_seed(13)
+    msa = torch.randn(s_, n, cm, device=dev, generator=g).to(torch.bfloat16)
+    pair = torch.randn(n, n, cz, device=dev, generator=g).to(torch.bfloat16)
+    mm = (torch.rand(s_, n, device=dev, generator=g) > 0.2).float()
+    pm = torch.ones(n, n, device=dev)
+    msa0, pair0 = msa.clone(), pair.clone()
+
+    def block():
+        D.msa_module_block(ctx, msa, pair, mm, pm, ws, False)
+
+    block()
+    msa.copy_(msa0)
+    pair.copy_(pair0)
+    ms = timed(block, reps)
+    kern = profile_ops(ctx, block, 2)
+    finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
+    return {"workload": f"one AF3 MSA-module block (AF3 order): N_tokens={n}, N_msa={s_}, c_m={cm}, c_z={cz}, "
+                        "pair-weighted averaging 8x8, pair attention 4 heads, int8 weights (fp16 scales, groups "
+                        "of 64), bf16 activations, 20% of MSA positions masked; synthetic",
+            "ms_per_block": round(ms, 3), "outputs_finite": finite, "kernels_ms": kern}
+
+
 def evoformer_stack_config4(ctx, D, synthetic, reps):
     """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
     pass (1 recycle), 48 distinct int8 weight sets, bf16 activations, through lf_evoformer_stack."""
@@ -378,6 +410,8 @@ def main():
         extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
         log("extra-MSA block ...")
         extras["extra_msa_block"] = extra_msa_block_n384(ctx, D, synthetic, 5)
+        log("AF3 MSA-module block ...")
+        extras["msa_module_block"] = msa_module_block_n384(ctx, D, synthetic, 5)
         log("config 5: one Pairformer block ...")
         extras["pairformer_block"] = pairformer_block_config5(ctx, D, synthetic, 5)
 
@@ -415,6 +449,7 @@ def main():
         "evoformer_stack": extras.get("evoformer_stack"),
         "pairformer_block": extras.get("pairformer_block"),
         "extra_msa_block": extras.get("extra_msa_block"),
+        "msa_module_block": extras.get("msa_module_block"),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -75,17 +75,142 @@ __global__ __launch_bounds__(256) void keybias_kernel(const float* mask, float* 
 }
 
 // One key-bias row shared by every batch row, from the mask's maximum over the batch
-// (AF3 pair-weighted averaging: a token any sequence covers is a key for every sequence)
-__global__ __launch_bounds__(256) void keymax_kernel(const float* mask, float* kb, int B, int Q, int Qp) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
-  if (k >= Qp) return;
-  if (k >= Q) {
-    kb[k] = -1e30f;
-    return;
-  }
+// (AF3 pair-weighted averaging: a token any sequence covers is a key for every sequence).
+// A block covers 64 keys with 16 rows of 64 lanes; each lane strides the batch by 16.
+__global__ __launch_bounds__(1024) void keymax_kernel(const float* mask, float* kb, int B, int Q, int Qp) {
+  __shared__ float part[16][64];
+  const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + lane;
   float m = 0.f;
-  for (int b = 0; b < B; ++b) m = fmaxf(m, mask[(long long)b * Q + k]);
-  kb[k] = (1e9f * LOG2E) * (m - 1.0f);
+  if (k < Q) {
+#pragma unroll 8
+    for (int b = r; b < B; b += 16) m = fmaxf(m, mask[(long long)b * Q + k]);
+  }
+  part[r][lane] = m;
+  __syncthreads();
+  if (r == 0 && k < Qp) {
+#pragma unroll
+    for (int i = 1; i < 16; ++i) m = fmaxf(m, part[i][lane]);
+    kb[k] = k < Q ? (1e9f * LOG2E) * (m - 1.0f) : -1e30f;
+  }
+}
+
+// Pair-weighted averaging, step 1: P[h][i][j] = softmax_j(bias[h][i][j] + kb[j]) in base 2,
+// written as f16 over the bias rows (row stride Qp), keys past Q zero.  One wave per row.
+// Every key masked: the 1e9 term swamps the logits in f32 and the row is uniform over the
+// Q keys, as in the reference's f32 softmax.
+__global__ __launch_bounds__(256) void pwa_softmax_kernel(_Float16* bias, const float* kb, int rows, int Q, int Qp) {
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  _Float16* r = bias + row * Qp;
+  float m = -3.0e38f;
+  for (int j = lane; j < Q; j += 64) m = fmaxf(m, (float)r[j] + kb[j]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float t = 0.f;
+  for (int j = lane; j < Q; j += 64) t += exp2f((float)r[j] + kb[j] - m);
+  t = wave_sum(t);
+  const float inv = 1.f / t;
+  for (int j = lane; j < Qp; j += 64) r[j] = (_Float16)(j < Q ? exp2f((float)r[j] + kb[j] - m) * inv : 0.f);
+}
+
+// Pair-weighted averaging, step 2, per head h an NT GEMM on the matrix cores:
+//   O^T[n][i] = sum_j Vt[n][j] P[i][j],  n = (s, e) over sequences s and head dims e < d,
+// gated and stored as o[(s Q + i)][h d + e] = O * g.  Vt rows: vt + ((s H + h) d + e) Qp.
+// Block: 4 waves in 2 x 2, a 128 (n) x 128 (i) tile; a wave holds 4 x 4 16x16 accumulators and
+// reads its fragments straight from L2 (P of one head is shared by every block of that head).
+// A lane's 4 accumulator rows are 4 consecutive n, i.e. 4 consecutive head dims of one
+// sequence (d % 4 == 0), stored as one 8-byte word.
+constexpr int PWA_T = 128;
+struct PwaParams {
+  const _Float16 *vt, *p, *g;
+  _Float16* o;
+  int S, H, Q, Qp, d, HD;
+  int ntn, nti;             // tiles along n and i per head
+  long long nblocks;
+};
+
+__global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  // XCD-aware order: each XCD walks a contiguous range, i tiles fastest, so the blocks that
+  // share one n tile of V (and one head of P) run on one L2
+  long long lb = blockIdx.x;
+  const long long per = p.nblocks / 8;
+  if (lb < per * 8) lb = (lb % 8) * per + lb / 8;
+  const int ti = (int)(lb % p.nti);
+  const int tn = (int)((lb / p.nti) % p.ntn);
+  const int h = (int)(lb / ((long long)p.nti * p.ntn));
+  const int N = p.S * p.d;
+  const int n0 = tn * PWA_T + (wave & 1) * 64, i0 = ti * PWA_T + (wave >> 1) * 64;
+
+  const _Float16* arow[4];
+  const _Float16* brow[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int n = min(n0 + t * 16 + r16, N - 1);
+    const int s = n / p.d, e = n - s * p.d;
+    arow[t] = p.vt + ((long long)(s * p.H + h) * p.d + e) * p.Qp + g4 * 8;
+    const int i = min(i0 + t * 16 + r16, p.Q - 1);
+    brow[t] = p.p + ((long long)h * p.Q + i) * p.Qp + g4 * 8;
+  }
+  f4 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+  h8 fa[4], fb[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    fa[t] = *(const h8*)arow[t];
+    fb[t] = *(const h8*)brow[t];
+  }
+  for (int k0 = 0; k0 < p.Qp; k0 += 32) {
+    // next step's fragments (clamped to the last step: unconditional loads keep the waits exact)
+    const int kn = min(k0 + 32, p.Qp - 32);
+    h8 na[4], nb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      na[t] = *(const h8*)(arow[t] + kn);
+      nb[t] = *(const h8*)(brow[t] + kn);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(fa[a], fb[b], acc[a][b]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      fa[t] = na[t];
+      fb[t] = nb[t];
+    }
+  }
+  // epilogue: gate values first (loads ahead of every store), then the gated stores
+  h4 gv[4][4];
+  long long oi[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int n = min(n0 + a * 16 + g4 * 4, N - 4);
+    const int s = n / p.d, e = n - s * p.d;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int i = min(i0 + b * 16 + r16, p.Q - 1);
+      oi[a][b] = ((long long)s * p.Q + i) * p.HD + h * p.d + e;
+      gv[a][b] = *(const h4*)(p.g + oi[a][b]);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const bool nok = n0 + a * 16 + g4 * 4 < N;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (!nok || i0 + b * 16 + r16 >= p.Q) continue;
+      h4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (_Float16)(acc[a][b][j] * (float)gv[a][b][j]);
+      *(h4*)(p.o + oi[a][b]) = v;
+    }
+  }
 }
 
 // (float)v[i] + c in one instruction (i is a constant once the caller's loop is unrolled)
@@ -487,7 +612,12 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     pp.g[gbias] = Group{views[5], WView{}, H, OP_STORE, LOG2E, nullptr, nullptr, Dst{}};
   }
 
-  size_t sizes[9] = {qkv, qkv, qkv, hd, hd, (size_t)(shared_key_mask ? 1 : B) * Qp * sizeof(float), biash, expanded_bytes(views[4]),
+  // pair-weighted averaging with d % 4 == 0: one softmax per (h, i) and an NT GEMM over the
+  // sequences instead of flash attention per sequence; V^T compact, [b][h][d][Qp]
+  const bool pwa = no_qk && shared_key_mask && d % 4 == 0 && !a.transpose && a.bias_mode != LF_BIAS_NONE;
+  const size_t vsize = pwa ? (size_t)B * HD * Qp * sizeof(_Float16) : qkv;
+  const size_t qksize = pwa ? 256 : qkv;
+  size_t sizes[9] = {qksize, qksize, vsize, hd, hd, (size_t)(shared_key_mask ? 1 : B) * Qp * sizeof(float), biash, expanded_bytes(views[4]),
                      std::max(lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb)
                                                                                        : (size_t)0)};
   LF_TRY(workspace(ctx, sizes, bufs, 9));
@@ -499,7 +629,9 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[7], &wo, "attention.expand"));
   // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
   // exact 0, which must not meet a non-finite value)
-  if (d < FA_DP || no_qk) {
+  if (pwa) {
+    if (Qp != Q) LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, vsize, ctx->stream), "attention memset"));
+  } else if (d < FA_DP || no_qk) {
     for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
   } else if (Qp != Q) {
     LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, qkv, ctx->stream), "attention memset"));
@@ -515,7 +647,8 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     const long long hq = (long long)Qp * FA_DP;
     if (gq >= 0) pp.g[gq].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
     if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    pp.g[gv].dst = Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
+    pp.g[gv].dst = pwa ? Dst{vb, DT_F16, Q, (long long)HD * Qp, 1, d, (long long)d * Qp, Qp}
+                       : Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
     pp.g[gg].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
     if (gbias >= 0) pp.g[gbias].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
@@ -525,8 +658,8 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   {
     LaunchScope ls(ctx, "attention.keybias");
     if (shared_key_mask)
-      hipLaunchKernelGGL(keymax_kernel, dim3((unsigned)((Qp + 255) / 256)), dim3(256), 0, ctx->stream, a.mask, keyb,
-                         B, Q, Qp);
+      hipLaunchKernelGGL(keymax_kernel, dim3((unsigned)(Qp / 64)), dim3(1024), 0, ctx->stream, a.mask, keyb, B, Q,
+                         Qp);
     else
       hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0,
                          ctx->stream, a.mask, keyb, B, Q, Qp, a.transpose);
@@ -537,8 +670,35 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   if (a.bias_mode == LF_BIAS_LOGITS)
     LF_TRY(f32_to_f16(ctx, a.bias_logits, bias16, (long long)H * Q * Q, a.swap_bias ? Q : 0, LOG2E, Q, Qp));
 
-  // 4. flash attention
-  {
+  // 4. flash attention, or the pair-weighted averaging's softmax + GEMM
+  if (pwa) {
+    {
+      LaunchScope ls(ctx, "attention.pwa_softmax");
+      hipLaunchKernelGGL(pwa_softmax_kernel, dim3((unsigned)(((long long)H * Q + 3) / 4)), dim3(256), 0, ctx->stream,
+                         bias16, keyb, H * Q, Q, Qp);
+    }
+    LF_TRY(check_hip(hipGetLastError(), "pwa softmax launch"));
+    PwaParams wp{};
+    wp.vt = vb;
+    wp.p = bias16;
+    wp.g = gb;
+    wp.o = ob;
+    wp.S = B;
+    wp.H = H;
+    wp.Q = Q;
+    wp.Qp = Qp;
+    wp.d = d;
+    wp.HD = HD;
+    wp.ntn = (int)(((long long)B * d + PWA_T - 1) / PWA_T);
+    wp.nti = (Q + PWA_T - 1) / PWA_T;
+    wp.nblocks = (long long)wp.ntn * wp.nti * H;
+    LF_REQUIRE((long long)B * d < (1LL << 31) && wp.nblocks < (1LL << 31), "attention: too many sequences");
+    {
+      LaunchScope ls(ctx, "attention.pwa_average");
+      hipLaunchKernelGGL(pwa_average_kernel, dim3((unsigned)wp.nblocks), dim3(256), 0, ctx->stream, wp);
+    }
+    LF_TRY(check_hip(hipGetLastError(), "pwa average launch"));
+  } else {
     FlashParams fp{};
     fp.q = qb;
     fp.k = kb;

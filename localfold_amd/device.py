@@ -567,7 +567,8 @@ def msa_module_weights(dw: DeviceWeights, w: dict) -> capi.lf_msa_module_weights
     msaAttention1, msaTransition and the pair weights of a pairformer block."""
     s = capi.lf_msa_module_weights()
     s.outer_product_mean = opm_weights(dw, w["outerProductMean"], capi.LF_AF3)
-    s.c_outer = np.asarray(w["outerProductMean"]["leftProjection"]).shape[1]
+    left = w["outerProductMean"]["leftProjection"]   # an array, or a stored record (quantised)
+    s.c_outer = left["shape"][-1] if isinstance(left, dict) else np.shape(left)[-1]
     s.msa_attention = pair_averaging_weights(dw, w["msaAttention1"])
     s.msa_heads, s.msa_head_dim = w["msaAttention1"]["heads"], w["msaAttention1"]["dimension"]
     s.msa_transition = transition_weights(dw, w["msaTransition"], capi.LF_TRANSITION_SWIGLU)

@@ -126,10 +126,12 @@ def _dev(ctx, x, dt=None):
 @pytest.mark.parametrize("s,n,cm,cz,heads,dim,dt", [(4, 9, 32, 16, 4, 8, "float32"),
                                                     (40, 70, 64, 128, 8, 8, "bfloat16"),
                                                     (7, 130, 64, 32, 2, 32, "float16"),
-                                                    (3, 5, 16, 16, 2, 4, "float32")])
+                                                    (3, 5, 16, 16, 2, 4, "float32"),
+                                                    (6, 70, 16, 16, 4, 6, "bfloat16")])
 def test_pair_weighted_averaging(ctx, s, n, cm, cz, heads, dim, dt):
     """The op (update only) against the oracle; ragged token counts (keys past one 64-key
-    chunk), a token masked in some sequences, a token no sequence covers."""
+    chunk), a token masked in some sequences, a token no sequence covers; head widths that are
+    multiples of 4 run the softmax + GEMM path, 6 the flash path."""
     import torch
     from localfold_amd import device as D
     w, msa, pair, mask = _avg_inputs(s, n, cm, cz, heads, dim, s + n)
