@@ -329,6 +329,46 @@ typedef struct {
  * in pairformerBlock order (cpu/af3/trunk/pairformer.js:495-541). */
 int lf_pairformer_block(lf_context* ctx, const lf_pairformer_block_args* args);
 
+/* ---- AF2 input and recycling embedder -------------------------------------------------- */
+
+/* All f32 on the device, (in,out) layout (InputEmbedderGpu's packWeights,
+ * webgpu/af2/evoformer/input-embedder.js:9-26). */
+typedef struct {
+  const float *preprocess_1d_w, *preprocess_1d_b;     /* [Ct x cM], [cM] */
+  const float *preprocess_msa_w, *preprocess_msa_b;   /* [Cf x cM], [cM] */
+  const float *left_w, *left_b, *right_w, *right_b;   /* [Ct x cZ], [cZ] */
+  const float *prev_pos_w, *prev_pos_b;               /* [15 x cZ], [cZ] */
+  const float *prev_msa_norm_scale, *prev_msa_norm_offset;    /* [cM] */
+  const float *prev_pair_norm_scale, *prev_pair_norm_offset;  /* [cZ] */
+  const float *relpos_w, *relpos_b;                   /* [65 x cZ], [cZ] */
+  const float *extra_w, *extra_b;                     /* [25 x cE], [cE] */
+} lf_input_embedder_weights;
+
+typedef struct {
+  int length, msa_sequences, extra_sequences;
+  int target_channels, msa_feature_channels;          /* 22, 49 in AF2 */
+  int c_m, c_z, c_e;                                  /* 256, 128, 64 */
+  const float* target_feat;       /* [L, Ct] */
+  const float* msa_feat;          /* [S, L, Cf] */
+  const float* extra_msa;         /* [Se, L] residue codes 0..22 as f32 */
+  const float* extra_has_deletion;    /* [Se, L] */
+  const float* extra_deletion_value;  /* [Se, L] */
+  const float* residue_index;     /* [L] */
+  const float* aatype;            /* [L] */
+  const void* prev_msa_first_row; /* [L, cM], msa_dtype; NULL = zeros (recycle 0) */
+  const void* prev_pair;          /* [L, L, cZ], pair_dtype; NULL = zeros */
+  const float* prev_positions;    /* [L, 37, 3] atom37; NULL = zeros */
+  int msa_dtype;   void* msa;     /* out [S, L, cM] */
+  int pair_dtype;  void* pair;    /* out [L, L, cZ]; may alias prev_pair (read and written per row) */
+  int extra_dtype; void* extra;   /* out [Se, L, cE] */
+  float epsilon;                  /* 1e-5 */
+  const lf_input_embedder_weights* w;
+} lf_input_embedder_args;
+
+/* Replaces InputEmbedderGpu.run / encodeInputEmbedder (webgpu/af2/evoformer/input-embedder.js:
+ * 160-231): the MSA, pair (without templates) and extra-MSA embeddings of one recycle. */
+int lf_input_embedder(lf_context* ctx, const lf_input_embedder_args* args);
+
 /* ---- AF3 MSA module ------------------------------------------------------------------- */
 
 /* Pair-weighted averaging weights (`msaAttention1`, cpu/af3/trunk/msa.js:157-219), no biases. */

@@ -137,6 +137,24 @@ class lf_pairformer_block_args(C.Structure):
                 ("epsilon", C.c_float), ("w", C.POINTER(lf_pairformer_weights))]
 
 
+class lf_input_embedder_weights(C.Structure):
+    _fields_ = [(n, P) for n in ("preprocess_1d_w", "preprocess_1d_b", "preprocess_msa_w", "preprocess_msa_b",
+                                 "left_w", "left_b", "right_w", "right_b", "prev_pos_w", "prev_pos_b",
+                                 "prev_msa_norm_scale", "prev_msa_norm_offset", "prev_pair_norm_scale",
+                                 "prev_pair_norm_offset", "relpos_w", "relpos_b", "extra_w", "extra_b")]
+
+
+class lf_input_embedder_args(C.Structure):
+    _fields_ = ([(n, C.c_int) for n in ("length", "msa_sequences", "extra_sequences", "target_channels",
+                                        "msa_feature_channels", "c_m", "c_z", "c_e")]
+                + [(n, P) for n in ("target_feat", "msa_feat", "extra_msa", "extra_has_deletion",
+                                    "extra_deletion_value", "residue_index", "aatype", "prev_msa_first_row",
+                                    "prev_pair", "prev_positions")]
+                + [("msa_dtype", C.c_int), ("msa", P), ("pair_dtype", C.c_int), ("pair", P),
+                   ("extra_dtype", C.c_int), ("extra", P), ("epsilon", C.c_float),
+                   ("w", C.POINTER(lf_input_embedder_weights))])
+
+
 class lf_pair_averaging_weights(C.Structure):
     _fields_ = [("act_norm_scale", P), ("act_norm_offset", P), ("pair_norm_scale", P), ("pair_norm_offset", P),
                 ("pair_logits", lf_weight), ("wv", lf_weight), ("wg", lf_weight), ("wo", lf_weight)]
@@ -189,6 +207,7 @@ PROTOTYPES = [
     ("lf_extra_msa_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights), C.c_int]),
     ("lf_evoformer_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
     ("lf_pairformer_block", C.c_int, [P, C.POINTER(lf_pairformer_block_args)]),
+    ("lf_input_embedder", C.c_int, [P, C.POINTER(lf_input_embedder_args)]),
     ("lf_msa_pair_weighted_averaging", C.c_int, [P, C.POINTER(lf_pair_averaging_args)]),
     ("lf_msa_module_block", C.c_int, [P, C.POINTER(lf_msa_block_args)]),
 ]

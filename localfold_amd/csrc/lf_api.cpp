@@ -269,6 +269,7 @@ inline int impl_lf_outer_product_mean(lf_context* c, const lf_opm_args& a) { ret
 inline int impl_lf_global_column_attention(lf_context* c, const lf_global_attention_args& a) {
   return global_attention(c, a);
 }
+inline int impl_lf_input_embedder(lf_context* c, const lf_input_embedder_args& a) { return input_embedder(c, a); }
 }  // namespace lf
 
 extern "C" {
@@ -277,4 +278,5 @@ LF_ENTRY(lf_attention, lf_attention_args)
 LF_ENTRY(lf_transition, lf_transition_args)
 LF_ENTRY(lf_outer_product_mean, lf_opm_args)
 LF_ENTRY(lf_global_column_attention, lf_global_attention_args)
+LF_ENTRY(lf_input_embedder, lf_input_embedder_args)
 }

@@ -47,5 +47,6 @@ size_t mlp_packed_bytes(int C, int H, bool swiglu);
 int transition_fused(lf_context* ctx, const lf_transition_args& a, const WView* views, void* packed);
 int outer_product_mean(lf_context* ctx, const lf_opm_args& a);
 int global_attention(lf_context* ctx, const lf_global_attention_args& a);
+int input_embedder(lf_context* ctx, const lf_input_embedder_args& a);
 
 }  // namespace lf

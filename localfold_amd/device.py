@@ -596,3 +596,52 @@ def msa_module_block(ctx: Context, msa, pair, msa_mask, pair_mask, wstruct, msa_
     a.epsilon = epsilon
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_msa_module_block(ctx.handle, C.byref(a)))
+
+
+_EMBED_WEIGHTS = {"preprocess_1d_w": "preprocess1dWeight", "preprocess_1d_b": "preprocess1dBias",
+                  "preprocess_msa_w": "preprocessMsaWeight", "preprocess_msa_b": "preprocessMsaBias",
+                  "left_w": "leftSingleWeight", "left_b": "leftSingleBias", "right_w": "rightSingleWeight",
+                  "right_b": "rightSingleBias", "prev_pos_w": "previousPositionWeight",
+                  "prev_pos_b": "previousPositionBias", "prev_msa_norm_scale": "previousMsaNormScale",
+                  "prev_msa_norm_offset": "previousMsaNormOffset", "prev_pair_norm_scale": "previousPairNormScale",
+                  "prev_pair_norm_offset": "previousPairNormOffset", "relpos_w": "relativePositionWeight",
+                  "relpos_b": "relativePositionBias", "extra_w": "extraMsaWeight", "extra_b": "extraMsaBias"}
+
+
+def input_embedder_weights(dw: DeviceWeights, w: dict) -> capi.lf_input_embedder_weights:
+    """InputEmbedderGpu's weights (`webgpu/af2/evoformer/input-embedder.js:9-26`), f32 (in,out)."""
+    s = capi.lf_input_embedder_weights()
+    for field, key in _EMBED_WEIGHTS.items():
+        setattr(s, field, dw.vec(np.asarray(w[key], np.float32).reshape(-1)))
+    return s
+
+
+def input_embedder(ctx: Context, f: dict, wstruct: capi.lf_input_embedder_weights, c_m: int = 256, c_z: int = 128,
+                   c_e: int = 64, dtype=torch.float32, prev_msa=None, prev_pair=None, prev_positions=None,
+                   pair_out: torch.Tensor = None, epsilon: float = 1e-5):
+    """One recycle's embeddings from device features `f` (InputEmbedderGpu.run input names, f32
+    tensors): returns (msa [S, L, cM], pair [L, L, cZ], extra [Se, L, cE]) in `dtype`."""
+    L, ct = f["targetFeatures"].shape
+    s_, _, cf = f["msaFeatures"].shape
+    se = f["extraMsa"].shape[0]
+    dev = f["targetFeatures"].device
+    msa = torch.empty(s_, L, c_m, device=dev, dtype=dtype)
+    pair = pair_out if pair_out is not None else torch.empty(L, L, c_z, device=dev, dtype=dtype)
+    extra = torch.empty(se, L, c_e, device=dev, dtype=dtype)
+    a = capi.lf_input_embedder_args()
+    a.length, a.msa_sequences, a.extra_sequences, a.target_channels, a.msa_feature_channels = L, s_, se, ct, cf
+    a.c_m, a.c_z, a.c_e = c_m, c_z, c_e
+    a.target_feat, a.msa_feat = ptr(f["targetFeatures"]), ptr(f["msaFeatures"])
+    a.extra_msa, a.extra_has_deletion = ptr(f["extraMsa"]), ptr(f["extraHasDeletion"])
+    a.extra_deletion_value = ptr(f["extraDeletionValue"])
+    a.residue_index, a.aatype = ptr(f["residueIndex"]), ptr(f["aatype"])
+    a.prev_msa_first_row = ptr(prev_msa) if prev_msa is not None else None
+    a.prev_pair = ptr(prev_pair) if prev_pair is not None else None
+    a.prev_positions = ptr(prev_positions) if prev_positions is not None else None
+    a.msa_dtype, a.msa = act_code(msa), ptr(msa)
+    a.pair_dtype, a.pair = act_code(pair), ptr(pair)
+    a.extra_dtype, a.extra = act_code(extra), ptr(extra)
+    a.epsilon = epsilon
+    a.w = C.pointer(wstruct)
+    check(ctx.lib.lf_input_embedder(ctx.handle, C.byref(a)))
+    return msa, pair, extra

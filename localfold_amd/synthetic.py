@@ -555,3 +555,44 @@ def config4_inputs(n: int = 384, sequences: int = 512, c_m: int = 256, c_z: int 
     pair = s.normal(n * n * c_z).reshape(n, n, c_z)
     return {"weights": quantise_tree(w, "int8", block), "msa": msa, "pair": pair, "tokens": tokens,
             "msa_mask": np.ones((sequences, n), np.float32), "pair_mask": np.ones((n, n), np.float32)}
+
+
+def synthetic_input_embedder(length: int, msa_sequences: int, extra_sequences: int, c_m: int = 256,
+                             c_z: int = 128, c_e: int = 64, target_channels: int = 22,
+                             msa_feature_channels: int = 49, seed: int = 17) -> tuple:
+    """Random-init AF2 input-embedder weights (`InputEmbedderGpu`, webgpu/af2/evoformer/
+    input-embedder.js:9-26, all (in,out) f32) and features of the shapes it reads: one-hot
+    target features, msa features, extra codes 0..22 with deletion features, residue indices
+    with a chain gap, aatype and atom37 positions.  Returns (weights, features)."""
+    st = Stream(seed)
+
+    def lin(i, o):
+        return st.normal(i * o, 1.0 / np.sqrt(i)).reshape(i, o).astype(np.float32)
+
+    w = {"preprocess1dWeight": lin(target_channels, c_m), "preprocess1dBias": st.values(c_m, 0.1),
+         "preprocessMsaWeight": lin(msa_feature_channels, c_m), "preprocessMsaBias": st.values(c_m, 0.1),
+         "leftSingleWeight": lin(target_channels, c_z), "leftSingleBias": st.values(c_z, 0.1),
+         "rightSingleWeight": lin(target_channels, c_z), "rightSingleBias": st.values(c_z, 0.1),
+         "previousPositionWeight": lin(15, c_z), "previousPositionBias": st.values(c_z, 0.1),
+         "previousMsaNormScale": st.values(c_m, 0.2, 1), "previousMsaNormOffset": st.values(c_m, 0.1),
+         "previousPairNormScale": st.values(c_z, 0.2, 1), "previousPairNormOffset": st.values(c_z, 0.1),
+         "relativePositionWeight": lin(65, c_z), "relativePositionBias": st.values(c_z, 0.1),
+         "extraMsaWeight": lin(25, c_e), "extraMsaBias": st.values(c_e, 0.1)}
+    rng = np.random.default_rng(seed)
+    aatype = rng.integers(0, 20, length)
+    target = np.zeros((length, target_channels), np.float32)
+    target[np.arange(length), aatype + 1] = 1
+    msa_feat = (rng.random((msa_sequences, length, msa_feature_channels)) < 0.1).astype(np.float32)
+    msa_feat[..., 48] = rng.random((msa_sequences, length))
+    residue_index = np.arange(length, dtype=np.float32)
+    residue_index[length // 2:] += 200            # a chain break: offsets past +-32 clip
+    positions = np.cumsum(rng.normal(0, 2.2, (length, 37, 3)), axis=0).astype(np.float32)
+    f = {"targetFeatures": target, "msaFeatures": msa_feat,
+         "extraMsa": rng.integers(0, 23, (extra_sequences, length)).astype(np.float32),
+         "extraHasDeletion": (rng.random((extra_sequences, length)) < 0.2).astype(np.float32),
+         "extraDeletionValue": rng.random((extra_sequences, length)).astype(np.float32),
+         "residueIndex": residue_index, "aatype": aatype.astype(np.float32),
+         "previousMsaFirstRow": rng.normal(0, 1, (length, c_m)).astype(np.float32),
+         "previousPair": rng.normal(0, 1, (length, length, c_z)).astype(np.float32),
+         "previousPositions": positions}
+    return w, f

@@ -331,7 +331,9 @@ def msa_pair_weighted_averaging_af3(msa, mask, pair, w, eps=1e-5):
     pn = layer_norm(pair, w["pairNormScale"], w["pairNormOffset"], eps, fast_variance=True)
     flat = np.asarray(linear(pn, w["pairLogits"]), F64)                # [N, N, H]
     key_mask = np.asarray(mask, F64).max(0)                           # [N]
-    logits = flat.transpose(2, 0, 1) + 1e9 * (key_mask[None, None, :] - 1.0)
+    # stored as f32 (weightsByHead is a Float32Array, :188-193): with every key masked the 1e9
+    # term swamps the logits and the row is uniform
+    logits = np.asarray(_f32(flat.transpose(2, 0, 1) + 1e9 * (key_mask[None, None, :] - 1.0)), F64)
     logits = logits - logits.max(-1, keepdims=True)
     p = np.exp(logits)
     p = np.asarray(_f32(p / p.sum(-1, keepdims=True)), F64)          # [H, N, N]
@@ -425,3 +427,65 @@ def error_metrics(actual, expected):
     return {"meanAbsoluteError": float(d.mean()), "maxAbsoluteError": float(d.max()),
             "rootMeanSquareError": float(np.sqrt((d * d).mean())),
             "relativeFrobenius": float(np.sqrt((d * d).sum()) / max(np.sqrt((e * e).sum()), 1e-30))}
+
+
+# ---------------------------------------------------------------------------------------
+# AF2 input and recycling embedder
+# ---------------------------------------------------------------------------------------
+
+EMBED_DGRAM_BINS, EMBED_MIN_BIN, EMBED_MAX_BIN, EMBED_MAX_RELATIVE = 15, 3.25, 20.75, 32
+
+
+def pseudo_beta(positions, aatype):
+    """CB of each residue from atom37 positions [L, 37, 3], CA (atom 1) for glycine (aatype 7)
+    (`PAIR_SHADER` pseudo_beta_coordinate, `webgpu/af2/evoformer/input-embedder.js:105-108`)."""
+    atom = np.where(np.asarray(aatype).astype(np.int64) == 7, 1, 3)
+    return np.asarray(positions, F64).reshape(-1, 37, 3)[np.arange(len(atom)), atom]
+
+
+def dgram_bins(d2):
+    """One-hot [.., 15] of squared distances: bin b covers (lower_b^2, upper_b^2) with
+    lower_b = 3.25 + b w, w = 17.5 / 14, upper the next lower, the last bin unbounded above
+    (`input-embedder.js:121-128`).  Squared distances at or below 3.25^2 fall in no bin."""
+    w = np.float32((EMBED_MAX_BIN - EMBED_MIN_BIN) / (EMBED_DGRAM_BINS - 1))
+    b = np.arange(EMBED_DGRAM_BINS)
+    lower = (np.float32(EMBED_MIN_BIN) + b.astype(np.float32) * w).astype(F64)
+    upper = np.append(lower[1:], np.inf)
+    d2 = np.asarray(d2, F64)[..., None]
+    return ((d2 > lower * lower) & (d2 < upper * upper)).astype(F64)
+
+
+def input_embedder_af2(target_feat, msa_feat, extra_msa, extra_has_deletion, extra_deletion_value,
+                       residue_index, aatype, prev_msa_first_row, prev_pair, prev_positions, w, eps=1e-5):
+    """AF2 input + recycling embedder before the template branch, `InputEmbedderGpu.run` /
+    `encodeInputEmbedder` (`webgpu/af2/evoformer/input-embedder.js:160-231`):
+      msa[s, r]   = target[r] W1d + b1d + msa_feat[s, r] Wmsa + bmsa (+ LN(prev_msa[r]) on s = 0)
+                    (MSA_SHADER, :61-83)
+      pair[i, j]  = target[i] Wl + bl + target[j] Wr + br + bpos + Wpos[dgram bin of the
+                    pseudo-beta distance] + LN(prev_pair[i, j]) + brel + Wrel[clip(ri - rj + 32,
+                    0, 64)]  (PAIR_SHADER, :99-137)
+      extra[s, r] = bext + Wext[code] + has_deletion Wext[23] + deletion_value Wext[24]
+                    (EXTRA_SHADER, :85-97)
+    Layer norms: two-pass, eps 1e-5 (`createAttentionNormParameters`, :197-204).
+    Returns (msa [S, L, cM], pair [L, L, cZ], extra [Se, L, cE])."""
+    tf = np.asarray(target_feat, F64)
+    n = tf.shape[0]
+    single = tf @ w["preprocess1dWeight"] + w["preprocess1dBias"]
+    msa = np.asarray(msa_feat, F64) @ w["preprocessMsaWeight"] + w["preprocessMsaBias"] + single[None]
+    msa[0] += layer_norm(prev_msa_first_row, w["previousMsaNormScale"], w["previousMsaNormOffset"], eps)
+    left = tf @ w["leftSingleWeight"] + w["leftSingleBias"]
+    right = tf @ w["rightSingleWeight"] + w["rightSingleBias"]
+    pair = left[:, None] + right[None, :] + w["previousPositionBias"]
+    cb = pseudo_beta(prev_positions, aatype)
+    d2 = ((cb[:, None] - cb[None, :]) ** 2).sum(-1)
+    pair += dgram_bins(d2) @ w["previousPositionWeight"]
+    pair += layer_norm(prev_pair, w["previousPairNormScale"], w["previousPairNormOffset"], eps)
+    ri = np.asarray(residue_index).astype(np.int64)
+    rel = np.clip(ri[:, None] - ri[None, :] + EMBED_MAX_RELATIVE, 0, 2 * EMBED_MAX_RELATIVE)
+    pair += w["relativePositionBias"] + np.asarray(w["relativePositionWeight"], F64)[rel]
+    we = np.asarray(w["extraMsaWeight"], F64)
+    codes = np.asarray(extra_msa).astype(np.int64)
+    extra = (w["extraMsaBias"] + we[codes] + np.asarray(extra_has_deletion, F64)[..., None] * we[23]
+             + np.asarray(extra_deletion_value, F64)[..., None] * we[24])
+    assert pair.shape[:2] == (n, n)
+    return _f32(msa), _f32(pair), _f32(extra)

@@ -65,6 +65,15 @@ def test_oracle_uncovered_token_equals_deleted_token():
     np.testing.assert_allclose(got[:, keep], ref, rtol=2e-5, atol=2e-5)
 
 
+def test_oracle_every_key_masked_is_uniform():
+    """No token covered: the f32 logits are all -1e9 and each head averages every token."""
+    w, msa, pair, mask = _avg_inputs(2, 5, 32, 16, 4, 8, 5)
+    mask[:] = 0
+    got = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    v, g = _values_gate(msa, w)
+    np.testing.assert_allclose(got, (v.mean(1, keepdims=True) * g) @ w["outputProjection"], rtol=2e-5, atol=2e-5)
+
+
 def test_oracle_sequences_do_not_mix():
     """The weights come from the pair alone: a sequence's update depends on its own row only,
     so permuting sequences permutes updates and changing one row leaves the others."""
@@ -144,6 +153,26 @@ def test_pair_weighted_averaging(ctx, s, n, cm, cz, heads, dim, dt):
     torch.cuda.synchronize()
     ref = ops.msa_pair_weighted_averaging_af3(x.float().cpu().numpy(), mask, p.float().cpu().numpy(), w)
     H.assert_close(out.float().cpu().numpy(), ref, label=f"pwa {s}x{n} {dt}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dim", [8, 6])
+def test_pair_weighted_averaging_every_key_masked(ctx, dim):
+    """Every token masked in every sequence: the reference's f32 softmax is uniform over the
+    tokens (the GEMM path matches it; the flash path clamps and differs only here, so only the
+    GEMM path is held to it)."""
+    import torch
+    from localfold_amd import device as D
+    w, msa, pair, mask = _avg_inputs(3, 20, 32, 16, 4, dim, 17)
+    mask[:] = 0
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.pair_averaging_weights(dw, w)
+    out = D.msa_pair_weighted_averaging(ctx, _dev(ctx, msa), _dev(ctx, mask), _dev(ctx, pair), ws, 4, dim)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    if dim % 4 == 0:
+        ref = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+        H.assert_close(out.cpu().numpy(), ref, label="pwa every key masked")
 
 
 @pytest.mark.gpu
