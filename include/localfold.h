@@ -369,6 +369,24 @@ typedef struct {
  * 160-231): the MSA, pair (without templates) and extra-MSA embeddings of one recycle. */
 int lf_input_embedder(lf_context* ctx, const lf_input_embedder_args* args);
 
+/* One AF2 recycle of the trunk before the structure module: the input embedder, the
+ * extra-MSA stack on the extra activations and the pair, the Evoformer stack on the msa and
+ * the pair.  The carried state is the embedder's recycled inputs: point
+ * embed.prev_msa_first_row at main.msa and embed.prev_pair at main.pair (they are read before
+ * being overwritten) and the outputs of one call are the recycled inputs of the next.
+ * extra.msa = embed.extra, extra.pair = main.pair = embed.pair; extra.w and main.w are not
+ * read.  Templates and the structure module are out of scope: prev_positions is the
+ * caller's (atom37 from its structure module, or NULL for zeros). */
+typedef struct {
+  lf_input_embedder_args embed;
+  lf_evoformer_block_args extra;  const lf_extra_msa_weights* extra_blocks;  int extra_block_count;
+  lf_evoformer_block_args main;   const lf_evoformer_weights* main_blocks;   int main_block_count;
+} lf_af2_recycle_args;
+
+/* Replaces one iteration of the recycle loop of AlphaFoldMonomerGpu (webgpu/af2/model/
+ * monomer.js:182-330) up to the Evoformer stack's output. */
+int lf_af2_recycle(lf_context* ctx, const lf_af2_recycle_args* args);
+
 /* ---- AF3 MSA module ------------------------------------------------------------------- */
 
 /* Pair-weighted averaging weights (`msaAttention1`, cpu/af3/trunk/msa.js:157-219), no biases. */

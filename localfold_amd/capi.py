@@ -155,6 +155,14 @@ class lf_input_embedder_args(C.Structure):
                    ("w", C.POINTER(lf_input_embedder_weights))])
 
 
+class lf_af2_recycle_args(C.Structure):
+    _fields_ = [("embed", lf_input_embedder_args),
+                ("extra", lf_evoformer_block_args), ("extra_blocks", C.POINTER(lf_extra_msa_weights)),
+                ("extra_block_count", C.c_int),
+                ("main", lf_evoformer_block_args), ("main_blocks", C.POINTER(lf_evoformer_weights)),
+                ("main_block_count", C.c_int)]
+
+
 class lf_pair_averaging_weights(C.Structure):
     _fields_ = [("act_norm_scale", P), ("act_norm_offset", P), ("pair_norm_scale", P), ("pair_norm_offset", P),
                 ("pair_logits", lf_weight), ("wv", lf_weight), ("wg", lf_weight), ("wo", lf_weight)]
@@ -208,6 +216,7 @@ PROTOTYPES = [
     ("lf_evoformer_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
     ("lf_pairformer_block", C.c_int, [P, C.POINTER(lf_pairformer_block_args)]),
     ("lf_input_embedder", C.c_int, [P, C.POINTER(lf_input_embedder_args)]),
+    ("lf_af2_recycle", C.c_int, [P, C.POINTER(lf_af2_recycle_args)]),
     ("lf_msa_pair_weighted_averaging", C.c_int, [P, C.POINTER(lf_pair_averaging_args)]),
     ("lf_msa_module_block", C.c_int, [P, C.POINTER(lf_msa_block_args)]),
 ]

@@ -414,6 +414,27 @@ int lf_msa_pair_weighted_averaging(lf_context* ctx, const lf_pair_averaging_args
   return lf::pair_weighted_averaging(ctx, *args);
 }
 
+int lf_af2_recycle(lf_context* ctx, const lf_af2_recycle_args* args) {
+  if (!ctx || !args) return lf::set_error(LF_ERR_INVALID, "lf_af2_recycle: NULL argument");
+  if (args->extra_block_count < 0 || args->main_block_count < 0 || (args->extra_block_count > 0 && !args->extra_blocks) ||
+      (args->main_block_count > 0 && !args->main_blocks))
+    return lf::set_error(LF_ERR_INVALID, "lf_af2_recycle: bad block list");
+  const lf_af2_recycle_args& a = *args;
+  if ((a.main_block_count > 0 && (a.main.pair != a.embed.pair || a.main.msa != a.embed.msa)) ||
+      (a.extra_block_count > 0 && (a.extra.pair != a.embed.pair || a.extra.msa != a.embed.extra)))
+    return lf::set_error(LF_ERR_INVALID, "lf_af2_recycle: the stacks must run on the embedder's outputs");
+  hipSetDevice(ctx->device);
+  {
+    lf::StageScope stage(ctx, "input_embedder");
+    LF_TRY(lf::input_embedder(ctx, a.embed));
+  }
+  for (int b = 0; b < a.extra_block_count; ++b)
+    LF_TRY(lf::evoformer_block(ctx, a.extra, a.extra_blocks[b].base, &a.extra_blocks[b].column_global,
+                               a.extra_blocks[b].column_global_heads));
+  for (int b = 0; b < a.main_block_count; ++b) LF_TRY(lf::evoformer_block(ctx, a.main, a.main_blocks[b]));
+  return LF_OK;
+}
+
 int lf_msa_module_block(lf_context* ctx, const lf_msa_block_args* args) {
   if (!ctx || !args) return lf::set_error(LF_ERR_INVALID, "lf_msa_module_block: NULL argument");
   hipSetDevice(ctx->device);

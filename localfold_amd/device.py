@@ -645,3 +645,49 @@ def input_embedder(ctx: Context, f: dict, wstruct: capi.lf_input_embedder_weight
     a.w = C.pointer(wstruct)
     check(ctx.lib.lf_input_embedder(ctx.handle, C.byref(a)))
     return msa, pair, extra
+
+
+def af2_recycle_state(f: dict, c_m: int = 256, c_z: int = 128, c_e: int = 64, dtype=torch.bfloat16) -> dict:
+    """Device buffers carried across recycles: msa [S, L, cM], pair [L, L, cZ], extra [Se, L, cE]."""
+    L = f["targetFeatures"].shape[0]
+    dev = f["targetFeatures"].device
+    return {"msa": torch.zeros(f["msaFeatures"].shape[0], L, c_m, device=dev, dtype=dtype),
+            "pair": torch.zeros(L, L, c_z, device=dev, dtype=dtype),
+            "extra": torch.zeros(f["extraMsa"].shape[0], L, c_e, device=dev, dtype=dtype)}
+
+
+def af2_recycle(ctx: Context, f: dict, state: dict, masks: dict, embed_ws, extra_wss, extra_w0: dict, main_wss,
+                main_w0: dict, first: bool, prev_positions: torch.Tensor = None, epsilon: float = 1e-5):
+    """One recycle (lf_af2_recycle): embed from the carried state (zeros when `first`), the
+    extra-MSA stack, the Evoformer stack; `state` holds the result, which is the next recycle's
+    carried state.  masks: msa [S, L], extra [Se, L], pair [L, L] (f32)."""
+    msa, pair, extra = state["msa"], state["pair"], state["extra"]
+    L, ct = f["targetFeatures"].shape
+    a = capi.lf_af2_recycle_args()
+    e = a.embed
+    e.length, e.msa_sequences, e.extra_sequences = L, msa.shape[0], extra.shape[0]
+    e.target_channels, e.msa_feature_channels = ct, f["msaFeatures"].shape[2]
+    e.c_m, e.c_z, e.c_e = msa.shape[2], pair.shape[2], extra.shape[2]
+    e.target_feat, e.msa_feat = ptr(f["targetFeatures"]), ptr(f["msaFeatures"])
+    e.extra_msa, e.extra_has_deletion = ptr(f["extraMsa"]), ptr(f["extraHasDeletion"])
+    e.extra_deletion_value = ptr(f["extraDeletionValue"])
+    e.residue_index, e.aatype = ptr(f["residueIndex"]), ptr(f["aatype"])
+    e.prev_msa_first_row = None if first else ptr(msa)
+    e.prev_pair = None if first else ptr(pair)
+    e.prev_positions = ptr(prev_positions)
+    e.msa_dtype, e.msa, e.pair_dtype, e.pair = act_code(msa), ptr(msa), act_code(pair), ptr(pair)
+    e.extra_dtype, e.extra = act_code(extra), ptr(extra)
+    e.epsilon = epsilon
+    e.w = C.pointer(embed_ws)
+    if extra_wss:
+        a.extra = evoformer_block_args(extra, pair, masks["extra"], masks["pair"], extra_w0, epsilon)
+        arr_e = (capi.lf_extra_msa_weights * len(extra_wss))(*extra_wss)
+        a.extra_blocks, a.extra_block_count = arr_e, len(extra_wss)
+    if main_wss:
+        a.main = evoformer_block_args(msa, pair, masks["msa"], masks["pair"], main_w0, epsilon)
+        arr_m = (capi.lf_evoformer_weights * len(main_wss))(*main_wss)
+        a.main_blocks, a.main_block_count = arr_m, len(main_wss)
+    else:
+        a.main.msa, a.main.pair = ptr(msa), ptr(pair)
+    check(ctx.lib.lf_af2_recycle(ctx.handle, C.byref(a)))
+    return state

@@ -145,3 +145,41 @@ def test_input_embedder_recycle_zero_and_in_place(ctx):
     torch.cuda.synchronize()
     _, rp2, _ = _oracle(f, w)
     H.assert_close(pair2.cpu().numpy(), rp2, label="embed pair in place")
+
+
+@pytest.mark.gpu
+def test_af2_recycle_two_recycles(ctx):
+    """Two recycles of embed -> extra-MSA block -> Evoformer block through lf_af2_recycle, the
+    second embedding the first's msa row 0 and pair (monomer.js:182-330 up to the stack's
+    output), against the oracle's composition of the same steps."""
+    import torch
+    from localfold_amd import device as D
+    from oracle import blocks
+    L, s_, se, cm, cz, ce = 14, 3, 6, 64, 32, 64
+    w, f = S.synthetic_input_embedder(L, s_, se, c_m=cm, c_z=cz, c_e=ce, seed=8)
+    wx = S.synthetic_extra_msa_block_weights(c_m=ce, c_z=cz, c_outer=8, heads_msa=8, heads_pair=2, tri_hidden=32,
+                                             msa_hidden=4 * ce, pair_hidden=4 * cz, seed=21)
+    wm = S.synthetic_block_weights(c_m=cm, c_z=cz, c_outer=8, heads_msa=4, heads_pair=2, tri_hidden=32,
+                                   msa_hidden=4 * cm, pair_hidden=4 * cz, seed=22)
+    rng = np.random.default_rng(3)
+    masks = {"msa": (rng.random((s_, L)) > 0.1).astype(np.float32),
+             "extra": (rng.random((se, L)) > 0.2).astype(np.float32), "pair": np.ones((L, L), np.float32)}
+    dw = D.DeviceWeights(ctx.device)
+    ews = D.input_embedder_weights(dw, w)
+    xws, mws = [D.extra_msa_weights(dw, wx)], [D.evoformer_weights(dw, wm)]
+    fd = _dev(ctx, f)
+    md = {k: torch.as_tensor(v).to(ctx.device) for k, v in masks.items()}
+    state = D.af2_recycle_state(fd, cm, cz, ce, torch.float32)
+    pos = [None, fd["previousPositions"]]
+    rm = rp = None
+    for r in range(2):
+        D.af2_recycle(ctx, fd, state, md, ews, xws, wx, mws, wm, first=(r == 0), prev_positions=pos[r])
+        prev = dict(f, previousMsaFirstRow=np.zeros((L, cm), np.float32) if r == 0 else rm[0],
+                    previousPair=np.zeros((L, L, cz), np.float32) if r == 0 else rp,
+                    previousPositions=np.zeros_like(f["previousPositions"]) if r == 0 else f["previousPositions"])
+        rm, rp, re = _oracle(prev, w)
+        re, rp = blocks.extra_msa_block_af2(re, rp, masks["extra"], masks["pair"], wx)
+        rm, rp = blocks.evoformer_block_af2(rm, rp, masks["msa"], masks["pair"], wm)
+    torch.cuda.synchronize()
+    H.assert_close(state["msa"].cpu().numpy(), rm, label="recycle msa")
+    H.assert_close(state["pair"].cpu().numpy(), rp, label="recycle pair")
