@@ -701,6 +701,105 @@ napi_value PairformerBlock(napi_env env, napi_callback_info info) {
   return undefined_value(env);
 }
 
+// msaModuleBlock(ctx, args): one AF3 MSA-module block, weights {opm, cOuter, pwa, msaHeads,
+// msaHeadDim, msaTransition, pair: {triOut, triIn, attStart, attEnd, pairHeads, pairTransition}}
+napi_value MsaModuleBlock(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return nullptr;
+  napi_value o = argv[1];
+  napi_value wv = prop(env, o, "weights");
+  lf_msa_module_weights w{};
+  w.outer_product_mean = opm_w(env, prop(env, wv, "opm"));
+  w.c_outer = get_int(env, wv, "cOuter");
+  napi_value pv = prop(env, wv, "pwa");
+  w.msa_attention.act_norm_scale = get_vec(env, pv, "actNormScale");
+  w.msa_attention.act_norm_offset = get_vec(env, pv, "actNormOffset");
+  w.msa_attention.pair_norm_scale = get_vec(env, pv, "pairNormScale");
+  w.msa_attention.pair_norm_offset = get_vec(env, pv, "pairNormOffset");
+  w.msa_attention.pair_logits = get_weight(env, pv, "pairLogits");
+  w.msa_attention.wv = get_weight(env, pv, "wv");
+  w.msa_attention.wg = get_weight(env, pv, "wg");
+  w.msa_attention.wo = get_weight(env, pv, "wo");
+  w.msa_heads = get_int(env, wv, "msaHeads");
+  w.msa_head_dim = get_int(env, wv, "msaHeadDim");
+  w.msa_transition = tr_weights(env, prop(env, wv, "msaTransition"));
+  napi_value q = prop(env, wv, "pair");
+  w.pair.tri_out = tri_weights(env, prop(env, q, "triOut"));
+  w.pair.tri_in = tri_weights(env, prop(env, q, "triIn"));
+  w.pair.att_start = att_weights(env, prop(env, q, "attStart"));
+  w.pair.att_end = att_weights(env, prop(env, q, "attEnd"));
+  w.pair.pair_heads = get_int(env, q, "pairHeads");
+  w.pair.pair_transition = tr_weights(env, prop(env, q, "pairTransition"));
+  lf_msa_block_args a{};
+  a.sequences = get_int(env, o, "sequences");
+  a.tokens = get_int(env, o, "tokens");
+  a.c_m = get_int(env, o, "cM");
+  a.c_z = get_int(env, o, "cZ");
+  a.msa_update_before_opm = get_int(env, o, "msaUpdateBeforeOuterProduct");
+  a.swap_transposed_bias = get_int(env, o, "swapTransposedBias");
+  a.divide_by_length = get_int(env, o, "divideByLength");
+  a.msa_dtype = get_int(env, o, "msaDtype");
+  a.msa = get_dev(env, o, "msa");
+  a.pair_dtype = get_int(env, o, "pairDtype");
+  a.pair = get_dev(env, o, "pair");
+  a.msa_mask = static_cast<const float*>(get_dev(env, o, "msaMask"));
+  a.pair_mask = static_cast<const float*>(get_dev(env, o, "pairMask"));
+  a.transition_chunk_bytes = (long long)get_num(env, o, "transitionChunkBytes", 0);
+  a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
+  a.w = &w;
+  int rc = lf_msa_module_block(as_ctx(env, argv[0]), &a);
+  if (rc != LF_OK) return throw_lf(env, rc, "lf_msa_module_block");
+  return undefined_value(env);
+}
+
+// inputEmbedder(ctx, args): device pointers for every feature, weight and output
+napi_value InputEmbedder(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return nullptr;
+  napi_value o = argv[1];
+  napi_value wv = prop(env, o, "weights");
+  lf_input_embedder_weights w{};
+  const struct { const float** dst; const char* name; } ws[] = {
+      {&w.preprocess_1d_w, "preprocess1dWeight"}, {&w.preprocess_1d_b, "preprocess1dBias"},
+      {&w.preprocess_msa_w, "preprocessMsaWeight"}, {&w.preprocess_msa_b, "preprocessMsaBias"},
+      {&w.left_w, "leftSingleWeight"}, {&w.left_b, "leftSingleBias"}, {&w.right_w, "rightSingleWeight"},
+      {&w.right_b, "rightSingleBias"}, {&w.prev_pos_w, "previousPositionWeight"},
+      {&w.prev_pos_b, "previousPositionBias"}, {&w.prev_msa_norm_scale, "previousMsaNormScale"},
+      {&w.prev_msa_norm_offset, "previousMsaNormOffset"}, {&w.prev_pair_norm_scale, "previousPairNormScale"},
+      {&w.prev_pair_norm_offset, "previousPairNormOffset"}, {&w.relpos_w, "relativePositionWeight"},
+      {&w.relpos_b, "relativePositionBias"}, {&w.extra_w, "extraMsaWeight"}, {&w.extra_b, "extraMsaBias"},
+  };
+  for (const auto& e : ws) *e.dst = get_vec(env, wv, e.name);
+  lf_input_embedder_args a{};
+  a.length = get_int(env, o, "length");
+  a.msa_sequences = get_int(env, o, "msaSequences");
+  a.extra_sequences = get_int(env, o, "extraSequences");
+  a.target_channels = get_int(env, o, "targetChannels");
+  a.msa_feature_channels = get_int(env, o, "msaFeatureChannels");
+  a.c_m = get_int(env, o, "msaChannels");
+  a.c_z = get_int(env, o, "pairChannels");
+  a.c_e = get_int(env, o, "extraMsaChannels");
+  a.target_feat = static_cast<const float*>(get_dev(env, o, "targetFeatures"));
+  a.msa_feat = static_cast<const float*>(get_dev(env, o, "msaFeatures"));
+  a.extra_msa = static_cast<const float*>(get_dev(env, o, "extraMsa"));
+  a.extra_has_deletion = static_cast<const float*>(get_dev(env, o, "extraHasDeletion"));
+  a.extra_deletion_value = static_cast<const float*>(get_dev(env, o, "extraDeletionValue"));
+  a.residue_index = static_cast<const float*>(get_dev(env, o, "residueIndex"));
+  a.aatype = static_cast<const float*>(get_dev(env, o, "aatype"));
+  a.prev_msa_first_row = get_dev(env, o, "previousMsaFirstRow");
+  a.prev_pair = get_dev(env, o, "previousPair");
+  a.prev_positions = static_cast<const float*>(get_dev(env, o, "previousPositions"));
+  a.msa_dtype = a.pair_dtype = a.extra_dtype = LF_F32;
+  a.msa = get_dev(env, o, "msa");
+  a.pair = get_dev(env, o, "pair");
+  a.extra = get_dev(env, o, "extra");
+  a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
+  a.w = &w;
+  int rc = lf_input_embedder(as_ctx(env, argv[0]), &a);
+  if (rc != LF_OK) return throw_lf(env, rc, "lf_input_embedder");
+  return undefined_value(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   const struct {
     const char* name;
@@ -712,7 +811,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"version", Version}, {"triMult", TriMult}, {"attention", Attention}, {"transition", Transition},
       {"outerProductMean", OuterProductMean}, {"evoformerStack", EvoformerStack},
       {"pairformerBlock", PairformerBlock}, {"globalColumnAttention", GlobalColumnAttention},
-      {"extraMsaStack", ExtraMsaStack},
+      {"extraMsaStack", ExtraMsaStack}, {"msaModuleBlock", MsaModuleBlock}, {"inputEmbedder", InputEmbedder},
   };
   for (const auto& f : fns) {
     napi_value v;

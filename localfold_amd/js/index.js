@@ -699,6 +699,143 @@ Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, optio
   });
 };
 
+// ---- AF3 MSA module ---------------------------------------------------------------------
+
+// cpu/af3/trunk/msa.js:233-287 block weights: outerProductMean (AF3 names), msaAttention1
+// (pair-weighted averaging), msaTransition (SwiGLU) and the pairformer block's pair weights.
+function msaModuleBlockWeights(up, w, cM, cZ) {
+  const pf = pairformerBlockWeights(up, w, cZ, 0);
+  const o = w.outerProductMean;
+  const cOuter = o.outerChannels || o.leftProjection.length / cM;
+  const a = w.msaAttention1;
+  const hd = a.heads * a.dimension;
+  return {
+    opm: {
+      normScale: up.vec(o.layerNormInputScale), normOffset: up.vec(o.layerNormInputOffset),
+      wl: up.weight(o.leftProjection, 'in_out', cM, cOuter), wr: up.weight(o.rightProjection, 'in_out', cM, cOuter),
+      wo: up.weight(o.outputW, 'in_out', cOuter * cOuter, cZ), bo: up.vec(o.outputB),
+    },
+    cOuter: cOuter,
+    pwa: {
+      actNormScale: up.vec(a.actNormScale), actNormOffset: up.vec(a.actNormOffset),
+      pairNormScale: up.vec(a.pairNormScale), pairNormOffset: up.vec(a.pairNormOffset),
+      pairLogits: up.weight(a.pairLogits, 'in_out', cZ, a.heads), wv: up.weight(a.vProjection, 'in_out', cM, hd),
+      wg: up.weight(a.gatingQuery, 'in_out', cM, hd), wo: up.weight(a.outputProjection, 'in_out', hd, cM),
+    },
+    msaHeads: a.heads, msaHeadDim: a.dimension,
+    msaTransition: {
+      normScale: up.vec(w.msaTransition.inputLayerNormScale), normOffset: up.vec(w.msaTransition.inputLayerNormOffset),
+      w1: up.weight(w.msaTransition.transition1, 'in_out', cM, 8 * cM),
+      w2: up.weight(w.msaTransition.transition2, 'in_out', 4 * cM, cM),
+    },
+    pair: pf,
+  };
+}
+
+// webgpu/af3/trunk/msa-stack.js:67-140: run(state, blocks, dialect, options) with state
+// {pair, msa, pairMask, msaMask, tokens, sequences}; dialect.msaUpdateBeforeOuterProduct and
+// dialect.swapTransposedBias have no default.
+function Af3MsaStackGpu(device, options) {
+  this.device = device;
+  this.options = options || {};
+}
+Af3MsaStackGpu.prototype.run = function run(state, blocks, dialect, options) {
+  const dev = this.device;
+  const opts = options || {};
+  return new Promise(function execute(resolve) {
+    if (!dialect || dialect.msaUpdateBeforeOuterProduct === undefined) {
+      throw new Error('dialect.msaUpdateBeforeOuterProduct has no default: AF3 takes the outer product off the '
+        + 'pre-update MSA and OpenDDE off the updated one');
+    }
+    if (dialect.swapTransposedBias === undefined) throw new Error('dialect.swapTransposedBias has no default');
+    positiveInteger('tokens', state.tokens);
+    positiveInteger('sequences', state.sequences);
+    const n = state.tokens;
+    const rows = state.sequences * n;
+    const cM = blocks[0].msaChannels || opts.msaChannels || 64;
+    const cZ = blocks[0].pairChannels || state.pair.length / (n * n);
+    expectLength('msa', state.msa, rows * cM);
+    expectLength('pair', state.pair, n * n * cZ);
+    expectLength('msaMask', state.msaMask, rows);
+    expectLength('pairMask', state.pairMask, n * n);
+    if (opts.variance !== undefined && opts.variance !== 'fast') {
+      throw new RangeError('the MSA stack runs the reference\'s fast variance; received ' + opts.variance);
+    }
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const msa = up.vec(state.msa);
+    const pair = up.vec(state.pair);
+    const msaMask = up.vec(state.msaMask);
+    const pairMask = up.vec(state.pairMask);
+    for (let b = 0; b < blocks.length; b += 1) {
+      if (opts.onBlock) opts.onBlock(b);
+      const w = resident(dev, blocks[b], function build(wu) { return msaModuleBlockWeights(wu, blocks[b], cM, cZ); });
+      dev.addon.msaModuleBlock(dev.ctx, {
+        sequences: state.sequences, tokens: n, cM: cM, cZ: cZ,
+        msaUpdateBeforeOuterProduct: dialect.msaUpdateBeforeOuterProduct ? 1 : 0,
+        swapTransposedBias: dialect.swapTransposedBias ? 1 : 0, divideByLength: dialect.divideByLength ? 1 : 0,
+        msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair, msaMask: msaMask, pairMask: pairMask,
+        transitionChunkBytes: opts.transitionChunkBytes || 0, epsilon: opts.epsilon || 1e-5, weights: w,
+      });
+    }
+    const r = finish(dev, up, [{ buffer: msa, elements: rows * cM }, { buffer: pair, elements: n * n * cZ }], start);
+    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels });
+  });
+};
+
+// ---- AF2 input embedder ------------------------------------------------------------------
+
+const EMBED_WEIGHT_NAMES = [
+  'preprocess1dWeight', 'preprocess1dBias', 'preprocessMsaWeight', 'preprocessMsaBias', 'leftSingleWeight',
+  'leftSingleBias', 'rightSingleWeight', 'rightSingleBias', 'previousPositionWeight', 'previousPositionBias',
+  'previousMsaNormScale', 'previousMsaNormOffset', 'previousPairNormScale', 'previousPairNormOffset',
+  'relativePositionWeight', 'relativePositionBias', 'extraMsaWeight', 'extraMsaBias',
+];
+
+// webgpu/af2/evoformer/input-embedder.js:233-356: run(input) with the reference's input
+// fields; returns {msa, pairWithoutTemplates, extraMsa, elapsedMilliseconds, memory}.
+function InputEmbedderGpu(device) { this.device = device; }
+InputEmbedderGpu.prototype.run = function run(input) {
+  const dev = this.device;
+  return new Promise(function execute(resolve) {
+    const L = input.length;
+    positiveInteger('length', L);
+    const msaElements = input.msaSequences * L * input.msaChannels;
+    const pairElements = L * L * input.pairChannels;
+    const extraElements = input.extraSequences * L * input.extraMsaChannels;
+    expectLength('previousMsaFirstRow', input.previousMsaFirstRow, L * input.msaChannels);
+    expectLength('previousPair', input.previousPair, pairElements);
+    expectLength('previousPositions', input.previousPositions, L * 37 * 3);
+    const weights = resident(dev, input.weights, function build(wu) {
+      const o = {};
+      EMBED_WEIGHT_NAMES.forEach(function each(name) { o[name] = wu.vec(input.weights[name]); });
+      return o;
+    });
+    const up = new Uploads(dev);
+    const start = performance.now();
+    const msa = up.alloc(msaElements * 4);
+    const pair = up.alloc(pairElements * 4);
+    const extra = up.alloc(Math.max(extraElements, 1) * 4);
+    dev.addon.inputEmbedder(dev.ctx, {
+      length: L, msaSequences: input.msaSequences, extraSequences: input.extraSequences,
+      targetChannels: input.targetChannels, msaFeatureChannels: input.msaFeatureChannels,
+      msaChannels: input.msaChannels, pairChannels: input.pairChannels, extraMsaChannels: input.extraMsaChannels,
+      targetFeatures: up.vec(input.targetFeatures), msaFeatures: up.vec(input.msaFeatures),
+      extraMsa: up.vec(input.extraMsa), extraHasDeletion: up.vec(input.extraHasDeletion),
+      extraDeletionValue: up.vec(input.extraDeletionValue), residueIndex: up.vec(input.residueIndex),
+      aatype: up.vec(input.aatype), previousMsaFirstRow: up.vec(input.previousMsaFirstRow),
+      previousPair: up.vec(input.previousPair), previousPositions: up.vec(input.previousPositions),
+      msa: msa, pair: pair, extra: extra, weights: weights,
+    });
+    const outs = [{ buffer: msa, elements: msaElements }, { buffer: extra, elements: extraElements }];
+    if (input.keepPair !== true) outs.push({ buffer: pair, elements: pairElements });
+    const r = finish(dev, up, outs, start);
+    resolve({ msa: r.results[0], extraMsa: r.results[1], pairWithoutTemplates: input.keepPair === true ? undefined : r.results[2],
+      elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
+  });
+};
+
 // shared/bundles/node.js:11-40: a triangle fixture directory (manifest.json + *.f32.bin)
 const TRIANGLE_WEIGHT_NAMES = [
   'layerNormInWeight', 'layerNormInBias', 'linearAPWeight', 'linearAPBias', 'linearAGWeight', 'linearAGBias',
@@ -743,6 +880,8 @@ module.exports = {
   EvoformerStackGpu: EvoformerStackGpu,
   ExtraMsaStackGpu: ExtraMsaStackGpu,
   Af3PairformerStackGpu: Af3PairformerStackGpu,
+  Af3MsaStackGpu: Af3MsaStackGpu,
+  InputEmbedderGpu: InputEmbedderGpu,
   validateTriangleInput: validateTriangleInput,
   validateAttentionInput: validateAttentionInput,
   validateTransitionInput: validateTransitionInput,

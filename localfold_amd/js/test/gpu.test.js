@@ -95,6 +95,20 @@ async function main() {
   const pfOut = await new lf.Af3PairformerStackGpu(device).run(pf.state, pf.blocks, { swapTransposedBias: false });
   report('pairformer pair', lf.errorMetrics(pfOut.pair, pf.expectedPair), { mean: 2e-3, max: 2e-2 });
   report('pairformer single', lf.errorMetrics(pfOut.single, pf.expectedSingle), { mean: 2e-3, max: 2e-2 });
+
+  const ms = revive(JSON.parse(fs.readFileSync(path.join(dir, 'msastack.json'), 'utf8')));
+  await assert.rejects(new lf.Af3MsaStackGpu(device).run(ms.state, ms.blocks, { swapTransposedBias: false }),
+    /msaUpdateBeforeOuterProduct has no default/);
+  const msOut = await new lf.Af3MsaStackGpu(device).run(ms.state, ms.blocks,
+    { swapTransposedBias: false, msaUpdateBeforeOuterProduct: false });
+  report('AF3 MSA stack msa', lf.errorMetrics(msOut.msa, ms.expectedMsa), { mean: 2e-3, max: 2e-2 });
+  report('AF3 MSA stack pair', lf.errorMetrics(msOut.pair, ms.expectedPair), { mean: 2e-3, max: 2e-2 });
+
+  const em = revive(JSON.parse(fs.readFileSync(path.join(dir, 'embed.json'), 'utf8')));
+  const emOut = await new lf.InputEmbedderGpu(device).run(em.input);
+  report('input embedder msa', lf.errorMetrics(emOut.msa, em.expectedMsa), { mean: 1e-4, max: 1e-3 });
+  report('input embedder pair', lf.errorMetrics(emOut.pairWithoutTemplates, em.expectedPair), { mean: 1e-4, max: 1e-3 });
+  report('input embedder extra', lf.errorMetrics(emOut.extraMsa, em.expectedExtra), { mean: 1e-4, max: 5e-4 });
   device.destroy();
   process.exitCode = failures === 0 ? 0 : 1;
 }

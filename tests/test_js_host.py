@@ -148,6 +148,30 @@ def test_js_gpu_suite(tmp_path):
           "blocks": pws, "expectedPair": rp, "expectedSingle": rs}
     (tmp_path / "pairformer.json").write_text(json.dumps(_dump_tree(pf, tmp_path, "pf")))
 
+    # Af3MsaStackGpu: two MSA-module blocks, AF3 order (webgpu/af3/trunk/msa-stack.js:67-140)
+    mws = [S.synthetic_msa_module_weights(c_m=64, c_z=32, heads=8, dim=8, heads_pair=2, c_outer=8, seed=s_)
+           for s_ in (41, 42)]
+    ma = S.synthetic_activations(6, 16, 64, 32, seed=43)
+    mm, mp = ma["msa"], ma["pair"]
+    for mw in mws:
+        mm, mp = blocks.msa_block_af3(mm, mp, ma["msaMask"], ma["pairMask"], mw, False)
+    ms = {"state": {"msa": ma["msa"], "pair": ma["pair"], "msaMask": ma["msaMask"], "pairMask": ma["pairMask"],
+                    "tokens": 16, "sequences": 6},
+          "blocks": [dict(w, msaChannels=64, pairChannels=32) for w in mws], "expectedMsa": mm, "expectedPair": mp}
+    (tmp_path / "msastack.json").write_text(json.dumps(_dump_tree(ms, tmp_path, "ms")))
+
+    # InputEmbedderGpu (the reference test's input fields, test/input-embedder.gpu.test.js:56-77)
+    iw, fe = S.synthetic_input_embedder(19, 3, 7, seed=44)
+    rm_, rp_, re_ = ops.input_embedder_af2(fe["targetFeatures"], fe["msaFeatures"], fe["extraMsa"],
+                                           fe["extraHasDeletion"], fe["extraDeletionValue"], fe["residueIndex"],
+                                           fe["aatype"], fe["previousMsaFirstRow"], fe["previousPair"],
+                                           fe["previousPositions"], iw)
+    em = {"input": dict({k: np.asarray(v, np.float32).reshape(-1) for k, v in fe.items()}, length=19,
+                        msaSequences=3, extraSequences=7, targetChannels=22, msaFeatureChannels=49, msaChannels=256,
+                        pairChannels=128, extraMsaChannels=64, weights=iw),
+          "expectedMsa": rm_, "expectedPair": rp_, "expectedExtra": re_}
+    (tmp_path / "embed.json").write_text(json.dumps(_dump_tree(em, tmp_path, "em")))
+
     (tmp_path / "cases.json").write_text(json.dumps(cases))
     r = _run_node("gpu.test.js", tmp_path)
     assert r.returncode == 0 and "FAIL" not in r.stdout
