@@ -238,6 +238,32 @@ def msa_module_block_n384(ctx, D, synthetic, reps):
             "ms_per_block": round(ms, 3), "outputs_finite": finite, "kernels_ms": kern}
 
 
+def input_embedder_n384(ctx, D, synthetic, reps):
+    """The AF2 input + recycling embedder at N_res=384, 512 MSA rows, 1024 extra rows, with
+    recycled msa row, pair and positions, bf16 outputs."""
+    import torch
+    n, s_, se = 384, 512, 1024
+    w, f = synthetic.synthetic_input_embedder(n, s_, se, seed=3)
+    dev = ctx.device
+    dw = D.DeviceWeights(dev)
+    ws = D.input_embedder_weights(dw, w)
+    fd = {k: torch.as_tensor(v).to(dev) for k, v in f.items()}
+    prev_msa = fd["previousMsaFirstRow"].to(torch.bfloat16)
+    prev_pair = fd["previousPair"].to(torch.bfloat16)
+    pair = torch.empty_like(prev_pair)
+
+    def step():
+        D.input_embedder(ctx, fd, ws, 256, 128, 64, torch.bfloat16, prev_msa, prev_pair, fd["previousPositions"],
+                         pair_out=pair)
+
+    step()
+    ms = timed(step, reps)
+    kern = profile_ops(ctx, step, 2)
+    return {"workload": f"AF2 input + recycling embedder: N_res={n}, N_seq={s_}, N_extra={se}, c_m=256, c_z=128, "
+                        "c_e=64, recycled inputs present, bf16 outputs; synthetic",
+            "ms": round(ms, 3), "kernels_ms": kern}
+
+
 def evoformer_stack_config4(ctx, D, synthetic, reps):
     """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
     pass (1 recycle), 48 distinct int8 weight sets, bf16 activations, through lf_evoformer_stack."""
@@ -410,6 +436,8 @@ def main():
         extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
         log("extra-MSA block ...")
         extras["extra_msa_block"] = extra_msa_block_n384(ctx, D, synthetic, 5)
+        log("input embedder ...")
+        extras["input_embedder"] = input_embedder_n384(ctx, D, synthetic, 10)
         log("AF3 MSA-module block ...")
         extras["msa_module_block"] = msa_module_block_n384(ctx, D, synthetic, 5)
         log("config 5: one Pairformer block ...")
@@ -450,6 +478,7 @@ def main():
         "pairformer_block": extras.get("pairformer_block"),
         "extra_msa_block": extras.get("extra_msa_block"),
         "msa_module_block": extras.get("msa_module_block"),
+        "input_embedder": extras.get("input_embedder"),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -15,6 +15,7 @@
 // the embedding once.  Layer norms are two-pass with eps 1e-5 (:197-204).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "lf_common.h"
@@ -88,31 +89,66 @@ __device__ __forceinline__ void wave_row_load(float (&v)[EMB_MAXV], const void* 
   }
 }
 
-// one wave per msa row (s, r)
+// One wave per EMB_ROWS msa rows: a lane holds one feature of each row (feature j = lane, up to
+// 64 per pass), broadcast through readlane, and the channels lane + 64 k of every row, so each
+// weight value Wmsa[j][c] (L1/L2-resident) is loaded once for EMB_ROWS rows.  The f32 FMAs
+// bound it (S L cM Cf of them); staging Wmsa in LDS measured slower (fewer waves per CU).
+constexpr int EMB_ROWS = 8;
 __global__ __launch_bounds__(256) void embed_msa_kernel(const float* msa_feat, int S, int L, int Cf, int cM,
                                                         const float* single, const float* wmsa, const void* prev,
                                                         int prev_dt, const float* ln_s, const float* ln_o,
                                                         float eps, void* out, int out_dt) {
-  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (long long)S * L) return;
+  const long long rows = (long long)S * L;
+  const long long row0 = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * EMB_ROWS;
+  if (row0 >= rows) return;
   const int lane = threadIdx.x & 63;
-  const int r = (int)(row % L);
-  float v[EMB_MAXV];
-  if (row < L) {   // sequence 0: the recycled first row, normalised
-    wave_row_load(v, prev, prev_dt, (size_t)r * cM, cM, lane);
-    wave_ln(v, cM, lane, ln_s, ln_o, eps);
-  } else {
+  const int nk = (cM + 63) / 64;
+  float acc[EMB_ROWS][EMB_MAXV];
 #pragma unroll
-    for (int k = 0; k < EMB_MAXV; ++k) v[k] = 0.f;
+  for (int r = 0; r < EMB_ROWS; ++r)
+#pragma unroll
+    for (int k = 0; k < EMB_MAXV; ++k) acc[r][k] = 0.f;
+  for (int j0 = 0; j0 < Cf; j0 += 64) {
+    float fv[EMB_ROWS];
+#pragma unroll
+    for (int r = 0; r < EMB_ROWS; ++r) {
+      const long long row = min(row0 + r, rows - 1);
+      fv[r] = j0 + lane < Cf ? msa_feat[row * Cf + j0 + lane] : 0.f;
+    }
+    const int jn = min(64, Cf - j0);
+    for (int j = 0; j < jn; ++j) {
+      float wj[EMB_MAXV];
+#pragma unroll
+      for (int k = 0; k < EMB_MAXV; ++k) {
+        const int c = lane + 64 * k;
+        wj[k] = (k < nk && c < cM) ? wmsa[(size_t)(j0 + j) * cM + c] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < EMB_ROWS; ++r) {
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fv[r]), j));
+#pragma unroll
+        for (int k = 0; k < EMB_MAXV; ++k) acc[r][k] += x * wj[k];
+      }
+    }
   }
-  const float* f = msa_feat + (size_t)row * Cf;
 #pragma unroll
-  for (int k = 0; k < EMB_MAXV; ++k) {
-    const int c = lane + 64 * k;
-    if (c >= cM) break;
-    float acc = single[(size_t)r * cM + c];
-    for (int j = 0; j < Cf; ++j) acc += f[j] * wmsa[(size_t)j * cM + c];
-    store_act(out, out_dt, (size_t)row * cM + c, acc + v[k]);
+  for (int r = 0; r < EMB_ROWS; ++r) {
+    const long long row = row0 + r;
+    if (row >= rows) break;
+    const int res = (int)(row % L);
+    float v[EMB_MAXV];
+    if (row < L) {   // sequence 0: the recycled first row, normalised
+      wave_row_load(v, prev, prev_dt, (size_t)res * cM, cM, lane);
+      wave_ln(v, cM, lane, ln_s, ln_o, eps);
+    } else {
+#pragma unroll
+      for (int k = 0; k < EMB_MAXV; ++k) v[k] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < EMB_MAXV; ++k) {
+      const int c = lane + 64 * k;
+      if (c < cM) store_act(out, out_dt, (size_t)row * cM + c, acc[r][k] + single[(size_t)res * cM + c] + v[k]);
+    }
   }
 }
 
@@ -172,7 +208,7 @@ __global__ __launch_bounds__(256) void embed_extra_kernel(const float* codes, co
                                                           const float* W, const float* bias, void* out, int out_dt) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= rows * cE) return;
-  const long long row = idx / cE;
+  const long long row = rows * cE < (1LL << 31) ? (long long)((int)idx / cE) : idx / cE;
   const int c = (int)(idx - row * cE);
   const int code = min(max((int)codes[row], 0), 22);   // 23 residue classes; keeps a bad code in bounds
   float acc = bias[c] + W[(size_t)code * cE + c];
@@ -217,7 +253,8 @@ int input_embedder(lf_context* ctx, const lf_input_embedder_args& a) {
   LF_TRY(check_hip(hipGetLastError(), "embed single launch"));
   {
     LaunchScope ls(ctx, "embed.msa");
-    hipLaunchKernelGGL(embed_msa_kernel, dim3((unsigned)(((long long)S * L + 3) / 4)), dim3(256), 0, ctx->stream,
+    const long long groups = ((long long)S * L + EMB_ROWS - 1) / EMB_ROWS;
+    hipLaunchKernelGGL(embed_msa_kernel, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, ctx->stream,
                        a.msa_feat, S, L, a.msa_feature_channels, a.c_m, single, w.preprocess_msa_w,
                        a.prev_msa_first_row, a.msa_dtype, w.prev_msa_norm_scale, w.prev_msa_norm_offset, eps, a.msa,
                        a.msa_dtype);
