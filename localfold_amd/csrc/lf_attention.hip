@@ -131,8 +131,12 @@ struct PwaParams {
   long long nblocks;
 };
 
+constexpr int PWA_KC = 32, PWA_LD = 40;   // k chunk; LDS row pitch in halves (80 B: 16-byte aligned, spread banks)
+
 __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][PWA_T * PWA_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][PWA_T * PWA_LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
   // XCD-aware order: each XCD walks a contiguous range, i tiles fastest, so the blocks that
   // share one n tile of V (and one head of P) run on one L2
@@ -143,47 +147,60 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
   const int tn = (int)((lb / p.nti) % p.ntn);
   const int h = (int)(lb / ((long long)p.nti * p.ntn));
   const int N = p.S * p.d;
-  const int n0 = tn * PWA_T + (wave & 1) * 64, i0 = ti * PWA_T + (wave >> 1) * 64;
+  const int nb0 = tn * PWA_T, ib0 = ti * PWA_T;
+  const int wn = (wave & 1) * 64, wi = (wave >> 1) * 64;
+  const int n0 = nb0 + wn, i0 = ib0 + wi;
 
-  const _Float16* arow[4];
-  const _Float16* brow[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int n = min(n0 + t * 16 + r16, N - 1);
+  // staging: thread t copies 16 halves (two 16-byte loads) of row t / 2 of each operand tile
+  const int srow = tid >> 1, shalf = (tid & 1) * 16;
+  const _Float16* ga;
+  const _Float16* gb;
+  {
+    const int n = min(nb0 + srow, N - 1);
     const int s = n / p.d, e = n - s * p.d;
-    arow[t] = p.vt + ((long long)(s * p.H + h) * p.d + e) * p.Qp + g4 * 8;
-    const int i = min(i0 + t * 16 + r16, p.Q - 1);
-    brow[t] = p.p + ((long long)h * p.Q + i) * p.Qp + g4 * 8;
+    ga = p.vt + ((long long)(s * p.H + h) * p.d + e) * p.Qp + shalf;
+    const int i = min(ib0 + srow, p.Q - 1);
+    gb = p.p + ((long long)h * p.Q + i) * p.Qp + shalf;
   }
   f4 acc[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-  h8 fa[4], fb[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    fa[t] = *(const h8*)arow[t];
-    fb[t] = *(const h8*)brow[t];
-  }
-  for (int k0 = 0; k0 < p.Qp; k0 += 32) {
-    // next step's fragments (clamped to the last step: unconditional loads keep the waits exact)
-    const int kn = min(k0 + 32, p.Qp - 32);
-    h8 na[4], nb[4];
+  h8 ra0 = *(const h8*)ga, ra1 = *(const h8*)(ga + 8), rb0 = *(const h8*)gb, rb1 = *(const h8*)(gb + 8);
+  *(h8*)&As[0][srow * PWA_LD + shalf] = ra0;
+  *(h8*)&As[0][srow * PWA_LD + shalf + 8] = ra1;
+  *(h8*)&Bs[0][srow * PWA_LD + shalf] = rb0;
+  *(h8*)&Bs[0][srow * PWA_LD + shalf + 8] = rb1;
+  __syncthreads();
+  const int nkc = p.Qp / PWA_KC;
+  for (int kc = 0; kc < nkc; ++kc) {
+    const int buf = kc & 1;
+    const bool more = kc + 1 < nkc;
+    if (more) {
+      const int k1 = (kc + 1) * PWA_KC;
+      ra0 = *(const h8*)(ga + k1);
+      ra1 = *(const h8*)(ga + k1 + 8);
+      rb0 = *(const h8*)(gb + k1);
+      rb1 = *(const h8*)(gb + k1 + 8);
+    }
+    h8 fa[4], fb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      na[t] = *(const h8*)(arow[t] + kn);
-      nb[t] = *(const h8*)(brow[t] + kn);
+      fa[t] = *(const h8*)&As[buf][(wn + t * 16 + r16) * PWA_LD + g4 * 8];
+      fb[t] = *(const h8*)&Bs[buf][(wi + t * 16 + r16) * PWA_LD + g4 * 8];
     }
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(fa[a], fb[b], acc[a][b]);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      fa[t] = na[t];
-      fb[t] = nb[t];
+    if (more) {
+      *(h8*)&As[buf ^ 1][srow * PWA_LD + shalf] = ra0;
+      *(h8*)&As[buf ^ 1][srow * PWA_LD + shalf + 8] = ra1;
+      *(h8*)&Bs[buf ^ 1][srow * PWA_LD + shalf] = rb0;
+      *(h8*)&Bs[buf ^ 1][srow * PWA_LD + shalf + 8] = rb1;
     }
+    __syncthreads();
   }
   // epilogue: gate values first (loads ahead of every store), then the gated stores
   h4 gv[4][4];
