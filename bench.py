@@ -27,7 +27,9 @@ def log(*a):
 
 
 def algorithmic(n=N, cz=CZ, ch=CH, act_bytes=2):
-    """Per-direction flops and minimum HBM bytes of each kernel (formulas in DESIGN.md)."""
+    """Per-direction flops and minimum HBM bytes of each kernel (p = N^2 pairs):
+    project reads z (cZ per pair) and writes a, b (cH each, f16); contract reads a, b and writes
+    X (cH); output reads X and z and writes the updated z."""
     p = n * n
     return {
         "project": {"flops": 2 * p * cz * ch * 4, "bytes": p * cz * act_bytes + 2 * p * ch * 2},
@@ -347,7 +349,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the pair stack's row "
-              "sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "sharding is a design note only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
