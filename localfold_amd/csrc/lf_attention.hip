@@ -117,7 +117,8 @@ __global__ __launch_bounds__(256) void pwa_softmax_kernel(_Float16* bias, const 
 
 // Pair-weighted averaging, step 2, per head h an NT GEMM on the matrix cores:
 //   O^T[n][i] = sum_j Vt[n][j] P[i][j],  n = (s, e) over sequences s and head dims e < d,
-// gated and stored as o[(s Q + i)][h d + e] = O * g.  Vt rows: vt + ((s H + h) d + e) Qp.
+// gated and stored as o[(s Q + i)][h d + e] = O * g.  Vt rows: vt + ((s H + h) d + e) Qp; the
+// gate is head-major, g[h][s][i][e], so a block's gate reads are whole lines.
 // Block: 4 waves in 2 x 2, a 128 (n) x 128 (i) tile; a wave holds 4 x 4 16x16 accumulators and
 // reads its fragments straight from L2 (P of one head is shared by every block of that head).
 // A lane's 4 accumulator rows are 4 consecutive n, i.e. 4 consecutive head dims of one
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
     for (int b = 0; b < 4; ++b) {
       const int i = min(i0 + b * 16 + r16, p.Q - 1);
       oi[a][b] = ((long long)s * p.Q + i) * p.HD + h * p.d + e;
-      gv[a][b] = *(const h4*)(p.g + oi[a][b]);
+      gv[a][b] = *(const h4*)(p.g + (((long long)h * p.S + s) * p.Q + i) * p.d + e);
     }
   }
 #pragma unroll
@@ -666,7 +667,8 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
     pp.g[gv].dst = pwa ? Dst{vb, DT_F16, Q, (long long)HD * Qp, 1, d, (long long)d * Qp, Qp}
                        : Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
-    pp.g[gg].dst = dst_rowmajor(gb, DT_F16, (int)rows, HD);
+    pp.g[gg].dst = pwa ? Dst{gb, DT_F16, Q, (long long)Q * d, d, d, (long long)B * Q * d, 1}
+                       : dst_rowmajor(gb, DT_F16, (int)rows, HD);
     if (gbias >= 0) pp.g[gbias].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
   }
