@@ -10,7 +10,7 @@
 //
 // Kernels:
 //   lnproj  LN + the q/k/v/g (+ bias) projections in one pass over the rows
-//           (q, k: [b][h][n][32] f16; v: [b][h][32][n] f16 (transposed for P.V); g: [rows][H*d])
+//           (q, k: [b][h][n][32] f16; v: [b][h][32][n] f16 (transposed for P.V); g: [h][rows][d], head-major)
 //   keybias kb[b][k] = 1e9 (mask - 1)
 //   flash   per (b, h, 128 queries): S^T = K Q^T on MFMA, online softmax with each lane
 //           owning one query (statistics: two cross-lane shuffles), O^T += V^T P^T on MFMA;
@@ -518,8 +518,9 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       const int d0 = dt * 16 + 4 * g4;
       if (d0 >= p.d) continue;
       const size_t base = row * p.HD + (size_t)h * p.d + d0;
+      const size_t gbase = ((size_t)h * p.B * p.Q + row) * p.d + d0;   // gate head-major [h][row][d]
       if (d0 + 4 <= p.d && (p.d & 3) == 0) {
-        const h4 gv = *reinterpret_cast<const h4*>(p.g + base);
+        const h4 gv = *reinterpret_cast<const h4*>(p.g + gbase);
         h4 ov;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov[i] = (_Float16)(o[dt][qt][i] * inv * (float)gv[i]);
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (d0 + i < p.d) p.o[base + i] = (_Float16)(o[dt][qt][i] * inv * (float)p.g[base + i]);
+          if (d0 + i < p.d) p.o[base + i] = (_Float16)(o[dt][qt][i] * inv * (float)p.g[gbase + i]);
       }
     }
   }
@@ -667,8 +668,9 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
     pp.g[gv].dst = pwa ? Dst{vb, DT_F16, Q, (long long)HD * Qp, 1, d, (long long)d * Qp, Qp}
                        : Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
-    pp.g[gg].dst = pwa ? Dst{gb, DT_F16, Q, (long long)Q * d, d, d, (long long)B * Q * d, 1}
-                       : dst_rowmajor(gb, DT_F16, (int)rows, HD);
+    // the gate head-major, g[h][b][q][d]: the consumers read one head's slice of many rows,
+    // which is then whole lines
+    pp.g[gg].dst = Dst{gb, DT_F16, Q, (long long)Q * d, d, d, (long long)B * Q * d, 1};
     if (gbias >= 0) pp.g[gbias].dst = bias_dst;
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
   }
