@@ -136,7 +136,8 @@ def _dev(ctx, x, dt=None):
                                                     (40, 70, 64, 128, 8, 8, "bfloat16"),
                                                     (7, 130, 64, 32, 2, 32, "float16"),
                                                     (3, 5, 16, 16, 2, 4, "float32"),
-                                                    (6, 70, 16, 16, 4, 6, "bfloat16")])
+                                                    (6, 70, 16, 16, 4, 6, "bfloat16"),
+                                                    (256, 200, 64, 128, 8, 8, "bfloat16")])
 def test_pair_weighted_averaging(ctx, s, n, cm, cz, heads, dim, dt):
     """The op (update only) against the oracle; ragged token counts (keys past one 64-key
     chunk), a token masked in some sequences, a token no sequence covers; head widths that are
