@@ -132,7 +132,7 @@ struct PwaParams {
   long long nblocks;
 };
 
-constexpr int PWA_KC = 32, PWA_LD = 40;   // k chunk; LDS row pitch in halves (80 B: 16-byte aligned, spread banks)
+constexpr int PWA_KC = 64, PWA_LD = 72;   // k chunk; LDS row pitch in halves (144 B: 16-byte aligned, spread banks)
 
 __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
   __shared__ __attribute__((aligned(16))) _Float16 As[2][PWA_T * PWA_LD];
@@ -152,8 +152,8 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
   const int wn = (wave & 1) * 64, wi = (wave >> 1) * 64;
   const int n0 = nb0 + wn, i0 = ib0 + wi;
 
-  // staging: thread t copies 16 halves (two 16-byte loads) of row t / 2 of each operand tile
-  const int srow = tid >> 1, shalf = (tid & 1) * 16;
+  // staging: thread t copies 32 halves (four 16-byte loads) of row t / 2 of each operand tile
+  const int srow = tid >> 1, shalf = (tid & 1) * 32;
   const _Float16* ga;
   const _Float16* gb;
   {
@@ -168,11 +168,17 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-  h8 ra0 = *(const h8*)ga, ra1 = *(const h8*)(ga + 8), rb0 = *(const h8*)gb, rb1 = *(const h8*)(gb + 8);
-  *(h8*)&As[0][srow * PWA_LD + shalf] = ra0;
-  *(h8*)&As[0][srow * PWA_LD + shalf + 8] = ra1;
-  *(h8*)&Bs[0][srow * PWA_LD + shalf] = rb0;
-  *(h8*)&Bs[0][srow * PWA_LD + shalf + 8] = rb1;
+  h8 ra[4], rb[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ra[u] = *(const h8*)(ga + 8 * u);
+    rb[u] = *(const h8*)(gb + 8 * u);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    *(h8*)&As[0][srow * PWA_LD + shalf + 8 * u] = ra[u];
+    *(h8*)&Bs[0][srow * PWA_LD + shalf + 8 * u] = rb[u];
+  }
   __syncthreads();
   const int nkc = p.Qp / PWA_KC;
   for (int kc = 0; kc < nkc; ++kc) {
@@ -180,26 +186,31 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
     const bool more = kc + 1 < nkc;
     if (more) {
       const int k1 = (kc + 1) * PWA_KC;
-      ra0 = *(const h8*)(ga + k1);
-      ra1 = *(const h8*)(ga + k1 + 8);
-      rb0 = *(const h8*)(gb + k1);
-      rb1 = *(const h8*)(gb + k1 + 8);
-    }
-    h8 fa[4], fb[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      fa[t] = *(const h8*)&As[buf][(wn + t * 16 + r16) * PWA_LD + g4 * 8];
-      fb[t] = *(const h8*)&Bs[buf][(wi + t * 16 + r16) * PWA_LD + g4 * 8];
+      for (int u = 0; u < 4; ++u) {
+        ra[u] = *(const h8*)(ga + k1 + 8 * u);
+        rb[u] = *(const h8*)(gb + k1 + 8 * u);
+      }
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int kk = 0; kk < PWA_KC; kk += 32) {
+      h8 fa[4], fb[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(fa[a], fb[b], acc[a][b]);
+      for (int t = 0; t < 4; ++t) {
+        fa[t] = *(const h8*)&As[buf][(wn + t * 16 + r16) * PWA_LD + kk + g4 * 8];
+        fb[t] = *(const h8*)&Bs[buf][(wi + t * 16 + r16) * PWA_LD + kk + g4 * 8];
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(fa[a], fb[b], acc[a][b]);
+    }
     if (more) {
-      *(h8*)&As[buf ^ 1][srow * PWA_LD + shalf] = ra0;
-      *(h8*)&As[buf ^ 1][srow * PWA_LD + shalf + 8] = ra1;
-      *(h8*)&Bs[buf ^ 1][srow * PWA_LD + shalf] = rb0;
-      *(h8*)&Bs[buf ^ 1][srow * PWA_LD + shalf + 8] = rb1;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        *(h8*)&As[buf ^ 1][srow * PWA_LD + shalf + 8 * u] = ra[u];
+        *(h8*)&Bs[buf ^ 1][srow * PWA_LD + shalf + 8 * u] = rb[u];
+      }
     }
     __syncthreads();
   }
