@@ -53,7 +53,10 @@ def test_struct_sizes_match_c_layout():
     structs = ["lf_weight", "lf_tri_mult_weights", "lf_tri_mult_args", "lf_attention_weights", "lf_attention_args",
                "lf_transition_weights", "lf_transition_args", "lf_opm_weights", "lf_opm_args",
                "lf_evoformer_weights", "lf_evoformer_block_args", "lf_pairformer_weights",
-               "lf_pairformer_block_args", "lf_kernel_timing"]
+               "lf_pairformer_block_args", "lf_kernel_timing", "lf_global_attention_weights",
+               "lf_global_attention_args", "lf_extra_msa_weights", "lf_input_embedder_weights",
+               "lf_input_embedder_args", "lf_af2_recycle_args", "lf_pair_averaging_weights",
+               "lf_pair_averaging_args", "lf_msa_module_weights", "lf_msa_block_args"]
     src = "#include <stdio.h>\n#include \"localfold.h\"\nint main(){\n" + "".join(
         f'printf("{s} %zu\\n", sizeof({s}));\n' for s in structs) + "return 0;}\n"
     with tempfile.TemporaryDirectory() as d:
