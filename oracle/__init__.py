@@ -22,7 +22,8 @@ Arithmetic follows the reference's JS: every intermediate is computed in float64
 numbers) and stored as float32 (`Float32Array`) at the same points the reference stores
 it.  Each function cites the reference file:line it follows.
 
-Pinning status (what checks each function, in tests/test_oracle.py):
+Pinning status (what checks each function, in tests/test_oracle.py and, for the AF3
+functions, tests/test_oracle_af3.py):
 
 * tri_mult_af2 outgoing   - the four committed fixtures (OpenFold + three AlphaFold captures)
 * tri_mult_af2 incoming   - transpose identity against outgoing on the same fixtures,
@@ -33,13 +34,24 @@ Pinning status (what checks each function, in tests/test_oracle.py):
 * attention (all modes)   - brute-force per-element softmax loops on tiny inputs;
                             invariants: one unmasked key -> that value row; transpose
                             identity; zero bias -> plain attention
-* outer_product_mean      - S=1 closed form and the count identity
+* outer_product_mean_af2  - S=1 closed form and the count identity
+* outer_product_mean_af3  - the reference's hand-computed cases (`test/af3-msa.test.js:40-107`:
+                            sum before divide, per-pair coverage, uncovered pair = 0,
+                            asymmetry) plus channel order and bias-before-divide
+* single_attention_af3    - per-element loops of `singleAttention` on tiny inputs; a
+                            two-token closed form that fixes the 1/sqrt(d) scale, the q bias
+                            and the pair logit; masked-key and one-unmasked-key invariants
+* grid_self_attention_af3 - per-element loops of `gridSelfAttention` (starting, ending,
+                            ending with the swapped bias) on an asymmetric mask; a closed
+                            form that fixes the scale and the key mask
 * transitions             - closed forms (ReLU split, SwiGLU blocked split, swish(1))
 * codecs                  - the reference's own int5 boundary cases
                             (`test/int5-tensor.test.js`), quantise->decode round trips
 * generator               - integer restatement (counter form), checked against a direct
                             sequential loop
-* evoformer / pairformer block order - composition of the pinned ops (parity of the
+* pairformer block order  - the single track reads the pair after all five pair updates
+                            (reading it before the pair transition fails the check)
+* evoformer block order   - composition of the pinned ops (parity of the
                             composition itself is pinned only by that construction:
                             the reference's block fixtures are absent from its checkout)
 """
