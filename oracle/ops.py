@@ -7,10 +7,27 @@ masks [N, N] / [S, N], triangle weights (out,in), everything else (in,out).
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 """
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 F32 = np.float32
 F64 = np.float64
+
+
+def _parallel(fn, items):
+    """Runs fn over independent items on host threads (numpy releases the GIL in its array
+    loops and BLAS calls); each item writes a disjoint slice of its output."""
+    items = list(items)
+    workers = min(len(items), int(os.environ.get("LOCALFOLD_ORACLE_THREADS", min(16, os.cpu_count() or 1))))
+    if workers <= 1:
+        for it in items:
+            fn(it)
+        return
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(1), ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(fn, items))
 
 
 def _f32(x):
@@ -191,21 +208,25 @@ def attention_af2(activations, mask, w, heads, transpose=False, pair_bias=None, 
     g = _f32(sigmoid(linear(x, w["gatingWeight"], w["gatingBias"])))
 
     def heads_of(t):
-        return np.asarray(t, F64).reshape(bsz, nq, heads, d).transpose(0, 2, 1, 3)
+        return np.asarray(t, F64).reshape(t.shape[0], nq, heads, d).transpose(0, 2, 1, 3)
 
     out = np.empty((bsz, nq, heads, d), F64)
-    step = batch_chunk or max(1, int(2 ** 25 // max(1, heads * nq * nq)))
-    for b0 in range(0, bsz, step):
+    step = batch_chunk or max(1, int(2 ** 22 // max(1, heads * nq * nq)))
+
+    def rows(b0):
         b1 = min(bsz, b0 + step)
         mb = (1e9 * (msk[b0:b1] - 1.0))[:, None, None, :]
         lb = mb if bias is None else mb + bias[None]
         qh, kh, vh = heads_of(q[b0:b1]), heads_of(kk[b0:b1]), heads_of(v[b0:b1])
-        logits = qh @ kh.transpose(0, 1, 3, 2) + lb
-        logits = np.clip(logits, -1e8, 1e8)
+        logits = qh @ kh.transpose(0, 1, 3, 2)
+        logits += lb
+        np.clip(logits, -1e8, 1e8, out=logits)
         logits -= logits.max(-1, keepdims=True)
-        p = np.exp(logits)
-        p /= p.sum(-1, keepdims=True)
-        out[b0:b1] = (p @ vh).transpose(0, 2, 1, 3)
+        np.exp(logits, out=logits)
+        logits /= logits.sum(-1, keepdims=True)
+        out[b0:b1] = (logits @ vh).transpose(0, 2, 1, 3)
+
+    _parallel(rows, range(0, bsz, step))
     o = _f32(out.reshape(bsz, nq, c) * np.asarray(g, F64))
     upd = linear(o, w["outputWeight"], w["outputBias"])
     if batch_rows is not None:
@@ -347,6 +368,15 @@ def msa_pair_weighted_averaging_af3(msa, mask, pair, w, eps=1e-5):
 # Outer product mean and transitions
 # ---------------------------------------------------------------------------------------
 
+def _outer_sum(left, right):
+    """outer[i, j, a*c + b] = sum_s left[s, i, a] * right[s, j, b] (the einsum 'sia,sjb->ijab'),
+    as one float64 GEMM over the sequences."""
+    s, n, co = left.shape
+    l2 = np.asarray(left, F64).reshape(s, n * co)
+    r2 = np.asarray(right, F64).reshape(s, n * co)
+    return (l2.T @ r2).reshape(n, co, n, co).transpose(0, 2, 1, 3).reshape(n, n, co * co)
+
+
 def outer_product_mean_af2(msa, mask, w, eps=1e-5, norm_eps=1e-3):
     """AF2 OPM, the semantics of `OuterProductMeanGpu` (`webgpu/kernels/outer-product-mean.js`).
 
@@ -360,7 +390,7 @@ def outer_product_mean_af2(msa, mask, w, eps=1e-5, norm_eps=1e-3):
     m = np.asarray(mask, F64)[..., None]
     left = _f32(np.asarray(linear(x, w["leftWeight"], w["leftBias"]), F64) * m)
     right = _f32(np.asarray(linear(x, w["rightWeight"], w["rightBias"]), F64) * m)
-    outer = np.einsum("sia,sjb->ijab", np.asarray(left, F64), np.asarray(right, F64)).reshape(n, n, co * co)
+    outer = _outer_sum(left, right)
     upd = outer @ np.asarray(w["outputWeight"], F64) + np.asarray(w["outputBias"], F64)
     count = np.asarray(mask, F64).T @ np.asarray(mask, F64)          # [i, j] = sum_s m_si m_sj
     return _f32(upd / (norm_eps + count)[..., None])
@@ -374,7 +404,7 @@ def outer_product_mean_af3(msa, mask, w, eps=1e-5, norm_eps=1e-3):
     m = np.asarray(mask, F64)[..., None]
     left = _f32(np.asarray(linear(x, w["leftProjection"]), F64) * m)
     right = _f32(np.asarray(linear(x, w["rightProjection"]), F64) * m)
-    outer = np.einsum("sia,sjb->ijab", np.asarray(left, F64), np.asarray(right, F64)).reshape(n, n, co * co)
+    outer = _outer_sum(left, right)
     upd = outer @ np.asarray(w["outputW"], F64)
     if w.get("outputB") is not None:
         upd = upd + np.asarray(w["outputB"], F64)
