@@ -127,6 +127,17 @@ typedef struct {
  * and encodeTriangleMultiplication (webgpu/af2/evoformer/block.js:1288-1535). */
 int lf_tri_mult(lf_context* ctx, const lf_tri_mult_args* args);
 
+/* No counterpart in the reference: lf_tri_mult for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as lf_tri_mult, but its scratch (the a, b and X planes,
+ * 3 * c_hidden * N^2 f16, plus the decoded weights) lives in a static per-device array of
+ * LF_TRI_NOALLOC_SCRATCH_BYTES, looked up once per device by lf_context_create; nothing is
+ * allocated or freed.  Shapes needing more scratch are rejected with LF_ERR_INVALID (c_hidden
+ * 128 fits N <= 417).  Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two threads, two contexts) race, so serialise them. */
+#define LF_TRI_NOALLOC_SCRATCH_BYTES (128u << 20)
+int lf_tri_mult_noalloc(lf_context* ctx, const lf_tri_mult_args* args);
+
 /* ---- gated attention (MSA row / column, triangle starting / ending, AF3 grid / single) -- */
 
 enum { LF_BIAS_NONE = 0, LF_BIAS_SEPARATE = 1, LF_BIAS_NORMALIZED_INPUT = 2, LF_BIAS_LOGITS = 3 };

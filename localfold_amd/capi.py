@@ -206,6 +206,7 @@ PROTOTYPES = [
     ("lf_profile_enable", C.c_int, [P, C.c_int]),
     ("lf_profile_read", C.c_int, [P, C.POINTER(lf_kernel_timing), C.c_int]),
     ("lf_tri_mult", C.c_int, [P, C.POINTER(lf_tri_mult_args)]),
+    ("lf_tri_mult_noalloc", C.c_int, [P, C.POINTER(lf_tri_mult_args)]),
     ("lf_attention", C.c_int, [P, C.POINTER(lf_attention_args)]),
     ("lf_transition", C.c_int, [P, C.POINTER(lf_transition_args)]),
     ("lf_outer_product_mean", C.c_int, [P, C.POINTER(lf_opm_args)]),

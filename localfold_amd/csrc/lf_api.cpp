@@ -143,6 +143,11 @@ lf_context* lf_context_create(int device_ordinal) {
     return nullptr;
   }
   ctx->stream = ctx->own_stream;
+  if (lf::tri_noalloc_init(device_ordinal) != LF_OK) {
+    hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return nullptr;
+  }
   return ctx;
 }
 
@@ -263,6 +268,7 @@ int lf_profile_read(lf_context* ctx, lf_kernel_timing* out, int max) {
 
 namespace lf {
 inline int impl_lf_tri_mult(lf_context* c, const lf_tri_mult_args& a) { return tri_mult(c, a); }
+inline int impl_lf_tri_mult_noalloc(lf_context* c, const lf_tri_mult_args& a) { return tri_mult_noalloc(c, a); }
 inline int impl_lf_attention(lf_context* c, const lf_attention_args& a) { return attention(c, a); }
 inline int impl_lf_transition(lf_context* c, const lf_transition_args& a) { return transition(c, a); }
 inline int impl_lf_outer_product_mean(lf_context* c, const lf_opm_args& a) { return outer_product_mean(c, a); }
@@ -274,6 +280,7 @@ inline int impl_lf_input_embedder(lf_context* c, const lf_input_embedder_args& a
 
 extern "C" {
 LF_ENTRY(lf_tri_mult, lf_tri_mult_args)
+LF_ENTRY(lf_tri_mult_noalloc, lf_tri_mult_args)
 LF_ENTRY(lf_attention, lf_attention_args)
 LF_ENTRY(lf_transition, lf_transition_args)
 LF_ENTRY(lf_outer_product_mean, lf_opm_args)

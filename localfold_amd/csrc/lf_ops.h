@@ -36,6 +36,10 @@ inline bool act_dtype_ok(int dt) { return dt == LF_F32 || dt == LF_F16 || dt == 
 inline size_t act_bytes(int dt) { return dt == LF_F32 ? 4 : 2; }
 
 int tri_mult(lf_context* ctx, const lf_tri_mult_args& a);
+// lf_tri_mult on the library's static per-device scratch (no allocation); tri_noalloc_init
+// looks up that scratch's address on `device`, which must be current
+int tri_mult_noalloc(lf_context* ctx, const lf_tri_mult_args& a);
+int tri_noalloc_init(int device);
 // no_qk: every logit is the bias alone (AF3 pair-weighted averaging; wq/wk are not read);
 // shared_key_mask: one key mask for every batch row, the maximum of a.mask over the batch
 int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk = false, bool shared_key_mask = false);

@@ -22,6 +22,8 @@
 // cpu/af3/trunk/pairformer.js:213-300 (AF3, both directions, interleaved split).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "lf_gemm.h"
@@ -1085,7 +1087,10 @@ static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resid
 
 static int kpad_of(int c) { return c <= 64 ? 64 : (c <= 128 ? 128 : 256); }
 
-int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
+// One triangle multiplicative update.  Its scratch (a, b, X planes and the expanded weights)
+// comes from the context workspace, or, when `scratch` is not NULL, from that device buffer of
+// `scratch_cap` bytes, in which case nothing is allocated.
+static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scratch, size_t scratch_cap) {
   LF_REQUIRE(a.w != nullptr, "tri_mult: weights are NULL");
   LF_REQUIRE(a.length > 0 && a.c_z > 0 && a.c_hidden > 0, "tri_mult: length, c_z and c_hidden must be positive");
   LF_REQUIRE(a.c_z <= 256 && a.c_hidden <= 256, "tri_mult: c_z and c_hidden must be <= 256");
@@ -1138,7 +1143,20 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
   size_t sizes[9] = {plane, plane, plane};
   for (int i = 0; i < 6; ++i) sizes[3 + i] = expanded_bytes(views[i]);
   void* bufs[9];
-  LF_TRY(workspace(ctx, sizes, bufs, 9));
+  if (scratch) {
+    size_t total = 0;
+    for (int i = 0; i < 9; ++i) {
+      bufs[i] = static_cast<char*>(scratch) + total;
+      total += (sizes[i] + 255) & ~size_t(255);
+    }
+    if (total > scratch_cap)
+      return set_error(LF_ERR_INVALID, "tri_mult_noalloc: N=" + std::to_string(N) + ", c_hidden=" +
+                                           std::to_string(H) + " needs " + std::to_string(total) +
+                                           " bytes of scratch; the static scratch holds " +
+                                           std::to_string(scratch_cap));
+  } else {
+    LF_TRY(workspace(ctx, sizes, bufs, 9));
+  }
   pp.out[0] = static_cast<_Float16*>(bufs[0]);
   pp.out[1] = static_cast<_Float16*>(bufs[1]);
   _Float16* X = static_cast<_Float16*>(bufs[2]);
@@ -1218,6 +1236,42 @@ int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) {
     else launch_output<DT_BF16>(ctx, op, resident, kz, kh);
   }
   return check_hip(hipGetLastError(), "tri_output launch");
+}
+
+int tri_mult(lf_context* ctx, const lf_tri_mult_args& a) { return tri_mult_impl(ctx, a, nullptr, 0); }
+
+// ---- the allocation-free entry point ---------------------------------------------------
+// A file-scope device array serves as the scratch of lf_tri_mult_noalloc.  Each device holds
+// its own copy at its own address, looked up once per device (with that device current) by
+// tri_noalloc_init, which lf_context_create calls; host code only ever passes that address,
+// never the array's name, which on the host is a stand-in and not a device address.
+static __device__ __align__(256) unsigned char scratch[LF_TRI_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int tri_noalloc_init(int device) {
+  if (device < 0 || device >= kMaxDevices) return set_error(LF_ERR_INVALID, "tri_noalloc_init: device out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return LF_OK;
+  void* p = nullptr;
+  LF_TRY(check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+  if (!p) return set_error(LF_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+  g_scratch_ptr[device] = p;
+  return LF_OK;
+}
+
+int tri_mult_noalloc(lf_context* ctx, const lf_tri_mult_args& a) {
+  LF_TRY(tri_noalloc_init(ctx->device));   // a lookup only on the first call on this device
+  void* p;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[ctx->device];
+  }
+  return tri_mult_impl(ctx, a, p, LF_TRI_NOALLOC_SCRATCH_BYTES);
 }
 
 }  // namespace lf

@@ -178,7 +178,11 @@ def tri_mult_weights(dw: DeviceWeights, w: dict, dialect: int = capi.LF_AF2) -> 
 
 def tri_mult(ctx: Context, z: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf_tri_mult_weights,
              direction: str = "outgoing", dialect: int = capi.LF_AF2, out: torch.Tensor = None,
-             accumulate: bool = False, epsilon: float = 1e-5, divide_by_length: bool = False) -> torch.Tensor:
+             accumulate: bool = False, epsilon: float = 1e-5, divide_by_length: bool = False,
+             noalloc: bool = False) -> torch.Tensor:
+    """One triangle multiplicative update through lf_tri_mult, or, with noalloc, through
+    lf_tri_mult_noalloc (the library's static scratch; `out` must then be given by callers
+    that cannot allocate)."""
     n, n2, cz = z.shape
     if n != n2 or tuple(mask.shape) != (n, n) or mask.dtype != torch.float32:
         raise ValueError("z must be [N, N, cZ] and mask [N, N] float32")
@@ -195,7 +199,8 @@ def tri_mult(ctx: Context, z: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf
     a.accumulate = int(accumulate)
     a.epsilon = epsilon
     a.w = C.pointer(wstruct)
-    check(ctx.lib.lf_tri_mult(ctx.handle, C.byref(a)))
+    fn = ctx.lib.lf_tri_mult_noalloc if noalloc else ctx.lib.lf_tri_mult
+    check(fn(ctx.handle, C.byref(a)))
     return out
 
 
