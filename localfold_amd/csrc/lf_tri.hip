@@ -202,130 +202,172 @@ struct TriContractParams {
   float scale;
 };
 
-constexpr int CT_TILE = 128, CT_BK = 64, CT_LD = CT_BK + 8;
-
-// Loads the [128 x 64] (m, k) tile of one operand into S[m][k], element by element (any N).
-// KMAJOR: element (m, k) is stored at src[k*N + m]; otherwise at src[m*N + k].
-template <bool KMAJOR>
+template <int TM, int BK, bool KMAJOR>
 __device__ __forceinline__ void ct_load(_Float16* S, const _Float16* src, int N, int m0, int k0, int tid) {
-  for (int e = tid; e < CT_TILE * CT_BK; e += 256) {
+  constexpr int LD = BK + 8;
+  for (int e = tid; e < TM * BK; e += 256) {
     int m, k;
     if (!KMAJOR) {
-      m = e / CT_BK;
-      k = e % CT_BK;
+      m = e / BK;
+      k = e % BK;
     } else {
-      k = e / CT_TILE;
-      m = e % CT_TILE;
+      k = e / TM;
+      m = e % TM;
     }
     const int gm = m0 + m, gk = k0 + k;
-    S[m * CT_LD + k] = (gm < N && gk < N) ? src[KMAJOR ? (size_t)gk * N + gm : (size_t)gm * N + gk] : (_Float16)0.f;
+    S[m * LD + k] = (gm < N && gk < N) ? src[KMAJOR ? (size_t)gk * N + gm : (size_t)gm * N + gk] : (_Float16)0.f;
   }
 }
 
 // Vector form (N % 8 == 0) split in two: global -> registers (issued before the current K
-// step's MFMAs so the loads are in flight during them) and registers -> LDS.
-struct CtRegs {
-  h8 v[4];
-};
+// step's MFMAs so the loads are in flight during them) and registers -> LDS.  PER = TM / 32
+// 16-byte pieces per thread and operand.
+// The piece it of a thread: its (m, k) origin in the [TM x 64] slice at (m0, k0).
+template <int TM, int BK, bool KMAJOR>
+__device__ __forceinline__ void ct_piece(int it, int tid, int m0, int k0, int& gm, int& gk) {
+  if (!KMAJOR) {
+    const int e = tid + it * 256;
+    gm = m0 + e / (BK / 8);
+    gk = k0 + (e % (BK / 8)) * 8;
+  } else {
+    const int e = tid + it * 256;
+    gk = k0 + e % BK;
+    gm = m0 + (e / BK) * 8;
+  }
+}
 
-template <bool KMAJOR>
-__device__ __forceinline__ void ct_fetch(CtRegs& r, const _Float16* src, int N, int m0, int k0, int tid) {
+// Branch-free: a clamped address always loads and an out-of-range piece is zeroed when it is
+// written to LDS (ct_store), not here: a select on the loaded value at this point would make
+// the compiler wait for the loads before the MFMAs they are meant to overlap, and a branch
+// per load lets it serialise them with vmcnt(0) waits.
+template <int TM, int BK, bool KMAJOR>
+__device__ __forceinline__ void ct_fetch(h8 (&r)[TM * BK / 2048], const _Float16* src, int N, int m0, int k0, int tid) {
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < TM * BK / 2048; ++it) {
     int gm, gk;
-    if (!KMAJOR) {
-      const int e = tid + it * 256;
-      gm = m0 + (e >> 3);
-      gk = k0 + (e & 7) * 8;
-    } else {
-      gk = k0 + (tid & 63);
-      gm = m0 + ((tid >> 6) + it * 4) * 8;
-    }
-    r.v[it] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (gm < N && gk < N) r.v[it] = *reinterpret_cast<const h8*>(src + (KMAJOR ? (size_t)gk * N + gm : (size_t)gm * N + gk));
+    ct_piece<TM, BK, KMAJOR>(it, tid, m0, k0, gm, gk);
+    const bool ok = gm < N && gk < N;
+    const int cm = ok ? gm : 0, ck = ok ? gk : 0;
+    r[it] = *reinterpret_cast<const h8*>(src + (KMAJOR ? (size_t)ck * N + cm : (size_t)cm * N + ck));
   }
 }
 
-template <bool KMAJOR>
-__device__ __forceinline__ void ct_store(_Float16* S, const CtRegs& r, int tid) {
+template <int TM, int BK, bool KMAJOR>
+__device__ __forceinline__ void ct_store(_Float16* S, const h8 (&r)[TM * BK / 2048], int N, int m0, int k0, int tid) {
+  constexpr int LD = BK + 8;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < TM * BK / 2048; ++it) {
+    int gm, gk;
+    ct_piece<TM, BK, KMAJOR>(it, tid, m0, k0, gm, gk);
+    const h8 v = (gm < N && gk < N) ? r[it] : h8{0, 0, 0, 0, 0, 0, 0, 0};
     if (!KMAJOR) {
-      const int e = tid + it * 256;
-      *reinterpret_cast<h8*>(S + (e >> 3) * CT_LD + (e & 7) * 8) = r.v[it];
+      *reinterpret_cast<h8*>(S + (gm - m0) * LD + (gk - k0)) = v;
     } else {
-      // lane -> k, so the eight 2-byte LDS stores of a wave hit 64 consecutive k
-      const int k = tid & 63, seg = (tid >> 6) + it * 4;
+      // lane -> k, so the eight 2-byte LDS stores of a wave hit consecutive k
 #pragma unroll
-      for (int j = 0; j < 8; ++j) S[(seg * 8 + j) * CT_LD + k] = r.v[it][j];
+      for (int j = 0; j < 8; ++j) S[(gm - m0 + j) * LD + (gk - k0)] = v[j];
     }
   }
 }
 
-// One 128x128 tile of X[h] per block.  The 1-D grid is remapped so that consecutive logical
-// blocks (the tiles of one channel, which share their A rows and B rows) run on the same
-// XCD: the hardware deals block ids round-robin over the 8 XCDs, each with its own L2.
-template <bool KMAJOR, bool VEC>
-__global__ __launch_bounds__(256) void tri_contract_kernel(TriContractParams p) {
-  __shared__ __attribute__((aligned(16))) _Float16 Ls[CT_TILE * CT_LD];
-  __shared__ __attribute__((aligned(16))) _Float16 Rs[CT_TILE * CT_LD];
+// One TM x TM tile of X[h] per block of 4 waves (2 x 2, a (TM/2)-square each), K in steps
+// of BK through one LDS stage, the next step's loads in registers during the current step's
+// MFMAs.  MINW waves per SIMD bound the registers (three: 12 waves a CU).  Measured at
+// N = 384 (128 channels): 128-wide tiles with 64-wide K steps beat 192-wide tiles (fewer,
+// longer blocks hide less latency), 32-wide K steps and 8-wave blocks.  The 1-D grid is
+// remapped so that consecutive logical blocks (the tiles of one channel, which share their
+// A rows and B rows) run on the same XCD: the hardware deals block ids round-robin over the
+// 8 XCDs, each with its own L2.
+template <int TM, int BK, int MINW, bool KMAJOR, bool VEC>
+__global__ __launch_bounds__(256, MINW) void tri_contract_kernel(TriContractParams p) {
+  constexpr int FM = TM / 32, WT = TM / 2, CT_LD = BK + 8, PER = TM * BK / 2048;
+  __shared__ __attribute__((aligned(16))) _Float16 Ls[TM * CT_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Rs[TM * CT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int tm = (p.N + CT_TILE - 1) / CT_TILE, tiles = tm * tm;
+  const int tm = (p.N + TM - 1) / TM, tiles = tm * tm;
   const int total = (int)gridDim.x, per = total >> 3;
   int lin = (int)blockIdx.x;
   if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
   const int h = lin / tiles, t = lin - h * tiles;
-  const int m0 = (t / tm) * CT_TILE, n0 = (t % tm) * CT_TILE;
+  const int m0 = (t / tm) * TM, n0 = (t % tm) * TM;
   const size_t plane = (size_t)p.N * p.N;
   const _Float16* L = p.L + h * plane;
   const _Float16* R = p.R + h * plane;
-  f4 acc[4][4];
-  zero_acc(acc);
+  f4 acc[FM][FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  CtRegs rl, rr;
+  h8 rl[PER], rr[PER];
   if (VEC) {
-    ct_fetch<KMAJOR>(rl, L, p.N, m0, 0, tid);
-    ct_fetch<KMAJOR>(rr, R, p.N, n0, 0, tid);
+    ct_fetch<TM, BK, KMAJOR>(rl, L, p.N, m0, 0, tid);
+    ct_fetch<TM, BK, KMAJOR>(rr, R, p.N, n0, 0, tid);
   }
-  for (int k0 = 0; k0 < p.N; k0 += CT_BK) {
+  for (int k0 = 0; k0 < p.N; k0 += BK) {
     __syncthreads();
     if (VEC) {
-      ct_store<KMAJOR>(Ls, rl, tid);
-      ct_store<KMAJOR>(Rs, rr, tid);
+      ct_store<TM, BK, KMAJOR>(Ls, rl, p.N, m0, k0, tid);
+      ct_store<TM, BK, KMAJOR>(Rs, rr, p.N, n0, k0, tid);
     } else {
-      ct_load<KMAJOR>(Ls, L, p.N, m0, k0, tid);
-      ct_load<KMAJOR>(Rs, R, p.N, n0, k0, tid);
+      ct_load<TM, BK, KMAJOR>(Ls, L, p.N, m0, k0, tid);
+      ct_load<TM, BK, KMAJOR>(Rs, R, p.N, n0, k0, tid);
     }
     __syncthreads();
-    if (VEC && k0 + CT_BK < p.N) {
-      ct_fetch<KMAJOR>(rl, L, p.N, m0, k0 + CT_BK, tid);
-      ct_fetch<KMAJOR>(rr, R, p.N, n0, k0 + CT_BK, tid);
+    if (VEC && k0 + BK < p.N) {
+      ct_fetch<TM, BK, KMAJOR>(rl, L, p.N, m0, k0 + BK, tid);
+      ct_fetch<TM, BK, KMAJOR>(rr, R, p.N, n0, k0 + BK, tid);
     }
 #pragma unroll
-    for (int kk = 0; kk < CT_BK; kk += 32) {
-      h8 a[4], b[4];
+    for (int kk = 0; kk < BK; kk += 32) {
+      h8 a[FM], b[FM];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const h8*>(Ls + (wm * 64 + i * 16 + r16) * CT_LD + kk + kq);
+      for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const h8*>(Ls + (wm * WT + i * 16 + r16) * CT_LD + kk + kq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(Rs + (wn * 64 + j * 16 + r16) * CT_LD + kk + kq);
+      for (int j = 0; j < FM; ++j) b[j] = *reinterpret_cast<const h8*>(Rs + (wn * WT + j * 16 + r16) * CT_LD + kk + kq);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(b[j], a[i], acc[i][j]);
     }
   }
+  // acc[i][j][r] = X[m0 + wm*WT + 16i + r16][n0 + wn*WT + 16j + 4*g4 + r]: four consecutive
+  // columns of one row per lane, stored as one 8-byte piece (16 rows x 32 bytes a store)
   _Float16* X = p.X + h * plane;
+  const int g4 = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i) {
+    const int gm = m0 + wm * WT + i * 16 + r16;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FM; ++j) {
+      const int gn = n0 + wn * WT + j * 16 + 4 * g4;
+      h4 o;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gm = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
-        const int gn = n0 + wn * 64 + j * 16 + r16;
-        if (gm < p.N && gn < p.N) X[(size_t)gm * p.N + gn] = (_Float16)(acc[i][j][r] * p.scale);
+      for (int r = 0; r < 4; ++r) o[r] = (_Float16)(acc[i][j][r] * p.scale);
+      if (VEC) {
+        if (gm < p.N && gn < p.N) *reinterpret_cast<h4*>(X + (size_t)gm * p.N + gn) = o;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (gm < p.N && gn + r < p.N) X[(size_t)gm * p.N + gn + r] = o[r];
       }
+    }
+  }
+}
+
+template <int TM, int BK = 64, int MINW = 1>
+static void launch_contract(lf_context* ctx, const TriContractParams& cp, int H, bool kmajor) {
+  const int tm = (cp.N + TM - 1) / TM;
+  const dim3 grid((unsigned)(tm * tm * H));
+  const bool vec = (cp.N % 8) == 0;
+  if (!kmajor) {
+    if (vec) hipLaunchKernelGGL((tri_contract_kernel<TM, BK, MINW, false, true>), grid, dim3(256), 0, ctx->stream, cp);
+    else hipLaunchKernelGGL((tri_contract_kernel<TM, BK, MINW, false, false>), grid, dim3(256), 0, ctx->stream, cp);
+  } else {
+    if (vec) hipLaunchKernelGGL((tri_contract_kernel<TM, BK, MINW, true, true>), grid, dim3(256), 0, ctx->stream, cp);
+    else hipLaunchKernelGGL((tri_contract_kernel<TM, BK, MINW, true, false>), grid, dim3(256), 0, ctx->stream, cp);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1198,16 +1240,7 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
   cp.R = outgoing ? pp.out[1] : pp.out[0];
   {
     LaunchScope ls(ctx, outgoing ? "tri_out.contract" : "tri_in.contract");
-    const int tm = (N + CT_TILE - 1) / CT_TILE;
-    dim3 grid((unsigned)(tm * tm * H));
-    const bool vec = (N % 8) == 0;
-    if (outgoing || pp.kmajor_out) {
-      if (vec) hipLaunchKernelGGL((tri_contract_kernel<false, true>), grid, dim3(256), 0, ctx->stream, cp);
-      else hipLaunchKernelGGL((tri_contract_kernel<false, false>), grid, dim3(256), 0, ctx->stream, cp);
-    } else {
-      if (vec) hipLaunchKernelGGL((tri_contract_kernel<true, true>), grid, dim3(256), 0, ctx->stream, cp);
-      else hipLaunchKernelGGL((tri_contract_kernel<true, false>), grid, dim3(256), 0, ctx->stream, cp);
-    }
+    launch_contract<128, 64, 3>(ctx, cp, H, !(outgoing || pp.kmajor_out));
   }
   LF_TRY(check_hip(hipGetLastError(), "tri_contract launch"));
 
