@@ -38,26 +38,65 @@ def algorithmic(n=N, cz=CZ, ch=CH, act_bytes=2):
     }
 
 
+def cpu_info():
+    """The host the CPU baseline ran on: model name, logical CPUs, physical cores, BLAS threads."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    physical = None
+    try:
+        import psutil
+        physical = psutil.cpu_count(logical=False)
+    except Exception:
+        pass
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+        blas = max((i.get("num_threads") or 0) for i in threadpool_info() if i.get("user_api") == "blas") or None
+    except Exception:
+        pass
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "physical_cores": physical, "blas_threads": blas}
+
+
 def cpu_baseline(c2, budget_s=30.0):
-    """The oracle (numpy, float64 compute / float32 storage) on the same workload, host cores."""
-    from oracle import codec, ops
+    """The oracle (numpy: float64 compute, float32 storage, BLAS and host threads) timed on
+    this box's host cores: config 2's step (the headline's workload) and config 1 (one AF2
+    Evoformer block at N_res = 64, N_seq = 1, the reference's CPU-path configuration), both at
+    full size."""
+    from oracle import blocks, codec, ops
+    from localfold_amd import synthetic
+    info = cpu_info()
     dec = lambda w: {k: (codec.decode(v) if isinstance(v, dict) and "dtype" in v else v) for k, v in w.items()}
     dec_out, dec_in = dec(c2["rec_out"]), dec(c2["rec_in"])
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     z = c2["z"]
     t0 = time.perf_counter()
     z1 = z + ops.tri_mult_af2(z, c2["mask"], dec_out, "outgoing")
     t1 = time.perf_counter()
-    sample = "one full step (outgoing + incoming) at N=384"
+    sample = "config 2: one full step (outgoing + incoming) at N=384"
     if (t1 - t0) * 2 < budget_s:
         ops.tri_mult_af2(z1, c2["mask"], dec_in, "incoming")
         secs = time.perf_counter() - t0
     else:
         secs = (t1 - t0) * 2
-        sample = "outgoing at N=384, doubled for the step"
+        sample = "config 2: outgoing at N=384, doubled for the step"
     flops = sum(v["flops"] for v in algorithmic().values()) * 2
-    return {"value": round(flops / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": sample + f"; numpy oracle, {secs:.1f} s per step", "ms_per_step": round(secs * 1e3, 1)}
+    w1, msa1, pair1 = synthetic.config1_inputs(seed=0)
+    n1 = pair1.shape[0]
+    t2 = time.perf_counter()
+    blocks.evoformer_block_af2(msa1, pair1, np.ones((1, n1), np.float32), np.ones((n1, n1), np.float32), w1)
+    c1_secs = time.perf_counter() - t2
+    return {"value": round(flops / secs / 1e12, 4), "unit": "TFLOP/s", "cores": info["blas_threads"] or info["logical_cpus"],
+            "kind": "port",
+            "sample": sample + f"; numpy oracle, {secs:.2f} s per step",
+            "ms_per_step": round(secs * 1e3, 1),
+            "config1_block_ms": round(c1_secs * 1e3, 1),
+            "config1_block_gflops": round(5.69 / c1_secs, 3),
+            **info}
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tri_mult_config2_kernel_stats.md")
@@ -144,16 +183,20 @@ def triangle_attention_config3(ctx, D, synthetic, reps):
             "kernels_ms": kern}
 
 
-def evoformer_block_config4(ctx, D, synthetic, reps):
-    """BASELINE config 4 at one block: N_res=384, N_seq=512, int8 weights, bf16 activations."""
+def evoformer_block_config4(ctx, D, synthetic, reps, storage="f32"):
+    """BASELINE config 4 at one block: N_res=384, N_seq=512, int8 weights; the residual
+    stream (msa, pair) stored in `storage` (f32: the configuration whose parity against the
+    oracle is tested within the north-star bound; bf16: the config's storage type, which
+    meets the relative bound only)."""
     import torch
     c4 = synthetic.config4_inputs()
     dev = ctx.device
     dw = D.DeviceWeights(dev)
     w = c4["weights"]
     ws = D.evoformer_weights(dw, w)
-    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16)
-    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16)
+    sdt = torch.float32 if storage == "f32" else torch.bfloat16
+    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16).to(sdt)
+    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16).to(sdt)
     mm = torch.as_tensor(c4["msa_mask"]).to(dev)
     pm = torch.as_tensor(c4["pair_mask"]).to(dev)
     msa0, pair0 = msa.clone(), pair.clone()
@@ -170,7 +213,7 @@ def evoformer_block_config4(ctx, D, synthetic, reps):
     kern = profile_ops(ctx, block, 2)
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     return {"workload": f"BASELINE config 4, one AF2 Evoformer block: N_res={n}, N_seq={s_}, c_m=256, c_z=128, "
-                        "int8 weights (fp16 scales, groups of 64), bf16 activations",
+                        f"int8 weights (fp16 scales, groups of 64), bf16 inputs, {storage} residual stream",
             "ms_per_block": round(ms, 3), "stack_48_blocks_s_estimate": round(48 * ms / 1e3, 3),
             "outputs_finite": finite, "kernels_ms": kern}
 
@@ -266,9 +309,10 @@ def input_embedder_n384(ctx, D, synthetic, reps):
             "ms": round(ms, 3), "kernels_ms": kern}
 
 
-def evoformer_stack_config4(ctx, D, synthetic, reps):
+def evoformer_stack_config4(ctx, D, synthetic, reps, storage="f32"):
     """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
-    pass (1 recycle), 48 distinct int8 weight sets, bf16 activations, through lf_evoformer_stack."""
+    pass (1 recycle), 48 distinct int8 weight sets, bf16 inputs, the residual stream stored in
+    `storage`, through lf_evoformer_stack."""
     import torch
     c4 = synthetic.config4_inputs()
     dev = ctx.device
@@ -276,8 +320,9 @@ def evoformer_stack_config4(ctx, D, synthetic, reps):
     weights = [c4["weights"]] + [synthetic.quantise_tree(synthetic.config1_inputs(seed=100 + k, n=1)[0], "int8", 64)
                                  for k in range(47)]
     ws = [D.evoformer_weights(dw, w) for w in weights]
-    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16)
-    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16)
+    sdt = torch.float32 if storage == "f32" else torch.bfloat16
+    msa = torch.as_tensor(c4["msa"]).to(dev).to(torch.bfloat16).to(sdt)
+    pair = torch.as_tensor(c4["pair"]).to(dev).to(torch.bfloat16).to(sdt)
     mm = torch.as_tensor(c4["msa_mask"]).to(dev)
     pm = torch.as_tensor(c4["pair_mask"]).to(dev)
     msa0, pair0 = msa.clone(), pair.clone()
@@ -294,13 +339,13 @@ def evoformer_stack_config4(ctx, D, synthetic, reps):
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     gflop = 48 * 1076.5
     return {"workload": f"BASELINE config 4, the 48-block AF2 Evoformer stack: N_res={n}, N_seq={s_}, c_m=256, "
-                        "c_z=128, 48 distinct int8 weight sets (fp16 scales, groups of 64), bf16 activations, "
-                        "one pass; time includes restoring the inputs (2 device copies, 138 MB)",
+                        f"c_z=128, 48 distinct int8 weight sets (fp16 scales, groups of 64), bf16 inputs, {storage} "
+                        "residual stream, one pass; time includes restoring the inputs (2 device copies)",
             "ms_per_stack": round(ms, 2), "ms_per_block": round(ms / 48, 3),
             "tflops": round(gflop / ms, 1), "algorithmic_gflop": gflop, "outputs_finite": finite}
 
 
-def pairformer_block_config5(ctx, D, synthetic, reps):
+def pairformer_block_config5(ctx, D, synthetic, reps, storage="f32"):
     """BASELINE config 5 at one block: an AF3 Pairformer block at N_tokens=1024, c_z=128,
     c_s=384, int5 weights (fp16 scale and zero, groups of 32), bf16 activations, the last 32
     tokens padded."""
@@ -309,8 +354,9 @@ def pairformer_block_config5(ctx, D, synthetic, reps):
     w = synthetic.quantise_tree(synthetic.synthetic_pairformer_weights(cz, cs, 4, 16, 24, seed=21), "int5", 32)
     st = synthetic.Stream(22)
     dev = ctx.device
-    pair = torch.as_tensor(st.normal(n * n * cz).reshape(n, n, cz)).to(dev).to(torch.bfloat16)
-    single = torch.as_tensor(st.normal(n * cs).reshape(n, cs)).to(dev).to(torch.bfloat16)
+    sdt = torch.float32 if storage == "f32" else torch.bfloat16
+    pair = torch.as_tensor(st.normal(n * n * cz).reshape(n, n, cz)).to(dev).to(torch.bfloat16).to(sdt)
+    single = torch.as_tensor(st.normal(n * cs).reshape(n, cs)).to(dev).to(torch.bfloat16).to(sdt)
     seq_mask = np.ones(n, np.float32)
     seq_mask[-32:] = 0
     sm = torch.as_tensor(seq_mask).to(dev)
@@ -331,7 +377,7 @@ def pairformer_block_config5(ctx, D, synthetic, reps):
     gflop = 2692.0
     return {"workload": f"BASELINE config 5, one AF3 Pairformer block: N_tokens={n}, c_z={cz}, c_s={cs}, "
                         "triangle attention 4x32, single attention 16x24, int5 weights (groups of 32), bf16 "
-                        "activations, last 32 tokens padded",
+                        f"inputs, {storage} residual stream, last 32 tokens padded",
             "ms_per_block": round(ms, 3), "stack_48_blocks_s_estimate": round(48 * ms / 1e3, 3),
             "tflops": round(gflop / ms, 1), "algorithmic_gflop": gflop, "outputs_finite": finite, "kernels_ms": kern}
 
@@ -343,6 +389,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config 3 / 4 / 5 measurements")
+    ap.add_argument("--only", choices=["tri", "attn", "evoblock", "evoblock-bf16", "stack", "pairformer",
+                                       "extra", "msa", "embed"],
+                    help="run one workload (a few calls), print its JSON and exit: the command the "
+                         "rocprofv3 summaries under profiles/ are taken over")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy 5 times (the reference "
                          "reading for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -366,6 +416,18 @@ def main():
 
     ctx = D.Context(0)
     dev = ctx.device
+    if args.only and args.only != "tri":
+        fn = {"attn": lambda: triangle_attention_config3(ctx, D, synthetic, 3),
+              "evoblock": lambda: evoformer_block_config4(ctx, D, synthetic, 3),
+              "evoblock-bf16": lambda: evoformer_block_config4(ctx, D, synthetic, 3, "bf16"),
+              "stack": lambda: evoformer_stack_config4(ctx, D, synthetic, 1),
+              "pairformer": lambda: pairformer_block_config5(ctx, D, synthetic, 3),
+              "extra": lambda: extra_msa_block_n384(ctx, D, synthetic, 3),
+              "msa": lambda: msa_module_block_n384(ctx, D, synthetic, 3),
+              "embed": lambda: input_embedder_n384(ctx, D, synthetic, 3)}[args.only]
+        print(json.dumps({"only": args.only, **fn()}), flush=True)
+        ctx.close()
+        return
     log("generating config-2 inputs ...")
     c2 = synthetic.config2_inputs(N, CZ, seed=2, masked_tail=MASKED)
     dw = D.DeviceWeights(dev)
@@ -429,13 +491,15 @@ def main():
     roof["traffic"] = measured_traffic(dom)
 
     extras = {}
-    if not args.no_extras:
+    if not args.no_extras and not args.only:
         log("config 3: triangle attention ...")
         extras["triangle_attention"] = triangle_attention_config3(ctx, D, synthetic, 10)
         log("config 4: one Evoformer block ...")
         extras["evoformer_block"] = evoformer_block_config4(ctx, D, synthetic, 5)
+        extras["evoformer_block_bf16"] = evoformer_block_config4(ctx, D, synthetic, 5, "bf16")
         log("config 4: the 48-block stack ...")
         extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
+        extras["evoformer_stack_bf16"] = evoformer_stack_config4(ctx, D, synthetic, 2, "bf16")
         log("extra-MSA block ...")
         extras["extra_msa_block"] = extra_msa_block_n384(ctx, D, synthetic, 5)
         log("input embedder ...")
@@ -444,9 +508,10 @@ def main():
         extras["msa_module_block"] = msa_module_block_n384(ctx, D, synthetic, 5)
         log("config 5: one Pairformer block ...")
         extras["pairformer_block"] = pairformer_block_config5(ctx, D, synthetic, 5)
+        extras["pairformer_block_bf16"] = pairformer_block_config5(ctx, D, synthetic, 5, "bf16")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.only:
         log("timing the CPU oracle ...")
         cpu = cpu_baseline(c2)
 
@@ -475,6 +540,9 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "evoformer_block": extras.get("evoformer_block"),
+        "evoformer_block_bf16": extras.get("evoformer_block_bf16"),
+        "evoformer_stack_bf16": extras.get("evoformer_stack_bf16"),
+        "pairformer_block_bf16": extras.get("pairformer_block_bf16"),
         "triangle_attention": extras.get("triangle_attention"),
         "evoformer_stack": extras.get("evoformer_stack"),
         "pairformer_block": extras.get("pairformer_block"),
