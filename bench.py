@@ -106,15 +106,23 @@ TRAFFIC_KERNELS = {"project": "tri_project", "output": "tri_output", "contract":
 
 def measured_traffic(kind):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (scaled by the copy-kernel calibration recorded in the same file)."""
+    WRITE_SIZE passes (scaled by the copy-kernel calibration recorded in the same file), with
+    the profile's source: None when the triangle kernels' source no longer matches the one the
+    counters were taken over."""
+    import hashlib
     try:
         line = next(l for l in open(TRAFFIC_FILE) if l.startswith("traffic_json: "))
-        table = json.loads(line[len("traffic_json: "):])["kernels"]
+        data = json.loads(line[len("traffic_json: "):])
+        table = data["kernels"]
+        src = os.path.join(os.path.dirname(TRAFFIC_FILE), "..", "localfold_amd", "csrc", "lf_tri.hip")
+        sha = hashlib.sha256(open(src, "rb").read()).hexdigest()[:16]
+        if data.get("csrc_sha16") != sha:
+            return None, "profile predates the current lf_tri.hip"
         prefix = TRAFFIC_KERNELS.get(kind)
         vals = [v["traffic_bytes"] for k, v in table.items() if prefix and k.startswith(prefix)]
-        return int(sum(vals) / len(vals)) if vals else None
+        return (int(sum(vals) / len(vals)) if vals else None), os.path.relpath(TRAFFIC_FILE, os.path.dirname(src) + "/../..")
     except (OSError, StopIteration, ValueError, KeyError):
-        return None
+        return None, "no profile"
 
 
 def tri_attention_flops(n, c=128, heads=4, d=32):
@@ -488,7 +496,7 @@ def main():
     roof["kernel"] = f"tri_*.{dom}"
     roof["ms_per_launch"] = round(dom_ms, 4)
     roof["mfma_tflops"] = round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2)
-    roof["traffic"] = measured_traffic(dom)
+    roof["traffic"], roof["traffic_source"] = measured_traffic(dom)
 
     extras = {}
     if not args.no_extras and not args.only:
