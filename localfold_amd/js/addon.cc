@@ -11,7 +11,9 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <string>
+#include <vector>
 
 #include "../../include/localfold.h"
 
@@ -51,6 +53,68 @@ napi_value throw_lf(napi_env env, int rc, const char* what) {
   std::string m = std::string(what) + " failed (" + std::to_string(rc) + "): " + lf_last_error();
   napi_throw_error(env, nullptr, m.c_str());
   return nullptr;
+}
+
+// Long runs (the stacks, a Pairformer block) execute on a libuv worker thread through
+// napi_async_work: the JS thread gets a promise at once, the worker calls the C entry point
+// and waits for the stream, and completion (back on the JS thread) resolves the promise or
+// rejects it with the worker's lf_last_error().  The call owns copies of its argument
+// structs (plain device pointers and sizes); the JS side keeps the device buffers alive until
+// the promise settles.  The context is not to be used from JS until then.
+struct AsyncRun {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  lf_context* ctx = nullptr;
+  std::function<int(lf_context*)> fn;
+  int rc = LF_OK;
+  std::string err;
+  const char* what = "";
+};
+
+void async_execute(napi_env, void* data) {
+  AsyncRun* r = static_cast<AsyncRun*>(data);
+  r->rc = r->fn(r->ctx);
+  if (r->rc == LF_OK) r->rc = lf_synchronize(r->ctx);
+  if (r->rc != LF_OK) r->err = lf_last_error();
+}
+
+void async_complete(napi_env env, napi_status status, void* data) {
+  AsyncRun* r = static_cast<AsyncRun*>(data);
+  if (status == napi_ok && r->rc == LF_OK) {
+    napi_value u;
+    napi_get_undefined(env, &u);
+    napi_resolve_deferred(env, r->deferred, u);
+  } else {
+    const std::string m = status != napi_ok ? std::string(r->what) + ": the async work was cancelled"
+                                            : std::string(r->what) + " failed (" + std::to_string(r->rc) + "): " + r->err;
+    napi_value msg, e;
+    napi_create_string_utf8(env, m.c_str(), NAPI_AUTO_LENGTH, &msg);
+    napi_create_error(env, nullptr, msg, &e);
+    napi_reject_deferred(env, r->deferred, e);
+  }
+  napi_delete_async_work(env, r->work);
+  delete r;
+}
+
+napi_value start_async(napi_env env, lf_context* ctx, std::function<int(lf_context*)> fn, const char* what) {
+  if (!ctx) {
+    napi_throw_error(env, nullptr, "the context was destroyed");
+    return nullptr;
+  }
+  AsyncRun* r = new AsyncRun();
+  r->ctx = ctx;
+  r->fn = std::move(fn);
+  r->what = what;
+  napi_value promise, name;
+  if (napi_create_promise(env, &r->deferred, &promise) != napi_ok ||
+      napi_create_string_utf8(env, what, NAPI_AUTO_LENGTH, &name) != napi_ok ||
+      napi_create_async_work(env, nullptr, name, async_execute, async_complete, r, &r->work) != napi_ok ||
+      napi_queue_async_work(env, r->work) != napi_ok) {
+    delete r;
+    napi_throw_error(env, nullptr, "could not queue the async work");
+    return nullptr;
+  }
+  return promise;
 }
 
 void buf_finalize(napi_env, void* data, void*) {
@@ -340,9 +404,20 @@ napi_value Download(napi_env env, napi_callback_info info) {
   napi_value argv[3];
   if (!get_args(env, info, 3, argv)) return nullptr;
   lf_context* ctx = as_ctx(env, argv[0]);
+  if (!ctx) {
+    napi_throw_error(env, nullptr, "download: the context was destroyed");
+    return nullptr;
+  }
   void* p = nullptr;
-  napi_get_value_external(env, argv[1], &p);
+  if (napi_get_value_external(env, argv[1], &p) != napi_ok || p == nullptr) {
+    napi_throw_type_error(env, nullptr, "download: the second argument is not a device buffer handle");
+    return nullptr;
+  }
   DevBuf* b = static_cast<DevBuf*>(p);
+  if (b->ptr == nullptr) {
+    napi_throw_error(env, nullptr, "download: the device buffer was freed");
+    return nullptr;
+  }
   napi_typedarray_type t;
   size_t len, off;
   void* data;
@@ -629,16 +704,16 @@ napi_value EvoformerStack(napi_env env, napi_callback_info info) {
   lf_evoformer_block_args a = evo_args(env, argv[1]);
   uint32_t n = 0;
   napi_get_array_length(env, argv[2], &n);
-  lf_evoformer_weights* ws = new lf_evoformer_weights[n > 0 ? n : 1];
+  std::vector<lf_evoformer_weights> ws(n > 0 ? n : 1);
   for (uint32_t i = 0; i < n; ++i) {
     napi_value e;
     napi_get_element(env, argv[2], i, &e);
     ws[i] = evo_weights(env, e);
   }
-  int rc = lf_evoformer_stack(as_ctx(env, argv[0]), &a, ws, (int)n);
-  delete[] ws;
-  if (rc != LF_OK) return throw_lf(env, rc, "lf_evoformer_stack");
-  return undefined_value(env);
+  // returns a promise: the stack runs on a worker thread (see start_async)
+  return start_async(env, as_ctx(env, argv[0]), [a, ws, n](lf_context* c) {
+    return lf_evoformer_stack(c, &a, ws.data(), (int)n);
+  }, "lf_evoformer_stack");
 }
 
 // extraMsaStack(ctx, args, [blockWeights...]): Evoformer block weights with columnGlobal
@@ -648,7 +723,7 @@ napi_value ExtraMsaStack(napi_env env, napi_callback_info info) {
   lf_evoformer_block_args a = evo_args(env, argv[1]);
   uint32_t n = 0;
   napi_get_array_length(env, argv[2], &n);
-  lf_extra_msa_weights* ws = new lf_extra_msa_weights[n > 0 ? n : 1];
+  std::vector<lf_extra_msa_weights> ws(n > 0 ? n : 1);
   for (uint32_t i = 0; i < n; ++i) {
     napi_value e;
     napi_get_element(env, argv[2], i, &e);
@@ -656,10 +731,10 @@ napi_value ExtraMsaStack(napi_env env, napi_callback_info info) {
     ws[i].column_global = glob_weights(env, prop(env, e, "columnGlobal"));
     ws[i].column_global_heads = get_int(env, e, "columnGlobalHeads");
   }
-  int rc = lf_extra_msa_stack(as_ctx(env, argv[0]), &a, ws, (int)n);
-  delete[] ws;
-  if (rc != LF_OK) return throw_lf(env, rc, "lf_extra_msa_stack");
-  return undefined_value(env);
+  // returns a promise: the stack runs on a worker thread (see start_async)
+  return start_async(env, as_ctx(env, argv[0]), [a, ws, n](lf_context* c) {
+    return lf_extra_msa_stack(c, &a, ws.data(), (int)n);
+  }, "lf_extra_msa_stack");
 }
 
 napi_value PairformerBlock(napi_env env, napi_callback_info info) {
@@ -695,10 +770,12 @@ napi_value PairformerBlock(napi_env env, napi_callback_info info) {
   a.seq_mask = static_cast<const float*>(get_dev(env, o, "seqMask"));
   a.transition_chunk_bytes = (long long)get_num(env, o, "transitionChunkBytes", 0);
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
-  a.w = &w;
-  int rc = lf_pairformer_block(as_ctx(env, argv[0]), &a);
-  if (rc != LF_OK) return throw_lf(env, rc, "lf_pairformer_block");
-  return undefined_value(env);
+  // returns a promise: the block runs on a worker thread (see start_async)
+  return start_async(env, as_ctx(env, argv[0]), [a, w](lf_context* c) {
+    lf_pairformer_block_args args = a;
+    args.w = &w;
+    return lf_pairformer_block(c, &args);
+  }, "lf_pairformer_block");
 }
 
 // msaModuleBlock(ctx, args): one AF3 MSA-module block, weights {opm, cOuter, pwa, msaHeads,
@@ -746,10 +823,12 @@ napi_value MsaModuleBlock(napi_env env, napi_callback_info info) {
   a.pair_mask = static_cast<const float*>(get_dev(env, o, "pairMask"));
   a.transition_chunk_bytes = (long long)get_num(env, o, "transitionChunkBytes", 0);
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
-  a.w = &w;
-  int rc = lf_msa_module_block(as_ctx(env, argv[0]), &a);
-  if (rc != LF_OK) return throw_lf(env, rc, "lf_msa_module_block");
-  return undefined_value(env);
+  // returns a promise: the block runs on a worker thread (see start_async)
+  return start_async(env, as_ctx(env, argv[0]), [a, w](lf_context* c) {
+    lf_msa_block_args args = a;
+    args.w = &w;
+    return lf_msa_module_block(c, &args);
+  }, "lf_msa_module_block");
 }
 
 // inputEmbedder(ctx, args): device pointers for every feature, weight and output

@@ -500,10 +500,13 @@ function blockDims(input, w) {
   };
 }
 
-function runEvoformer(device, input, blockWeights) {
-  return new Promise(function execute(resolve) {
+// The stack runs on a libuv worker thread (the addon's call returns a promise), so the JS
+// thread stays free while the GPU works; the device buffers stay referenced until it settles.
+async function runEvoformer(device, input, blockWeights) {
+  let up = null;
+  try {
     const dims = blockDims(input, blockWeights[0]);
-    const up = new Uploads(device);
+    up = new Uploads(device);
     const start = performance.now();
     const ws = blockWeights.map(function each(w) {
       return resident(device, w, function build(wu) { return evoformerBlockWeights(wu, w, dims); });
@@ -514,7 +517,7 @@ function runEvoformer(device, input, blockWeights) {
     expectLength('pair', input.pair, pairElements);
     const msa = up.vec(input.msa);
     const pair = up.vec(input.pair);
-    device.addon.evoformerStack(device.ctx, {
+    await device.addon.evoformerStack(device.ctx, {
       sequences: input.sequences, length: input.length, cM: dims.cM, cZ: dims.cZ, cOuter: dims.cOuter,
       triangleHidden: dims.triangleHidden, msaHidden: dims.msaHidden, pairHidden: dims.pairHidden,
       msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair,
@@ -522,9 +525,11 @@ function runEvoformer(device, input, blockWeights) {
     }, ws);
     const r = finish(device, up, [{ buffer: msa, elements: msaElements }, { buffer: pair, elements: pairElements }],
       start);
-    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
-      kernels: r.kernels });
-  });
+    return { msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels };
+  } finally {
+    if (up) up.release();
+  }
 }
 
 // webgpu/af2/evoformer/block.js:1783-1824
@@ -560,13 +565,14 @@ function globalAttentionWeights(up, g, cM) {
 // Evoformer block's weights with msaColumnGlobalAttention in place of msaColumnAttention
 // (encodeExtraMsaBlock, block.js:1715-1744); returns {msa, pair, elapsedMilliseconds, memory}.
 function ExtraMsaStackGpu(device) { this.device = device; }
-ExtraMsaStackGpu.prototype.run = function run(input) {
+ExtraMsaStackGpu.prototype.run = async function run(input) {
   const device = this.device;
-  return new Promise(function execute(resolve) {
+  let up = null;
+  try {
     const blocks = input.blockWeights;
     if (!Array.isArray(blocks) || blocks.length === 0) throw new RangeError('blockWeights must be a non-empty array');
     const dims = blockDims(input, blocks[0]);
-    const up = new Uploads(device);
+    up = new Uploads(device);
     const start = performance.now();
     const ws = blocks.map(function each(w) {
       return resident(device, w, function build(wu) {
@@ -582,7 +588,7 @@ ExtraMsaStackGpu.prototype.run = function run(input) {
     expectLength('pair', input.pair, pairElements);
     const msa = up.vec(input.msa);
     const pair = up.vec(input.pair);
-    device.addon.extraMsaStack(device.ctx, {
+    await device.addon.extraMsaStack(device.ctx, {
       sequences: input.sequences, length: input.length, cM: dims.cM, cZ: dims.cZ, cOuter: dims.cOuter,
       triangleHidden: dims.triangleHidden, msaHidden: dims.msaHidden, pairHidden: dims.pairHidden,
       msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair,
@@ -590,9 +596,11 @@ ExtraMsaStackGpu.prototype.run = function run(input) {
     }, ws);
     const r = finish(device, up, [{ buffer: msa, elements: msaElements }, { buffer: pair, elements: pairElements }],
       start);
-    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
-      kernels: r.kernels });
-  });
+    return { msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels };
+  } finally {
+    if (up) up.release();
+  }
 };
 
 // ---- AF3 pairformer stack ------------------------------------------------------------
@@ -657,10 +665,11 @@ function Af3PairformerStackGpu(device, options) {
   this.device = device;
   this.options = options || {};
 }
-Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, options) {
+Af3PairformerStackGpu.prototype.run = async function run(state, blocks, dialect, options) {
   const dev = this.device;
   const opts = options || {};
-  return new Promise(function execute(resolve) {
+  let up = null;
+  try {
     if (!dialect || typeof dialect.swapTransposedBias !== 'boolean') {
       throw new Error('dialect.swapTransposedBias has no default');
     }
@@ -674,7 +683,7 @@ Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, optio
     if (opts.variance !== undefined && opts.variance !== 'fast') {
       throw new RangeError('the pairformer runs the reference\'s fast variance; received ' + opts.variance);
     }
-    const up = new Uploads(dev);
+    up = new Uploads(dev);
     const start = performance.now();
     const pair = up.vec(state.pair);
     const single = state.single ? up.vec(state.single) : null;
@@ -683,7 +692,7 @@ Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, optio
     for (let b = 0; b < blocks.length; b += 1) {
       if (opts.onBlock) opts.onBlock(b);
       const w = resident(dev, blocks[b], function build(wu) { return pairformerBlockWeights(wu, blocks[b], cZ, cS); });
-      dev.addon.pairformerBlock(dev.ctx, {
+      await dev.addon.pairformerBlock(dev.ctx, {
         tokens: n, cZ: cZ, cS: cS, swapTransposedBias: dialect.swapTransposedBias ? 1 : 0,
         divideByLength: dialect.divideByLength ? 1 : 0, pairDtype: ACT.float32, pair: pair,
         singleDtype: ACT.float32, single: single, pairMask: pairMask, seqMask: seqMask,
@@ -694,9 +703,11 @@ Af3PairformerStackGpu.prototype.run = function run(state, blocks, dialect, optio
     const outs = [{ buffer: pair, elements: n * n * cZ }];
     if (single) outs.push({ buffer: single, elements: n * cS });
     const r = finish(dev, up, outs, start);
-    resolve({ pair: r.results[0], single: single ? r.results[1] : null, elapsedMilliseconds: r.elapsedMilliseconds,
-      memory: r.memory, kernels: r.kernels });
-  });
+    return { pair: r.results[0], single: single ? r.results[1] : null, elapsedMilliseconds: r.elapsedMilliseconds,
+      memory: r.memory, kernels: r.kernels };
+  } finally {
+    if (up) up.release();
+  }
 };
 
 // ---- AF3 MSA module ---------------------------------------------------------------------
@@ -739,10 +750,11 @@ function Af3MsaStackGpu(device, options) {
   this.device = device;
   this.options = options || {};
 }
-Af3MsaStackGpu.prototype.run = function run(state, blocks, dialect, options) {
+Af3MsaStackGpu.prototype.run = async function run(state, blocks, dialect, options) {
   const dev = this.device;
   const opts = options || {};
-  return new Promise(function execute(resolve) {
+  let up = null;
+  try {
     if (!dialect || dialect.msaUpdateBeforeOuterProduct === undefined) {
       throw new Error('dialect.msaUpdateBeforeOuterProduct has no default: AF3 takes the outer product off the '
         + 'pre-update MSA and OpenDDE off the updated one');
@@ -761,7 +773,7 @@ Af3MsaStackGpu.prototype.run = function run(state, blocks, dialect, options) {
     if (opts.variance !== undefined && opts.variance !== 'fast') {
       throw new RangeError('the MSA stack runs the reference\'s fast variance; received ' + opts.variance);
     }
-    const up = new Uploads(dev);
+    up = new Uploads(dev);
     const start = performance.now();
     const msa = up.vec(state.msa);
     const pair = up.vec(state.pair);
@@ -770,7 +782,7 @@ Af3MsaStackGpu.prototype.run = function run(state, blocks, dialect, options) {
     for (let b = 0; b < blocks.length; b += 1) {
       if (opts.onBlock) opts.onBlock(b);
       const w = resident(dev, blocks[b], function build(wu) { return msaModuleBlockWeights(wu, blocks[b], cM, cZ); });
-      dev.addon.msaModuleBlock(dev.ctx, {
+      await dev.addon.msaModuleBlock(dev.ctx, {
         sequences: state.sequences, tokens: n, cM: cM, cZ: cZ,
         msaUpdateBeforeOuterProduct: dialect.msaUpdateBeforeOuterProduct ? 1 : 0,
         swapTransposedBias: dialect.swapTransposedBias ? 1 : 0, divideByLength: dialect.divideByLength ? 1 : 0,
@@ -779,9 +791,11 @@ Af3MsaStackGpu.prototype.run = function run(state, blocks, dialect, options) {
       });
     }
     const r = finish(dev, up, [{ buffer: msa, elements: rows * cM }, { buffer: pair, elements: n * n * cZ }], start);
-    resolve({ msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
-      kernels: r.kernels });
-  });
+    return { msa: r.results[0], pair: r.results[1], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory,
+      kernels: r.kernels };
+  } finally {
+    if (up) up.release();
+  }
 };
 
 // ---- AF2 input embedder ------------------------------------------------------------------

@@ -17,8 +17,11 @@ function f32(name) {
   return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
 }
 
+// mean and max absolute bounds per case, and the north-star relative Frobenius bound on all
+const REL_FRO = 5e-3;
 function report(name, metrics, bounds) {
-  const ok = metrics.meanAbsoluteError < bounds.mean && metrics.maxAbsoluteError < bounds.max;
+  const ok = metrics.meanAbsoluteError < bounds.mean && metrics.maxAbsoluteError < bounds.max
+    && metrics.relativeFrobenius <= (bounds.relFro || REL_FRO);
   if (!ok) failures += 1;
   console.log((ok ? 'ok   ' : 'FAIL ') + name + ' ' + JSON.stringify(metrics));
 }
