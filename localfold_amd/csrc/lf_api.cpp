@@ -63,6 +63,28 @@ LaunchScope::~LaunchScope() {
   if (idx >= 0) hipEventRecord(ctx->recs[idx].stop, ctx->stream);
 }
 
+// How the kernels fetch the view: in runs of 8 adjacent stored weights when the run's first
+// flat index is a multiple of 8 (so an int5 run is 5 whole bytes and a flat group, a
+// power-of-two multiple of 8, holds the whole run), the data pointer is aligned for the run's
+// vector load and flat and int5 bit offsets fit 32 bits; per-column groups need the run along
+// k (one column, one scale).  Otherwise weight by weight.
+static int weight_run(WView& v, long long elements) {
+  static const int align[] = {16, 16, 16, 8, 4};   // f32 (two 16-byte loads), f16, bf16, int8, int5
+  if (elements >= (1LL << 28)) return WRUN_GATHER;
+  if ((reinterpret_cast<uintptr_t>(v.data) & (uintptr_t)(align[v.dtype] - 1)) != 0) return WRUN_GATHER;
+  const bool quant = v.dtype == LF_INT8 || v.dtype == LF_INT5;
+  v.gshift = 0;
+  if (quant && v.group > 0) {
+    if (v.group % 8 != 0 || (v.group & (v.group - 1)) != 0) return WRUN_GATHER;
+    while ((1 << v.gshift) < v.group) ++v.gshift;
+  }
+  if (v.ld_k == 1 && v.K % 8 == 0 && v.ld_n % 8 == 0) return WRUN_K;
+  if (v.ld_n == 1 && v.col_stride == 1 && v.col_off % 8 == 0 && v.N % 8 == 0 && v.ld_k % 8 == 0 &&
+      !(quant && v.group == 0))
+    return WRUN_N;
+  return WRUN_GATHER;
+}
+
 int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, int col_off, int col_stride,
               bool subset) {
   const std::string nm(name);
@@ -108,6 +130,7 @@ int make_view(const lf_weight& w, int K, int N, const char* name, WView* out, in
     default:
       return set_error(LF_ERR_INVALID, nm + ": unknown dtype " + std::to_string(w.dtype));
   }
+  v.run = weight_run(v, (long long)w.rows * w.cols);
   *out = v;
   return LF_OK;
 }

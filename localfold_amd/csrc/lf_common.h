@@ -68,7 +68,15 @@ struct WView {
   int ld_k, ld_n;
   int col_off, col_stride;
   int K, N;
+  // How the kernels fetch and decode the weights themselves, 8 at a time (set by make_view):
+  // WRUN_K when 8 consecutive k of one column are adjacent in storage ((out,in) layout), WRUN_N
+  // when 8 consecutive columns of one k are ((in,out) layout) -- one vector load of codes and
+  // one scale per run -- and WRUN_GATHER, element by element, when neither holds with the
+  // alignment the vector loads need (interleaved columns, widths not a multiple of 8).
+  int run;
+  int gshift;               // log2(group) for flat groups (a power of two, multiple of 8)
 };
+enum { WRUN_GATHER = 0, WRUN_K = 1, WRUN_N = 2 };
 
 __device__ __forceinline__ float wdecode(const WView& w, int k, int n) {
   if (k >= w.K || n >= w.N) return 0.f;

@@ -1,5 +1,6 @@
-// Shared MFMA tile machinery: weight staging (in-kernel dequant into LDS) and the
-// 16-row x (16*NT)-column wave tile over an LDS-resident A block.
+// Shared MFMA tile machinery: weight staging into LDS (from an f16 expansion, or decoded from
+// the stored codes inside the kernel) and the 16-row x (16*NT)-column wave tile over an
+// LDS-resident A block.
 //
 // LDS layouts (f16, row stride padded by 8 halves so the 16-byte fragment reads of 16
 // consecutive rows land in different banks):
@@ -33,32 +34,157 @@ struct ExpandBatch {
   int count;
 };
 
-// Ws[n][k] = E[n_base + n][k] for n < ncols, k < e.kp (zero past the valid columns).
-__device__ __forceinline__ void stage_expanded(_Float16* Ws, int ldw, const WExp& e, int ncols, int n_base, int tid,
-                                               int nthreads) {
-  const int segs = e.kp >> 3;
-  const int total = ncols * segs;
-  for (int i = tid; i < total; i += nthreads) {
-    const int n = i / segs, seg = i - n * segs;
-    h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (n_base + n < e.N) v = *reinterpret_cast<const h8*>(e.p + (size_t)(n_base + n) * e.kp + seg * 8);
-    *reinterpret_cast<h8*>(Ws + n * ldw + seg * 8) = v;
+// ---- in-kernel dequantisation ----------------------------------------------------------
+// A run is 8 stored weights adjacent in memory (WView::run): k..k+7 of column n (WRUN_K) or
+// columns n..n+7 at k (WRUN_N).  wrun_fetch issues its loads -- codes and the group's scale
+// and zero exactly as stored, no arithmetic on them, so a prefetch never waits -- and
+// wrun_decode turns the words into 8 f16 values when they are written to LDS.  The decode is
+// the reference's readTensorRange arithmetic (shared/weights/dtype.js:212-406): int8
+// code * scale, int5 fma(code, scale, zero) with codes LSB-first at bit 5i, in f32, times
+// `mul`, rounded once to f16.  f32 weights are converted at fetch (they are not a codec).
+// Coordinates outside the view are clamped for the fetch and decode to zeros.
+struct WRunAt {
+  int flat;   // flat index of the run's first stored weight (clamped)
+  int grp;    // its group (scale / zero index)
+  bool ok;    // inside the view
+};
+
+__device__ __forceinline__ WRunAt wrun_at(const WView& w, int k, int n) {
+  WRunAt r;
+  r.ok = k < w.K && n < w.N;
+  const int kc = k < w.K ? k : 0, nc = n < w.N ? n : 0;
+  const int np = w.col_off + nc * w.col_stride;
+  r.flat = kc * w.ld_k + np * w.ld_n;
+  r.grp = w.group > 0 ? r.flat >> w.gshift : np;
+  return r;
+}
+
+// Views without runs (interleaved columns, tiny or unaligned matrices): the 8 weights
+// k..k+7 of column n decoded one by one at fetch (out of line: rare, and it keeps the
+// generic decoder's code out of the kernels' loops).
+__device__ __noinline__ u32x4 wrun_gather(WView w, int k, int n, float mul) {
+  h8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * wdecode(w, k + j, n));
+  u32x4 v;
+  __builtin_memcpy(&v, &h, 16);
+  return v;
+}
+
+// GATHER = false: the caller guarantees w.run != WRUN_GATHER (kernels are instantiated
+// without the out-of-line call, which costs registers even where it is never taken).
+template <bool GATHER = true>
+__device__ __forceinline__ u32x4 wrun_fetch(const WView& w, int k, int n, float mul) {
+  if (GATHER && w.run == WRUN_GATHER) return wrun_gather(w, k, n, mul);
+  const WRunAt r = wrun_at(w, k, n);
+  u32x4 v;
+  switch (w.dtype) {
+    case DT_F32: {
+      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(w.data) + r.flat);
+      const float4 a = src[0], b = src[1];
+      h8 h;
+      h[0] = (_Float16)(mul * a.x); h[1] = (_Float16)(mul * a.y); h[2] = (_Float16)(mul * a.z); h[3] = (_Float16)(mul * a.w);
+      h[4] = (_Float16)(mul * b.x); h[5] = (_Float16)(mul * b.y); h[6] = (_Float16)(mul * b.z); h[7] = (_Float16)(mul * b.w);
+      __builtin_memcpy(&v, &h, 16);
+      break;
+    }
+    case DT_F16:
+    case DT_BF16:
+      v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w.data) + r.flat);
+      break;
+    case DT_I8: {
+      const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w.data) + r.flat);
+      v = u32x4{c.x, c.y, (uint32_t)w.scales[r.grp], 0u};
+      break;
+    }
+    default: {   // int5: the run is the 5 bytes at 5 * flat / 8, inside two aligned words
+      const uint8_t* b = static_cast<const uint8_t*>(w.data) + (((r.flat >> 3) * 5) & ~3);
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(b);
+      v = u32x4{q[0], q[1], (uint32_t)w.scales[r.grp], (uint32_t)w.zeros[r.grp]};
+    }
+  }
+  return v;
+}
+
+template <bool GATHER = true>
+__device__ __forceinline__ h8 wrun_decode(const WView& w, const u32x4& v, int k, int n, float mul) {
+  const WRunAt r = wrun_at(w, k, n);
+  h8 h;
+  switch (GATHER && w.run == WRUN_GATHER ? DT_F32 : w.dtype) {
+    case DT_F32:   // converted at fetch (f32 storage, or a gathered run)
+      __builtin_memcpy(&h, &v, 16);
+      break;
+    case DT_F16: {
+      __builtin_memcpy(&h, &v, 16);
+      if (mul != 1.f) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * (float)h[j]);
+      }
+      break;
+    }
+    case DT_BF16: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t word = v[j >> 1];
+        h[j] = (_Float16)(mul * __uint_as_float((j & 1) ? (word & 0xffff0000u) : (word << 16)));
+      }
+      break;
+    }
+    case DT_I8: {
+      const float sc = h2f((uint16_t)v.z);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int code = (int)(int8_t)(((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu);
+        h[j] = (_Float16)(mul * ((float)code * sc));
+      }
+      break;
+    }
+    default: {
+      const float sc = h2f((uint16_t)v.z), zp = h2f((uint16_t)v.w);
+      const int sh = (((r.flat >> 3) * 5) & 3) * 8;
+      const uint64_t x = (((uint64_t)v.y << 32) | v.x) >> sh;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * fmaf((float)((uint32_t)(x >> (5 * j)) & 31u), sc, zp));
+    }
+  }
+  if (!r.ok) h = h8{0, 0, 0, 0, 0, 0, 0, 0};
+  return h;
+}
+
+// Writes a decoded run to Ws[n][k] (pitch ldw halves): one 16-byte store for a run along k
+// at (n, k..k+7), eight 2-byte stores down the rows for a run along n at (n..n+7, k).
+__device__ __forceinline__ void wrun_put(_Float16* Ws, int ldw, bool krun, int n, int k, const h8& h) {
+  if (krun) {
+    *reinterpret_cast<h8*>(Ws + n * ldw + k) = h;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Ws[(n + j) * ldw + k] = h[j];
   }
 }
 
-// Ws[n][k] = W[k][n_base + n] for n < ncols, k < kpad (zero outside the view).
-__device__ __forceinline__ void stage_weights(_Float16* Ws, int ldw, const WView& w, int ncols, int n_base,
-                                              int kpad, int tid, int nthreads) {
-  const int total = ncols * kpad;
-  if (w.ld_k == 1) {
-    for (int e = tid; e < total; e += nthreads) {
-      const int n = e / kpad, k = e - n * kpad;
-      Ws[n * ldw + k] = (_Float16)wdecode(w, k, n_base + n);
+// Ws[n][k] = mul * W[k][n_base + n] for n < ncols, k < kpad (zeros outside the view), decoded
+// from the stored runs; ncols and kpad multiples of 8.  Runs are taken four at a time so their
+// loads overlap.
+__device__ __forceinline__ void stage_view(_Float16* Ws, int ldw, const WView& w, int ncols, int n_base, int kpad,
+                                           float mul, int tid, int nthreads) {
+  const bool krun = w.run != WRUN_N;
+  const int runs = ncols * kpad / 8;
+  const int per = krun ? kpad >> 3 : kpad;   // runs per LDS row (krun) or per 8-row band
+  for (int i0 = tid; i0 < runs; i0 += 4 * nthreads) {
+    u32x4 v[4];
+    int nn[4], kk[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + u * nthreads, runs - 1);
+      const int q = i / per, m = i - q * per;
+      nn[u] = krun ? q : 8 * q;
+      kk[u] = krun ? 8 * m : m;
+      v[u] = wrun_fetch(w, kk[u], n_base + nn[u], mul);
     }
-  } else {
-    for (int e = tid; e < total; e += nthreads) {
-      const int k = e / ncols, n = e - k * ncols;
-      Ws[n * ldw + k] = (_Float16)wdecode(w, k, n_base + n);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i0 + u * nthreads < runs)
+        wrun_put(Ws, ldw, krun, nn[u], kk[u], wrun_decode(w, v[u], kk[u], n_base + nn[u], mul));
     }
   }
 }

@@ -31,6 +31,22 @@
 
 namespace lf {
 
+// A weight operand of the triangle kernels: the stored view, decoded inside the kernels as
+// they stage it into LDS, the factor applied to the decoded values before the f16 rounding,
+// and kp = K rounded up to 32 (the k extent staged).
+struct WSrc {
+  WView v;
+  float mul;
+  int kp;
+};
+
+inline WSrc wsrc(const WView& v, float mul = 1.f) { return WSrc{v, mul, (v.K + 31) & ~31}; }
+
+__device__ __forceinline__ void stage_src(_Float16* Ws, int ldw, const WSrc& s, int ncols, int n_base, int tid,
+                                          int nthreads) {
+  stage_view(Ws, ldw, s.v, ncols, n_base, s.kp, s.mul, tid, nthreads);
+}
+
 struct TriProjectParams {
   const void* z;
   const float* mask;
@@ -38,11 +54,13 @@ struct TriProjectParams {
   float eps;
   int fast_var;
   int P, C, H;         // pairs, cZ, cHidden
-  WExp wp[2], wg[2];   // [0] -> a, [1] -> b
+  WSrc wp[2], wg[2];   // [0] -> a, [1] -> b
   const float *bp[2], *bg[2];
   _Float16* out[2];    // a, b: [H][P]
   int N;               // length (P = N * N)
   int kmajor_out;      // store each channel plane transposed: a[h][j][k] for pair (k, j)
+  int split;           // AF3 in the resident kernels: wp[0] / wg[0] are the whole interleaved
+                       // tensors (even stored columns -> a, odd -> b); wp[1] / wg[1] unused
 };
 
 struct TriOutputParams {
@@ -54,7 +72,7 @@ struct TriOutputParams {
   float eps, eps_x;    // eps_x: centre-norm epsilon on the stored (scaled) X
   int fast_var;
   int P, C, H;
-  WExp wz, wg;
+  WSrc wz, wg;
   const float *bz, *bg;
 };
 
@@ -87,11 +105,11 @@ __global__ __launch_bounds__(256) void tri_project_kernel(TriProjectParams p) {
   const int hchunks = (p.H + PJ_COLS - 1) / PJ_COLS;
   for (int chunk = 0; chunk < 2 * hchunks; ++chunk) {
     const int which = chunk / hchunks, h0 = (chunk % hchunks) * PJ_COLS;
-    const WExp wpe = which ? p.wp[1] : p.wp[0];
-    const WExp wge = which ? p.wg[1] : p.wg[0];
+    const WSrc& wpe = which ? p.wp[1] : p.wp[0];
+    const WSrc& wge = which ? p.wg[1] : p.wg[0];
     __syncthreads();  // As ready / previous chunk done with Ws, Os
-    stage_expanded(Ws, LDW, wpe, PJ_COLS, h0, tid, 256);
-    stage_expanded(Ws + PJ_COLS * LDW, LDW, wge, PJ_COLS, h0, tid, 256);
+    stage_src(Ws, LDW, wpe, PJ_COLS, h0, tid, 256);
+    stage_src(Ws + PJ_COLS * LDW, LDW, wge, PJ_COLS, h0, tid, 256);
     __syncthreads();
     f4 acc[1][4];
     zero_acc(acc);
@@ -168,8 +186,8 @@ __global__ __launch_bounds__(256) void tri_output_kernel(TriOutputParams p) {
   T* out = static_cast<T*>(p.out);
   for (int c0 = 0; c0 < p.C; c0 += OT_COLS) {
     __syncthreads();
-    stage_expanded(Wzs, LDX, p.wz, OT_COLS, c0, tid, 256);
-    stage_expanded(Wgs, LDZ, p.wg, OT_COLS, c0, tid, 256);
+    stage_src(Wzs, LDX, p.wz, OT_COLS, c0, tid, 256);
+    stage_src(Wgs, LDZ, p.wg, OT_COLS, c0, tid, 256);
     __syncthreads();
     f4 az[1][4], ag[1][4];
     zero_acc(az);
@@ -378,13 +396,65 @@ constexpr int RS_LD = 136;
 
 // 128 + 8 halves: 16-byte fragment reads of 16 rows hit distinct banks
 
-__device__ __forceinline__ void stage_resident(_Float16* W, const WExp& e, int tid, int nthreads) {
-  const int segs = e.kp >> 3;
-  for (int i = tid; i < 128 * 16; i += nthreads) {
-    const int n = i >> 4, seg = i & 15;
-    h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (n < e.N && seg < segs) v = *reinterpret_cast<const h8*>(e.p + (size_t)n * e.kp + seg * 8);
-    *reinterpret_cast<h8*>(W + n * RS_LD + seg * 8) = v;
+// The weights of a resident kernel: COUNT matrices of up to 128 x 128 (k, n < 128) into dst[m]
+// as [n][k] rows of pitch RS_LD, decoded from the stored codes.  SPLIT: each view is an AF3
+// interleaved tensor of 256 stored columns, column c going to row c / 2 of dst[m] (c even) or
+// of dst2[m] (c odd).  Every run's loads are issued before the first decode, so the whole
+// stage waits for memory once.
+template <int COUNT, int NT, bool SPLIT = false>
+__device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], const WSrc* const (&src)[COUNT],
+                                               int tid, _Float16* const (&dst2)[COUNT] = {}) {
+  constexpr int COLS = SPLIT ? 256 : 128, RUNS = COLS * 128 / 8, PER = (RUNS + NT - 1) / NT;
+  auto coords = [&](bool krun, int i, int& n, int& k) {
+    if (krun) { n = i >> 4; k = (i & 15) * 8; }
+    else { n = (i >> 7) * 8; k = i & 127; }
+  };
+  u32x4 v[COUNT][PER];
+#pragma unroll
+  for (int m = 0; m < COUNT; ++m) {
+    const bool krun = src[m]->v.run != WRUN_N;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      int n, k;
+      coords(krun, min(tid + u * NT, RUNS - 1), n, k);
+      v[m][u] = wrun_fetch(src[m]->v, k, n, src[m]->mul);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < COUNT; ++m) {
+    const bool krun = src[m]->v.run != WRUN_N;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      if (tid + u * NT >= RUNS) continue;
+      int n, k;
+      coords(krun, tid + u * NT, n, k);
+      const h8 h = wrun_decode(src[m]->v, v[m][u], k, n, src[m]->mul);
+      if (!SPLIT) {
+        wrun_put(dst[m], RS_LD, krun, n, k, h);
+      } else if (krun) {
+        *reinterpret_cast<h8*>(((n & 1) ? dst2[m] : dst[m]) + (n >> 1) * RS_LD + k) = h;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ((j & 1) ? dst2[m] : dst[m])[((n + j) >> 1) * RS_LD + k] = h[j];
+      }
+    }
+  }
+}
+
+// The a/b projection and gate weights of the project kernels: blocks [a-proj, a-gate, b-proj,
+// b-gate] of 128 rows from Ws.  AF3 (p.split): wp[0] and wg[0] are the whole interleaved
+// projection and gate tensors.
+template <int NT>
+__device__ __forceinline__ void stage_project_weights(_Float16* Ws, const TriProjectParams& p, int tid) {
+  if (p.split) {
+    _Float16* const even[2] = {Ws, Ws + 128 * RS_LD};
+    _Float16* const odd[2] = {Ws + 2 * 128 * RS_LD, Ws + 3 * 128 * RS_LD};
+    const WSrc* const src[2] = {&p.wp[0], &p.wg[0]};
+    stage_resident<2, NT, true>(even, src, tid, odd);
+  } else {
+    _Float16* const dst[4] = {Ws, Ws + 128 * RS_LD, Ws + 2 * 128 * RS_LD, Ws + 3 * 128 * RS_LD};
+    const WSrc* const src[4] = {&p.wp[0], &p.wg[0], &p.wp[1], &p.wg[1]};
+    stage_resident<4, NT>(dst, src, tid);
   }
 }
 
@@ -399,10 +469,7 @@ __global__ __launch_bounds__(512) void tri_project_resident_kernel(TriProjectPar
   __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors
   __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  stage_resident(Ws, p.wp[0], tid, 512);
-  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, 512);
-  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, 512);
-  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, 512);
+  stage_project_weights<512>(Ws, p, tid);
   stage_vec(Bs, p.bp[0], p.H, 0.f, 128, tid, 512);
   stage_vec(Bs + 128, p.bg[0], p.H, 0.f, 128, tid, 512);
   stage_vec(Bs + 256, p.bp[1], p.H, 0.f, 128, tid, 512);
@@ -500,8 +567,11 @@ __global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParam
   __shared__ __attribute__((aligned(16))) float Scr[OR_WAVES * OR_SCR];
   __shared__ __attribute__((aligned(16))) float Vs[6 * 128];           // bz, bg, centre-norm scale/offset, LN_in scale/offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  stage_resident(Wz, p.wz, tid, 512);
-  stage_resident(Wg, p.wg, tid, 512);
+  {
+    _Float16* const dst[2] = {Wz, Wg};
+    const WSrc* const src[2] = {&p.wz, &p.wg};
+    stage_resident<2, 512>(dst, src, tid);
+  }
   stage_vec(Vs, p.bz, p.C, 0.f, 128, tid, 512);
   stage_vec(Vs + 128, p.bg, p.C, 0.f, 128, tid, 512);
   stage_vec(Vs + 256, p.ln_out_s, p.H, 1.f, 128, tid, 512);
@@ -678,10 +748,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
   __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
   __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  stage_resident(Ws, p.wp[0], tid, NT);
-  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, NT);
-  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, NT);
-  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, NT);
+  stage_project_weights<NT>(Ws, p, tid);
   for (int i = tid; i < 128; i += NT) {
     Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
     Bs[128 + i] = p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f;
@@ -800,10 +867,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
   __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  stage_resident(Ws, p.wp[0], tid, NT);
-  stage_resident(Ws + 128 * RS_LD, p.wg[0], tid, NT);
-  stage_resident(Ws + 2 * 128 * RS_LD, p.wp[1], tid, NT);
-  stage_resident(Ws + 3 * 128 * RS_LD, p.wg[1], tid, NT);
+  stage_project_weights<NT>(Ws, p, tid);
   for (int i = tid; i < 128; i += NT) {
     Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
     Bs[128 + i] = p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f;
@@ -939,8 +1003,11 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][2][16 * O2_LD];
   __shared__ __attribute__((aligned(16))) float Vs[6 * 128];         // bz, bg', centre-norm s/o, LN_in s/o
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  stage_resident(Wz, p.wz, tid, NT);
-  stage_resident(Wg, p.wg, tid, NT);
+  {
+    _Float16* const dst[2] = {Wz, Wg};
+    const WSrc* const src[2] = {&p.wz, &p.wg};
+    stage_resident<2, NT>(dst, src, tid);
+  }
   for (int i = tid; i < 128; i += NT) {
     Vs[i] = p.bz ? p.bz[i] : 0.f;
     Vs[128 + i] = p.bg ? TRI_NLOG2E * p.bg[i] : 0.f;
@@ -1182,12 +1249,11 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
   LF_TRY(make_view(w.wg, C, C, "linearGWeight", &views[5]));
 
   const size_t plane = (size_t)H * P * sizeof(_Float16);
-  size_t sizes[9] = {plane, plane, plane};
-  for (int i = 0; i < 6; ++i) sizes[3 + i] = expanded_bytes(views[i]);
-  void* bufs[9];
+  size_t sizes[3] = {plane, plane, plane};
+  void* bufs[3];
   if (scratch) {
     size_t total = 0;
-    for (int i = 0; i < 9; ++i) {
+    for (int i = 0; i < 3; ++i) {
       bufs[i] = static_cast<char*>(scratch) + total;
       total += (sizes[i] + 255) & ~size_t(255);
     }
@@ -1197,20 +1263,18 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
                                            " bytes of scratch; the static scratch holds " +
                                            std::to_string(scratch_cap));
   } else {
-    LF_TRY(workspace(ctx, sizes, bufs, 9));
+    LF_TRY(workspace(ctx, sizes, bufs, 3));
   }
   pp.out[0] = static_cast<_Float16*>(bufs[0]);
   pp.out[1] = static_cast<_Float16*>(bufs[1]);
   _Float16* X = static_cast<_Float16*>(bufs[2]);
-  WExp ex[6];
+  WSrc ex[6];
   // the 128-wide project kernel takes its gate weights pre-multiplied by -log2(e)
   const bool v2 = C == 128 && H == 128 && N >= 16;
   // incoming: the 128-wide project kernel stores a and b transposed per channel
   pp.kmajor_out = v2 && a.direction != LF_OUTGOING;
   const float gate = v2 ? TRI_NLOG2E : 1.f;
-  const float scales[6] = {1.f, gate, 1.f, gate, 1.f, gate};
-  LF_TRY(expand_weights(ctx, views, 6, bufs + 3, ex,
-                        a.direction == LF_OUTGOING ? "tri_out.expand" : "tri_in.expand", scales));
+  for (int i = 0; i < 6; ++i) ex[i] = wsrc(views[i], i % 2 ? gate : 1.f);
   pp.wp[0] = ex[0];
   pp.wg[0] = ex[1];
   pp.wp[1] = ex[2];
@@ -1220,6 +1284,15 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
 
   const int kz = kpad_of(C), kh = kpad_of(H);
   const bool resident = C <= 128 && H <= 128 && N >= 16;
+  if (a.dialect == LF_AF3 && resident) {
+    // the resident kernels stage each interleaved tensor whole and split its columns in LDS
+    WView full[2];
+    LF_TRY(make_view(w.ap, C, 2 * C, "projection", &full[0]));
+    LF_TRY(make_view(w.ag, C, 2 * C, "gate", &full[1]));
+    pp.split = 1;
+    pp.wp[0] = wsrc(full[0]);
+    pp.wg[0] = wsrc(full[1], gate);
+  }
   {
     LaunchScope ls(ctx, a.direction == LF_OUTGOING ? "tri_out.project" : "tri_in.project");
     if (a.act_dtype == LF_F32) launch_project<DT_F32>(ctx, pp, resident, kz);

@@ -121,3 +121,60 @@ def test_invalid_shapes_rejected(ctx):
     m = torch.ones(4, 4, device=ctx.device)
     with pytest.raises(capi.LocalfoldError, match="inputs"):
         D.tri_mult(ctx, z, m, ws)
+
+
+def _tri_records(w, dtype, layout):
+    """The six matrices as `dtype` records stored (out,in) or, transposed, (in,out); returns
+    (records, the (out,in) float32 matrices the oracle takes)."""
+    recs, dec = dict(w), dict(w)
+    for name in H.TRI_MATS:
+        m = np.asarray(w[name], np.float32)
+        stored = m if layout == "out_in" else np.ascontiguousarray(m.T)
+        rec = S.make_record(stored, dtype)
+        rec["layout"] = layout
+        recs[name] = rec
+        d = H.decoded({"x": rec})["x"]
+        dec[name] = d if layout == "out_in" else np.ascontiguousarray(d.T)
+    return recs, dec
+
+
+def _shift_codes(dw, wt, rec, offset):
+    """Rebinds wt.data to a copy of the record's stored bytes that starts `offset` bytes past
+    an aligned address, so that the kernels cannot load the weights in aligned runs."""
+    import torch
+    dt = rec["dtype"]
+    host = (np.asarray(rec["data"], np.float32) if dt == "float32" else
+            np.asarray(rec["data"], np.float32).astype(np.float16) if dt == "float16" else np.asarray(rec["data"]))
+    raw = np.ascontiguousarray(host).view(np.uint8).reshape(-1)
+    buf = torch.zeros(raw.size + 64, dtype=torch.uint8, device=dw.device)
+    buf[offset:offset + raw.size] = torch.from_numpy(raw.copy()).to(dw.device)
+    dw.keep.append(buf)
+    wt.data = buf.data_ptr() + offset
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "int8", "int5"])
+@pytest.mark.parametrize("mode", ["in_out", "misaligned"])
+def test_weight_storage_paths(ctx, dtype, mode):
+    """The kernels decode the stored weights themselves, three ways: runs of 8 along k
+    ((out,in) storage, the other tests), runs along n ((in,out) storage: 8 columns per load,
+    written down the LDS rows), and weight by weight when the codes' address is not aligned
+    for the run loads (here 4 bytes past alignment: f32 and f16 runs need 16, int8 8; int5
+    1 byte past, against 4)."""
+    import torch
+    from localfold_amd import device as D
+    inp = S.deterministic_triangle_input(40, 128, 128, 13)
+    layout = "in_out" if mode == "in_out" else "out_in"
+    recs, dec = _tri_records(inp["weights"], dtype, layout)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.tri_mult_weights(dw, recs)
+    if mode == "misaligned":
+        off = 1 if dtype == "int5" else 4
+        for field, name in zip(("ap", "ag", "bp", "bg", "wz", "wg"), H.TRI_MATS):
+            _shift_codes(dw, getattr(ws, field), recs[name], off)
+    zt = torch.as_tensor(inp["z"]).to(ctx.device)
+    mt = torch.as_tensor(inp["mask"]).to(ctx.device)
+    for direction in ("outgoing", "incoming"):
+        out = D.tri_mult(ctx, zt, mt, ws, direction)
+        torch.cuda.synchronize()
+        ref = ops.tri_mult_af2(inp["z"], inp["mask"], dec, direction)
+        H.assert_close(out.cpu().numpy(), ref, label=f"{dtype}/{mode}/{direction}")
