@@ -44,7 +44,8 @@ def test_fixture_incoming_vs_oracle(ctx, name):
 
 
 @pytest.mark.parametrize("n,cz,ch,seed", [(3, 4, 5, 42), (37, 64, 32, 5), (37, 128, 128, 3), (64, 128, 128, 7),
-                                         (130, 128, 128, 11)])
+                                         (130, 128, 128, 11), (24, 256, 128, 17), (20, 256, 256, 19),
+                                         (12, 128, 128, 23)])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_deterministic_input(ctx, n, cz, ch, seed, direction):
     inp = S.deterministic_triangle_input(n, cz, ch, seed)
@@ -70,8 +71,11 @@ def test_quantised_weights_and_activation_dtypes(ctx, dtype, per_channel, act):
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 @pytest.mark.parametrize("divide", [False, True])
-def test_af3_dialect(ctx, direction, divide):
-    n, c = 40, 128
+@pytest.mark.parametrize("n", [40, 12])
+def test_af3_dialect(ctx, direction, divide, n):
+    """n = 40: the resident kernels (interleaved tensors split in LDS); n = 12: the chunked
+    kernels (the interleaved columns decoded weight by weight)."""
+    c = 128
     w = H.af3_tri_weights(c, 21)
     s = S.Stream(77)
     z = s.normal(n * n * c).reshape(n, n, c)
@@ -79,6 +83,7 @@ def test_af3_dialect(ctx, direction, divide):
     mask[-4:, :] = 0
     mask[:, -4:] = 0
     out, _ = _run(ctx, z, mask, w, direction, dialect=1, divide=divide)
+    assert out.shape == (n, n, c)
     ref = ops.tri_mult_af3(z, mask, w, direction, divide_by_length=divide)
     H.assert_close(out, ref, label=f"af3/{direction}/{divide}")
 
