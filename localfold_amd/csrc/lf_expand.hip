@@ -8,17 +8,33 @@
 
 namespace lf {
 
+// One thread per run of 8 stored weights (wrun_fetch / wrun_decode): along k, 8 values of one
+// destination row in one 16-byte store; along n ((in,out) storage, consecutive threads on
+// consecutive k, so each of the 8 row stores is coalesced), 8 rows of one column k.  Column n
+// goes to row (n / W) * 64 + off + n % W; runs along n never straddle a W group (W is a
+// multiple of 8 for such views).
 __global__ __launch_bounds__(256) void expand_weights_kernel(ExpandBatch b) {
   const int m = blockIdx.y;
   if (m >= b.count) return;
   const WView& v = b.v[m];
   const int kp = b.kp[m], W = b.W[m], off = b.off[m];
   const float sc = b.scale[m];
-  const long total = (long)b.ncols[m] * kp;
+  const bool krun = v.run != WRUN_N;
+  const int per = krun ? kp >> 3 : kp;
+  const long total = krun ? (long)b.ncols[m] * per : (long)((b.ncols[m] + 7) >> 3) * kp;
+  _Float16* dst = b.dst[m];
   for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
-    const int n = (int)(e / kp), k = (int)(e - (long)n * kp);
+    const int q = (int)(e / per), r = (int)(e - (long)q * per);
+    const int n = krun ? q : 8 * q, k = krun ? 8 * r : r;
+    const h8 h = wrun_decode(v, wrun_fetch(v, k, n, sc), k, n, sc);
     const long row = (long)(n / W) * 64 + off + n % W;
-    b.dst[m][row * kp + k] = (_Float16)(sc * wdecode(v, k, n));
+    if (krun) {
+      *reinterpret_cast<h8*>(dst + row * kp + k) = h;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (n + j < b.ncols[m]) dst[(row + j) * kp + k] = h[j];
+    }
   }
 }
 
@@ -41,7 +57,7 @@ int expand_weights(lf_context* ctx, const WView* views, int count, void* const* 
       most = std::max(most, (long)v.N * b.kp[i]);
     }
     LaunchScope ls(ctx, label);
-    dim3 grid((unsigned)std::min<long>((most + 255) / 256, 1024), b.count);
+    dim3 grid((unsigned)std::min<long>((most / 8 + 255) / 256, 1024), b.count);
     hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
     LF_TRY(check_hip(hipGetLastError(), "expand_weights launch"));
   }
@@ -66,7 +82,7 @@ int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* 
       most = std::max(most, (long)b.ncols[i] * kp);
     }
     LaunchScope ls(ctx, label);
-    dim3 grid((unsigned)std::min<long>((most + 255) / 256, 1024), b.count);
+    dim3 grid((unsigned)std::min<long>((most / 8 + 255) / 256, 1024), b.count);
     hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
     LF_TRY(check_hip(hipGetLastError(), "expand_packed launch"));
   }

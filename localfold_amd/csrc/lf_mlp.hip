@@ -50,27 +50,55 @@ struct MlpParams {
   const float *ln_s, *ln_o, *b1g, *b1v, *b2;
 };
 
+// GEMM2's k order within a chunk: position q = 8g + e holds hidden unit 4g + e (e < 4) or
+// 16 + 4g + e - 4 (e >= 4); q_of is the inverse, the position of hidden unit hl (its 4-aligned
+// groups stay together: q_of(4a + i) = q_of(4a) + i).
+__host__ __device__ constexpr int mlp_q_of(int hl) {
+  return hl < 16 ? 8 * (hl >> 2) + (hl & 3) : 8 * ((hl - 16) >> 2) + 4 + (hl & 3);
+}
+
 // Packed weights, chunk s of 32 hidden units: NG x 32 rows of W1^T (row r of group grp =
 // hidden unit 32s + r of the gate (grp 0) or value (grp 1) half, over the C inputs), then C
 // rows of W2^T, each holding the chunk's 32 hidden units in GEMM2's k order.  Decoding from
-// f32/f16/bf16/int8/int5 happens here, on the device.
-__global__ __launch_bounds__(256) void mlp_pack_kernel(WView w1g, WView w1v, WView w2, int C, int NG, long long total,
+// f32/f16/bf16/int8/int5 happens here, on the device, one thread per run of 8 stored weights
+// (wrun_fetch / wrun_decode): W1 runs are 8 inputs of one hidden unit (a 16-byte store) or 8
+// hidden units of one input (8 rows); W2 runs 8 hidden units of one output (two 4-wide pieces
+// of the k order) or 8 outputs of one hidden unit (8 rows).
+__global__ __launch_bounds__(256) void mlp_pack_kernel(WView w1g, WView w1v, WView w2, int C, int H, int NG,
                                                        _Float16* dst) {
   const long long ce = (long long)(NG * MLP_HC + MLP_HC) * C, w1e = (long long)NG * MLP_HC * C;
+  const bool k1 = w1g.run != WRUN_N, k2 = w2.run != WRUN_N;
+  const long long r1 = (long long)NG * H * C / 8, total = r1 + (long long)H * C / 8;
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
-    const long long s = i / ce, o = i - s * ce;
-    float v;
-    if (o < w1e) {
-      const int grp = (int)(o / ((long long)MLP_HC * C));
-      const int r = (int)((o / C) % MLP_HC), c = (int)(o % C);
-      v = wdecode(grp ? w1v : w1g, c, (int)(s * MLP_HC) + r);
-    } else {
-      const int o2 = (int)(o - w1e), c = o2 / MLP_HC, q = o2 % MLP_HC;
-      const int g = q >> 3, e = q & 7;
-      const int hl = e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4);
-      v = wdecode(w2, (int)(s * MLP_HC) + hl, c);
+    if (i < r1) {   // W1: (hidden unit u of group grp, input c)
+      const int grp = (int)(i / ((long long)H * C / 8)), j = (int)(i - (long long)grp * H * C / 8);
+      const int u = k1 ? j / (C / 8) : 8 * (j / C), c = k1 ? 8 * (j % (C / 8)) : j % C;
+      const WView& w = grp ? w1v : w1g;
+      const h8 h = wrun_decode(w, wrun_fetch(w, c, u, 1.f), c, u, 1.f);
+      _Float16* base = dst + (long long)(u / MLP_HC) * ce + (long long)grp * MLP_HC * C + c;
+      if (k1) {
+        *reinterpret_cast<h8*>(base + (long long)(u % MLP_HC) * C) = h;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) base[(long long)((u + e) % MLP_HC) * C] = h[e];
+      }
+    } else {        // W2: (hidden unit u, output c)
+      const int j = (int)(i - r1);
+      const int c = k2 ? j / (H / 8) : 8 * (j % (C / 8)), u = k2 ? 8 * (j % (H / 8)) : j / (C / 8);
+      const h8 h = wrun_decode(w2, wrun_fetch(w2, u, c, 1.f), u, c, 1.f);
+      _Float16* base = dst + (long long)(u / MLP_HC) * ce + w1e;
+      const int q = mlp_q_of(u % MLP_HC);
+      if (k2) {   // hidden units u..u+3 and u+4..u+7 sit 8 apart in the k order
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          base[(long long)c * MLP_HC + q + e] = h[e];
+          base[(long long)c * MLP_HC + q + 8 + e] = h[4 + e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) base[(long long)(c + e) * MLP_HC + q] = h[e];
+      }
     }
-    dst[i] = (_Float16)v;
   }
 }
 
@@ -255,10 +283,10 @@ int transition_fused(lf_context* ctx, const lf_transition_args& a, const WView* 
   const lf_transition_weights& w = *a.w;
   {
     LaunchScope ls(ctx, "transition.pack");
-    const long long total = (long long)mlp_packed_bytes(C, H, swiglu) / (long long)sizeof(_Float16);
-    const long long blocks = std::min<long long>((total + 255) / 256, 8192);
+    const long long runs = (long long)(NG + 1) * H * C / 8;
+    const long long blocks = std::min<long long>((runs + 255) / 256, 8192);
     hipLaunchKernelGGL(mlp_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, views[0],
-                       swiglu ? views[1] : views[0], views[NG], C, NG, total, static_cast<_Float16*>(packed));
+                       swiglu ? views[1] : views[0], views[NG], C, H, NG, static_cast<_Float16*>(packed));
   }
   LF_TRY(check_hip(hipGetLastError(), "transition pack launch"));
   MlpParams mp{};
