@@ -9,6 +9,8 @@
 //             MFMA, 256x256 tiles (128x128 when N*c is not a multiple of 256), written
 //             pair-major f16 (the next GEMM's rows)
 //   rowgemm   O W_out + b, / den, + pair residual
+//   fused     (c_outer 32, c_z 128, whole 256 tiles) the outer tile kept in LDS and the output
+//             GEMM, /den and residual run in the same kernel: O never reaches memory
 #include <algorithm>
 #include <cmath>
 
@@ -161,21 +163,14 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OuterParams p) {
   }
 }
 
-// The outer-product GEMM with 256x256 tiles for whole tiles (N*co a multiple of 256, S of
-// 64): half the L2-to-CU operand traffic per flop of the 128x128 kernel, which the L2 latency
-// at the bytes a CU keeps in flight otherwise bounds.  512 threads = 8 waves of 128x64
-// (2 in m x 4 in n); K steps of 64 double-buffered in LDS (147 KB, one block per CU), the next
-// step fetched into registers during the current one's MFMAs.  Same XCD band order as above.
 constexpr int OB = 256;
 constexpr size_t OB_SMEM = (size_t)2 * 2 * OB * OT_LD * sizeof(_Float16);   // 147,456 bytes
-__global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 obs[];   // [2][A 256 x OT_LD | B 256 x OT_LD]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
-  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+
+// The XCD band order of the 256-tile grid: tile (mt, nt) of block blockIdx.x.
+__device__ __forceinline__ void opm_big_order(const OuterParams& p, int& mt, int& nt) {
   const int M = p.N * p.co, tm = M / OB;
   const int total = (int)gridDim.x, per = total >> 3;
-  int lin = (int)blockIdx.x, mt, nt;
+  const int lin = (int)blockIdx.x;
   if (lin < per * 8) {
     const int x = lin & 7, q = lin >> 3;
     if (per % tm == 0) {
@@ -191,7 +186,15 @@ __global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
     mt = lin / tm;
     nt = lin % tm;
   }
-  const int m0 = mt * OB, n0 = nt * OB;
+}
+
+// The 256x256 tile at (m0, n0) accumulated into acc: lane holds rows m0 + wm*128 + 16i + r16,
+// columns n0 + wn*64 + 16j + 4g4 + u (wm = wave / 4, wn = wave % 4).  Ends after a barrier,
+// so the caller may reuse the LDS.
+__device__ __forceinline__ void opm_big_tile(const OuterParams& p, int m0, int n0, f4 (&acc)[8][4], _Float16* obs) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   constexpr int STAGE = 2 * OB * OT_LD;
   // thread tid loads rows (tid >> 3) + 64*it of each tile, k pieces (tid & 7)*8 .. +8
   const _Float16* pa = p.L + (size_t)(m0 + (tid >> 3)) * p.S + (tid & 7) * 8;
@@ -215,7 +218,6 @@ __global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
       *reinterpret_cast<h8*>(B + r * OT_LD + c) = rb[it];
     }
   };
-  f4 acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -228,22 +230,44 @@ __global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
     if (more) fetch(k0 + OT_BK);
     const _Float16* A = obs + kb * STAGE;
     const _Float16* B = A + OB * OT_LD;
+    // the A fragment of row tile i + 1 is read while row tile i's MFMAs run (the scheduling
+    // barriers keep the compiler from sinking each read to its use, which exposed the LDS
+    // latency once per 4 MFMAs)
 #pragma unroll
     for (int kk = 0; kk < OT_BK; kk += 32) {
-      h8 a[8], b[4];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const h8*>(A + (wm * 128 + i * 16 + r16) * OT_LD + kk + kq);
+      h8 b[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const h8*>(B + (wn * 64 + j * 16 + r16) * OT_LD + kk + kq);
+      h8 acur = *reinterpret_cast<const h8*>(A + (wm * 128 + r16) * OT_LD + kk + kq);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i) {
+        const h8 anext = *reinterpret_cast<const h8*>(A + (wm * 128 + ((i + 1) & 7) * 16 + r16) * OT_LD + kk + kq);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(b[j], a[i], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(b[j], acur, acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+        acur = anext;
+      }
     }
     if (more) put(kb ^ 1);
     __syncthreads();
   }
-  // acc[i][j][u]: row m = m0 + wm*128 + 16i + r16, columns n = n0 + wn*64 + 16j + 4g4 + u
+}
+
+// The outer-product GEMM with 256x256 tiles for whole tiles (N*co a multiple of 256, S of
+// 64): half the L2-to-CU operand traffic per flop of the 128x128 kernel, which the L2 latency
+// at the bytes a CU keeps in flight otherwise bounds.  512 threads = 8 waves of 128x64
+// (2 in m x 4 in n); K steps of 64 double-buffered in LDS (147 KB, one block per CU), the next
+// step fetched into registers during the current one's MFMAs.  Same XCD band order as above.
+__global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 obs[];   // [2][A 256 x OT_LD | B 256 x OT_LD]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3, r16 = lane & 15, g4 = lane >> 4;
+  int mt, nt;
+  opm_big_order(p, mt, nt);
+  const int m0 = mt * OB, n0 = nt * OB;
+  f4 acc[8][4];
+  opm_big_tile(p, m0, n0, acc, obs);
   const unsigned co = (unsigned)p.co;
   const long long cc = (long long)p.co * p.co;
   long long colpart[4];
@@ -262,6 +286,105 @@ __global__ __launch_bounds__(512) void opm_outer_big_kernel(OuterParams p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) o[u] = (_Float16)acc[i][j][u];
       *reinterpret_cast<h4*>(p.O + rowpart + colpart[j]) = o;
+    }
+  }
+}
+
+// The whole OPM update for c_outer = 32, c_z = 128 in one kernel: the 256x256 outer-product
+// tile above covers 8 x 8 residue pairs; instead of being stored, it goes to LDS as f16 rows
+// [pair][a*32 + b] (132 KB, reusing the K-step buffers), and the block runs the output GEMM
+// on it, D[c][pair] = sum_k W^T[c][k] O^T[k][pair], K = 1024: wave w owns all 64 pairs and
+// the channels 16 w .. +16, its W^T fragments read straight from the expanded weights (256 KB,
+// L2-resident, read once per block) a group of eight k steps ahead.  Epilogue as rowgemm's:
+// (D + b) / den + residual, a lane storing 4 consecutive channels of one pair.  The 302 MB
+// outer product at N = 384 never reaches memory.
+constexpr int OF_LD = 1024 + 8;
+struct OpmFusedParams {
+  OuterParams o;
+  const _Float16* W;    // expanded W_out: [c_z][1024], k contiguous
+  int kp;
+  const float* bias;    // [c_z] or null
+  const float* den;     // [N*N]
+  const void* resid;    // [N*N][c_z] or null
+  void* out;
+};
+
+template <int ACT>
+__global__ __launch_bounds__(512) void opm_fused_kernel(OpmFusedParams f) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 obs[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3, r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+  int mt, nt;
+  opm_big_order(f.o, mt, nt);
+  {
+    f4 acc[8][4];
+    opm_big_tile(f.o, mt * OB, nt * OB, acc, obs);
+    // tile row wm*128 + 16i + r16 = (residue, a), column wn*64 + 16j + 4g4 + u = (residue, b)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ml = wm * 128 + i * 16 + r16, ri = ml >> 5, a = ml & 31;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nl = wn * 64 + j * 16 + 4 * g4, rj = nl >> 5, b = nl & 31;
+        *reinterpret_cast<h4*>(obs + (ri * 8 + rj) * OF_LD + a * 32 + b) =
+            h4{(_Float16)acc[i][j][0], (_Float16)acc[i][j][1], (_Float16)acc[i][j][2], (_Float16)acc[i][j][3]};
+      }
+    }
+  }
+  __syncthreads();
+  // wave w: all 64 pairs (4 tiles of 16) x channels 16 w .. +16, so each block reads W once
+  const _Float16* wrow = f.W + (size_t)(wave * 16 + r16) * f.kp + kq;
+  const _Float16* orow = obs + r16 * OF_LD + kq;
+  f4 d[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) d[pt] = f4{0.f, 0.f, 0.f, 0.f};
+  // W^T fragments in groups of 8 k steps, double-buffered: group g + 1's loads are issued
+  // before group g's MFMAs, and scheduling barriers keep the compiler from sinking them
+  // towards their use (which left two or three loads in flight)
+  h8 wcur[8], wnext[8];
+  auto wload = [&](int g, h8 (&w)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const h8*>(wrow + 256 * g + 32 * u);
+  };
+  wload(0, wcur);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    wload(g < 3 ? g + 1 : 3, wnext);   // the last group reloads itself: loads stay unconditional
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = 256 * g + 32 * u;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+        d[pt] = mfma16(wcur[u], *reinterpret_cast<const h8*>(orow + pt * 16 * OF_LD + k), d[pt]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) wcur[u] = wnext[u];
+  }
+  // lane: channels c = 16 w + 4 g4 + i of pair 16 pt + r16 of the tile
+  const int N = f.o.N;
+  const int c = wave * 16 + 4 * g4;
+  float bias[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bias[i] = f.bias ? f.bias[c + i] : 0.f;
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) {
+    const int pl = pt * 16 + r16;
+    const size_t row = (size_t)(mt * 8 + (pl >> 3)) * N + nt * 8 + (pl & 7);
+    const float inv = 1.f / f.den[row];
+    {
+      const size_t idx = row * 128 + c;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (d[pt][i] + bias[i]) * inv;
+      if (f.resid) {
+        float r[4];
+        ld4v<ACT>(f.resid, idx, r);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += r[i];
+      }
+      st4v<ACT>(f.out, idx, v);
     }
   }
 }
@@ -291,10 +414,15 @@ __global__ __launch_bounds__(256) void opm_count_kernel(const float* mask, float
   if (i < N && j < N) den[(size_t)i * N + j] = eps + acc;
 }
 
-// The big kernel's dynamic LDS (above the 64 KB default) is opted into once per process.
+// The big kernels' dynamic LDS (above the 64 KB default) is opted into once per process.
 static bool big_smem_ok(lf_context*) {
-  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(opm_outer_big_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)OB_SMEM) == hipSuccess;
+  auto opt = [](const void* k) {
+    return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)OB_SMEM) == hipSuccess;
+  };
+  static const bool ok = opt(reinterpret_cast<const void*>(opm_outer_big_kernel)) &&
+                         opt(reinterpret_cast<const void*>(opm_fused_kernel<DT_F32>)) &&
+                         opt(reinterpret_cast<const void*>(opm_fused_kernel<DT_F16>)) &&
+                         opt(reinterpret_cast<const void*>(opm_fused_kernel<DT_BF16>));
   return ok;
 }
 
@@ -334,7 +462,9 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   pp.ngroups = 2;
 
   const size_t lr = (size_t)N * co * S * sizeof(_Float16);
-  const size_t ob = (size_t)pairs * co * co * sizeof(_Float16);
+  // c_outer 32, c_z 128, whole 256 tiles: the output GEMM runs inside the outer-product kernel
+  const bool fused = co == 32 && cz == 128 && (N * co) % OB == 0 && S % OT_BK == 0 && big_smem_ok(ctx);
+  const size_t ob = fused ? 0 : (size_t)pairs * co * co * sizeof(_Float16);
   size_t sizes[6] = {lr, lr, ob, (size_t)pairs * sizeof(float), expanded_bytes(views[2]), lnproj_packed_bytes(pp)};
   void* bufs[6];
   LF_TRY(workspace(ctx, sizes, bufs, 6));
@@ -352,6 +482,19 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
                        S, N, a.norm_epsilon);
   }
   LF_TRY(check_hip(hipGetLastError(), "opm count launch"));
+  if (fused) {
+    OpmFusedParams f{OuterParams{L, R, nullptr, N, co, S}, wo.p, wo.kp, w.bo, den,
+                     a.accumulate ? a.pair_in : nullptr, a.out};
+    const int tb = N * co / OB;
+    LaunchScope ls(ctx, "opm.fused");
+    if (a.pair_dtype == LF_F32)
+      hipLaunchKernelGGL(opm_fused_kernel<DT_F32>, dim3((unsigned)(tb * tb)), dim3(512), OB_SMEM, ctx->stream, f);
+    else if (a.pair_dtype == LF_F16)
+      hipLaunchKernelGGL(opm_fused_kernel<DT_F16>, dim3((unsigned)(tb * tb)), dim3(512), OB_SMEM, ctx->stream, f);
+    else
+      hipLaunchKernelGGL(opm_fused_kernel<DT_BF16>, dim3((unsigned)(tb * tb)), dim3(512), OB_SMEM, ctx->stream, f);
+    return check_hip(hipGetLastError(), "opm fused launch");
+  }
   {  // O[(i, j)][a*co + b] = sum_s l[i][a][s] r[j][b][s]
     OuterParams op{L, R, O, N, co, S};
     const int tm = (N * co + OT - 1) / OT;

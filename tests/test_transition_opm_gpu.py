@@ -94,6 +94,37 @@ def test_opm_af2(ctx, blockw, s, n):
     H.assert_close(pair.cpu().numpy(), ref, label=f"opm {s}x{n}")
 
 
+@pytest.mark.parametrize("dt,accumulate", [("bfloat16", True), ("float16", False), ("float32", False)])
+def test_opm_fused_output(ctx, blockw, dt, accumulate):
+    """c_outer 32, c_z 128 with whole 256-row outer tiles (N = 64, S = 64) takes the fused kernel:
+    the output GEMM, the /den and the residual run on the outer-product tile in LDS.  Pair in
+    each activation dtype, accumulated in place or written to a separate output."""
+    import torch
+    from localfold_amd import device as D
+    s_, n = 64, 64
+    act = S.synthetic_activations(s_, n, 256, 128, seed=91)
+    mask = act["msaMask"].copy()
+    mask[3, ::4] = 0
+    mask[:, -3:] = 0
+    w = blockw["outerProductMean"]
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.opm_weights(dw, w)
+    tdt = getattr(torch, dt)
+    pair_in = _dev(ctx, act["pair"]).to(tdt)
+    before = pair_in.float().cpu().numpy().astype(np.float64)   # the stored input, before the update
+    out = pair_in if accumulate else torch.full_like(pair_in, 7.0)
+    D.outer_product_mean(ctx, _dev(ctx, act["msa"]), _dev(ctx, mask), ws, 32, 128, pair=pair_in, out=out,
+                         accumulate=accumulate)
+    torch.cuda.synchronize()
+    upd = ops.outer_product_mean_af2(act["msa"], mask, w)
+    ref = (before + upd) if accumulate else upd
+    # the result is stored in the pair dtype: add one rounding of the largest value to the
+    # bound (half an ulp, at most 2^-8 of the value for bf16's 8 significant bits, 2^-11 for f16)
+    half_ulp = {"bfloat16": 2.0 ** -8, "float16": 2.0 ** -11, "float32": 0.0}[dt]
+    H.assert_close(out.float().cpu().numpy(), ref, max_abs=H.MAX_ABS + half_ulp * float(np.abs(ref).max()),
+                   label=f"opm fused {dt} accumulate={accumulate}")
+
+
 def test_opm_af3(ctx):
     import torch
     from localfold_amd import capi, device as D
