@@ -320,33 +320,44 @@ __device__ __forceinline__ void frag_load_row(FragTile<ACT, KS>& t, const void* 
   const T* s = static_cast<const T*>(src) + srow * (size_t)C;
   const int g = lane >> 4;
   if (C == 32 * KS) {
+    // one per-lane base, then compile-time offsets (immediates of the loads): with the lane
+    // term inside each address the compiler kept a 64-bit address per load live and spilled
+    const T* sg = s + 8 * g;
 #pragma unroll
     for (int j = 0; j < KS; ++j)
 #pragma unroll
       for (int v = 0; v < FragTile<ACT, KS>::NV; ++v)
-        t.raw[j][v] = *reinterpret_cast<const u32x4*>(s + 32 * j + 8 * g + v * (16 / (int)sizeof(T)));
+        t.raw[j][v] = *reinterpret_cast<const u32x4*>(sg + 32 * j + v * (16 / (int)sizeof(T)));
   } else {
+    // C not a multiple of 32: when rows stay 16-byte aligned, whole 8-channel groups below C
+    // take the vector loads and the group that straddles C (one lane group of one k-step)
+    // reads element by element, zero past C; otherwise every group reads element by element
+    const T* sg = s + 8 * g;
+    const bool vec = (C * (int)sizeof(T)) % 16 == 0;
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      uint32_t w[4 * FragTile<ACT, KS>::NV];
-      if constexpr (ACT == DT_F32) {
+      const int c0 = 32 * j + 8 * g;
+      if (vec && c0 + 8 <= C) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int c = 32 * j + 8 * g + k;
-          const uint32_t bits = __float_as_uint(s[c < C ? c : 0]);
-          w[k] = c < C ? bits : 0u;
-        }
-        t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
-        t.raw[j][1] = u32x4{w[4], w[5], w[6], w[7]};
+        for (int v = 0; v < FragTile<ACT, KS>::NV; ++v)
+          t.raw[j][v] = *reinterpret_cast<const u32x4*>(sg + 32 * j + v * (16 / (int)sizeof(T)));
       } else {
+        uint32_t w[4 * FragTile<ACT, KS>::NV];
+        if constexpr (ACT == DT_F32) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int c0 = 32 * j + 8 * g + 2 * k;
-          const uint16_t lo = c0 < C ? __builtin_bit_cast(uint16_t, s[c0 < C ? c0 : 0]) : (uint16_t)0;
-          const uint16_t hi = c0 + 1 < C ? __builtin_bit_cast(uint16_t, s[c0 + 1 < C ? c0 + 1 : 0]) : (uint16_t)0;
-          w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+          for (int k = 0; k < 8; ++k) w[k] = c0 + k < C ? __float_as_uint(s[c0 + k]) : 0u;
+          t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
+          t.raw[j][1] = u32x4{w[4], w[5], w[6], w[7]};
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int c = c0 + 2 * k;
+            const uint16_t lo = c < C ? __builtin_bit_cast(uint16_t, s[c]) : (uint16_t)0;
+            const uint16_t hi = c + 1 < C ? __builtin_bit_cast(uint16_t, s[c + 1]) : (uint16_t)0;
+            w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+          }
+          t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
         }
-        t.raw[j][0] = u32x4{w[0], w[1], w[2], w[3]};
       }
     }
   }

@@ -263,6 +263,10 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
     FragTile<ACT, KS> t0;
     frag_load_row(t0, p.x, (size_t)srow_of(myrow < p.rows ? myrow : 0), p.C, lane);
     frag_ln_raw1(t0, xb[tt], p.C, Gs, Gs + KP, p.eps, p.fast_var, lane);
+    // one raw tile live at a time: without the barrier the second tile's loads are hoisted
+    // above the first tile's LayerNorm, and with f32 rows (64 VGPRs a tile at C = 256) the
+    // prologue spilled to scratch
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   for (int ci = ci0; ci < ci1; ++ci) {
