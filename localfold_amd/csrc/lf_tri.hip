@@ -867,6 +867,19 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
   __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
+  const int ntiles = p.kmajor_out ? p.N * (p.N >> 4) : p.P >> 4, nw = gridDim.x * NWV;
+  auto fetch = [&](int tl, FragTile<ACT, 4>& t, float (&m)[4]) __attribute__((always_inline)) {
+    const TileGeom g = tile_geom(p, tl);
+    frag_load_row(t, p.z, (size_t)g.src0 + (size_t)r16 * g.sstride, 128, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = p.mask[g.src0 + (q4 + i) * g.sstride];
+  };
+  // the first tile's rows load while the weights are decoded into LDS (clamped, never skipped)
+  int tile = blockIdx.x * NWV + wave;
+  FragTile<ACT, 4> tc;
+  float mc[4];
+  fetch(tile < ntiles ? tile : 0, tc, mc);
   stage_project_weights<NT>(Ws, p, tid);
   for (int i = tid; i < 128; i += NT) {
     Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
@@ -877,20 +890,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   stage_vec(Gs, p.ln_s, 128, 1.f, 128, tid, NT);
   stage_vec(Gs + 128, p.ln_o, 128, 0.f, 128, tid, NT);
   __syncthreads();
-
-  const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
-  const int ntiles = p.kmajor_out ? p.N * (p.N >> 4) : p.P >> 4, nw = gridDim.x * NWV;
-  auto fetch = [&](int tl, FragTile<ACT, 4>& t, float (&m)[4]) __attribute__((always_inline)) {
-    const TileGeom g = tile_geom(p, tl);
-    frag_load_row(t, p.z, (size_t)g.src0 + (size_t)r16 * g.sstride, 128, lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m[i] = p.mask[g.src0 + (q4 + i) * g.sstride];
-  };
-  int tile = blockIdx.x * NWV + wave;
   if (tile >= ntiles) return;
-  FragTile<ACT, 4> tc;
-  float mc[4];
-  fetch(tile, tc, mc);
   for (; tile < ntiles; tile += nw) {
     const int out0 = tile_geom(p, tile).out0;
     h8 xa[4];
@@ -1003,6 +1003,17 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][2][16 * O2_LD];
   __shared__ __attribute__((aligned(16))) float Vs[6 * 128];         // bz, bg', centre-norm s/o, LN_in s/o
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nfull = p.P >> 4, nw = gridDim.x * NWV;
+  // the first tile's z rows and X columns load while the weights are decoded into LDS
+  // (clamped, never skipped)
+  int tile = blockIdx.x * NWV + wave;
+  FragTile<ACT, 4> zc;
+  h8 xv[4];
+  {
+    const int t0 = tile < nfull ? tile : 0;
+    frag_load(zc, p.z, (size_t)t0 * 16, 16, 128, lane);
+    if constexpr (VECX) x_fetch(xv, p.X, p.P, t0 * 16, lane);
+  }
   {
     _Float16* const dst[2] = {Wz, Wg};
     const WSrc* const src[2] = {&p.wz, &p.wg};
@@ -1019,7 +1030,6 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   __syncthreads();
 
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
-  const int nfull = p.P >> 4, nw = gridDim.x * NWV;
 
   // One tile: LN_out of X (LDS buffer Xc) and LN_in of z (zc), then two passes of 64 output
   // channels.  A pass stages its f32 update in Xc (the X fragments are in registers by then)
@@ -1097,13 +1107,8 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     pass(std::integral_constant<int, 1>{});
   };
 
-  int tile = blockIdx.x * NWV + wave;
   if (tile < nfull) {
-    FragTile<ACT, 4> zc;
-    frag_load(zc, p.z, (size_t)tile * 16, 16, 128, lane);
     if constexpr (VECX) {
-      h8 xv[4];
-      x_fetch(xv, p.X, p.P, tile * 16, lane);
       x_put(Xs[wave][0], xv, lane);
     } else {
       x_transpose<ACT>(Xs[wave][0], p.X, p.P, tile * 16, 16, lane);
