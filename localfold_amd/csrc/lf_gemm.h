@@ -40,8 +40,9 @@ struct ExpandBatch {
 // and zero exactly as stored, no arithmetic on them, so a prefetch never waits -- and
 // wrun_decode turns the words into 8 f16 values when they are written to LDS.  The decode is
 // the reference's readTensorRange arithmetic (shared/weights/dtype.js:212-406): int8
-// code * scale, int5 fma(code, scale, zero) with codes LSB-first at bit 5i, in f32, times
-// `mul`, rounded once to f16.  f32 weights are converted at fetch (they are not a codec).
+// code * scale, int5 fma(code, scale, zero) with codes LSB-first at bit 5i, in f32, with the
+// kernel's factor `mul` folded into scale and zero (1 for the reference's own weights),
+// rounded once to f16.  f32 weights are converted at fetch (they are not a codec).
 // Coordinates outside the view are clamped for the fetch and decode to zeros.
 struct WRunAt {
   int flat;   // flat index of the run's first stored weight (clamped)
@@ -71,84 +72,92 @@ __device__ __noinline__ u32x4 wrun_gather(WView w, int k, int n, float mul) {
   return v;
 }
 
+// The fetch and decode of one stored dtype (a compile-time constant): straight-line code for
+// callers that know every view they stage has that dtype.
+template <int DT>
+__device__ __forceinline__ u32x4 wrun_fetch_dt(const WView& w, const WRunAt& r, float mul) {
+  u32x4 v;
+  if constexpr (DT == DT_F32) {
+    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(w.data) + r.flat);
+    const float4 a = src[0], b = src[1];
+    h8 h;
+    h[0] = (_Float16)(mul * a.x); h[1] = (_Float16)(mul * a.y); h[2] = (_Float16)(mul * a.z); h[3] = (_Float16)(mul * a.w);
+    h[4] = (_Float16)(mul * b.x); h[5] = (_Float16)(mul * b.y); h[6] = (_Float16)(mul * b.z); h[7] = (_Float16)(mul * b.w);
+    __builtin_memcpy(&v, &h, 16);
+  } else if constexpr (DT == DT_F16 || DT == DT_BF16) {
+    v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w.data) + r.flat);
+  } else if constexpr (DT == DT_I8) {
+    const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w.data) + r.flat);
+    v = u32x4{c.x, c.y, (uint32_t)w.scales[r.grp], 0u};
+  } else {   // int5: the run is the 5 bytes at 5 * flat / 8, inside two aligned words
+    const uint8_t* b = static_cast<const uint8_t*>(w.data) + (((r.flat >> 3) * 5) & ~3);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(b);
+    v = u32x4{q[0], q[1], (uint32_t)w.scales[r.grp], (uint32_t)w.zeros[r.grp]};
+  }
+  return v;
+}
+
+template <int DT>
+__device__ __forceinline__ h8 wrun_decode_dt(const u32x4& v, const WRunAt& r, float mul) {
+  h8 h;
+  if constexpr (DT == DT_F32) {   // converted at fetch
+    __builtin_memcpy(&h, &v, 16);
+  } else if constexpr (DT == DT_F16) {
+    __builtin_memcpy(&h, &v, 16);
+    if (mul != 1.f) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * (float)h[j]);
+    }
+  } else if constexpr (DT == DT_BF16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t word = v[j >> 1];
+      h[j] = (_Float16)(mul * __uint_as_float((j & 1) ? (word & 0xffff0000u) : (word << 16)));
+    }
+  } else if constexpr (DT == DT_I8) {
+    // `mul` folded into the scale (and zero): one product per run instead of per weight
+    const float sc = mul * h2f((uint16_t)v.z);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int code = (int)(int8_t)(((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu);
+      h[j] = (_Float16)((float)code * sc);
+    }
+  } else {
+    const float sc = mul * h2f((uint16_t)v.z), zp = mul * h2f((uint16_t)v.w);
+    const int sh = (((r.flat >> 3) * 5) & 3) * 8;
+    const uint64_t x = (((uint64_t)v.y << 32) | v.x) >> sh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)fmaf((float)((uint32_t)(x >> (5 * j)) & 31u), sc, zp);
+  }
+  if (!r.ok) h = h8{0, 0, 0, 0, 0, 0, 0, 0};
+  return h;
+}
+
 // GATHER = false: the caller guarantees w.run != WRUN_GATHER (kernels are instantiated
 // without the out-of-line call, which costs registers even where it is never taken).
 template <bool GATHER = true>
 __device__ __forceinline__ u32x4 wrun_fetch(const WView& w, int k, int n, float mul) {
   if (GATHER && w.run == WRUN_GATHER) return wrun_gather(w, k, n, mul);
   const WRunAt r = wrun_at(w, k, n);
-  u32x4 v;
   switch (w.dtype) {
-    case DT_F32: {
-      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(w.data) + r.flat);
-      const float4 a = src[0], b = src[1];
-      h8 h;
-      h[0] = (_Float16)(mul * a.x); h[1] = (_Float16)(mul * a.y); h[2] = (_Float16)(mul * a.z); h[3] = (_Float16)(mul * a.w);
-      h[4] = (_Float16)(mul * b.x); h[5] = (_Float16)(mul * b.y); h[6] = (_Float16)(mul * b.z); h[7] = (_Float16)(mul * b.w);
-      __builtin_memcpy(&v, &h, 16);
-      break;
-    }
-    case DT_F16:
-    case DT_BF16:
-      v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w.data) + r.flat);
-      break;
-    case DT_I8: {
-      const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w.data) + r.flat);
-      v = u32x4{c.x, c.y, (uint32_t)w.scales[r.grp], 0u};
-      break;
-    }
-    default: {   // int5: the run is the 5 bytes at 5 * flat / 8, inside two aligned words
-      const uint8_t* b = static_cast<const uint8_t*>(w.data) + (((r.flat >> 3) * 5) & ~3);
-      const uint32_t* q = reinterpret_cast<const uint32_t*>(b);
-      v = u32x4{q[0], q[1], (uint32_t)w.scales[r.grp], (uint32_t)w.zeros[r.grp]};
-    }
+    case DT_F32: return wrun_fetch_dt<DT_F32>(w, r, mul);
+    case DT_F16: return wrun_fetch_dt<DT_F16>(w, r, mul);
+    case DT_BF16: return wrun_fetch_dt<DT_BF16>(w, r, mul);
+    case DT_I8: return wrun_fetch_dt<DT_I8>(w, r, mul);
+    default: return wrun_fetch_dt<DT_I5>(w, r, mul);
   }
-  return v;
 }
 
 template <bool GATHER = true>
 __device__ __forceinline__ h8 wrun_decode(const WView& w, const u32x4& v, int k, int n, float mul) {
   const WRunAt r = wrun_at(w, k, n);
-  h8 h;
   switch (GATHER && w.run == WRUN_GATHER ? DT_F32 : w.dtype) {
-    case DT_F32:   // converted at fetch (f32 storage, or a gathered run)
-      __builtin_memcpy(&h, &v, 16);
-      break;
-    case DT_F16: {
-      __builtin_memcpy(&h, &v, 16);
-      if (mul != 1.f) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * (float)h[j]);
-      }
-      break;
-    }
-    case DT_BF16: {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t word = v[j >> 1];
-        h[j] = (_Float16)(mul * __uint_as_float((j & 1) ? (word & 0xffff0000u) : (word << 16)));
-      }
-      break;
-    }
-    case DT_I8: {
-      const float sc = h2f((uint16_t)v.z);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int code = (int)(int8_t)(((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu);
-        h[j] = (_Float16)(mul * ((float)code * sc));
-      }
-      break;
-    }
-    default: {
-      const float sc = h2f((uint16_t)v.z), zp = h2f((uint16_t)v.w);
-      const int sh = (((r.flat >> 3) * 5) & 3) * 8;
-      const uint64_t x = (((uint64_t)v.y << 32) | v.x) >> sh;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) h[j] = (_Float16)(mul * fmaf((float)((uint32_t)(x >> (5 * j)) & 31u), sc, zp));
-    }
+    case DT_F32: return wrun_decode_dt<DT_F32>(v, r, mul);   // a gathered run is converted at fetch
+    case DT_F16: return wrun_decode_dt<DT_F16>(v, r, mul);
+    case DT_BF16: return wrun_decode_dt<DT_BF16>(v, r, mul);
+    case DT_I8: return wrun_decode_dt<DT_I8>(v, r, mul);
+    default: return wrun_decode_dt<DT_I5>(v, r, mul);
   }
-  if (!r.ok) h = h8{0, 0, 0, 0, 0, 0, 0, 0};
-  return h;
 }
 
 // Writes a decoded run to Ws[n][k] (pitch ldw halves): one 16-byte store for a run along k

@@ -401,9 +401,11 @@ constexpr int RS_LD = 136;
 // interleaved tensor of 256 stored columns, column c going to row c / 2 of dst[m] (c even) or
 // of dst2[m] (c odd).  Every run's loads are issued before the first decode, so the whole
 // stage waits for memory once.
-template <int COUNT, int NT, bool SPLIT = false>
-__device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], const WSrc* const (&src)[COUNT],
-                                               int tid, _Float16* const (&dst2)[COUNT] = {}) {
+// DT >= 0: every view is stored as DT with runs (no gathered view), so the fetches and
+// decodes are straight-line code; DT < 0: each run dispatches on its view's dtype and run.
+template <int COUNT, int NT, bool SPLIT, int DT>
+__device__ __forceinline__ void stage_resident_as(_Float16* const (&dst)[COUNT], const WSrc* const (&src)[COUNT],
+                                                  int tid, _Float16* const (&dst2)[COUNT]) {
   constexpr int COLS = SPLIT ? 256 : 128, RUNS = COLS * 128 / 8, PER = (RUNS + NT - 1) / NT;
   auto coords = [&](bool krun, int i, int& n, int& k) {
     if (krun) { n = i >> 4; k = (i & 15) * 8; }
@@ -417,7 +419,8 @@ __device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], co
     for (int u = 0; u < PER; ++u) {
       int n, k;
       coords(krun, min(tid + u * NT, RUNS - 1), n, k);
-      v[m][u] = wrun_fetch(src[m]->v, k, n, src[m]->mul);
+      if constexpr (DT >= 0) v[m][u] = wrun_fetch_dt<DT>(src[m]->v, wrun_at(src[m]->v, k, n), src[m]->mul);
+      else v[m][u] = wrun_fetch(src[m]->v, k, n, src[m]->mul);
     }
   }
 #pragma unroll
@@ -428,7 +431,9 @@ __device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], co
       if (tid + u * NT >= RUNS) continue;
       int n, k;
       coords(krun, tid + u * NT, n, k);
-      const h8 h = wrun_decode(src[m]->v, v[m][u], k, n, src[m]->mul);
+      h8 h;
+      if constexpr (DT >= 0) h = wrun_decode_dt<DT>(v[m][u], wrun_at(src[m]->v, k, n), src[m]->mul);
+      else h = wrun_decode(src[m]->v, v[m][u], k, n, src[m]->mul);
       if (!SPLIT) {
         wrun_put(dst[m], RS_LD, krun, n, k, h);
       } else if (krun) {
@@ -439,6 +444,31 @@ __device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], co
       }
     }
   }
+}
+
+// The weights of a resident kernel: COUNT matrices of up to 128 x 128 (k, n < 128) into dst[m]
+// as [n][k] rows of pitch RS_LD, decoded from the stored codes.  SPLIT: each view is an AF3
+// interleaved tensor of 256 stored columns, column c going to row c / 2 of dst[m] (c even) or
+// of dst2[m] (c odd).  Every run's loads are issued before the first decode, so the whole
+// stage waits for memory once.  When all views share one stored dtype and none is gathered
+// (the usual case: one codec per model), the stage runs as straight-line code for that dtype.
+template <int COUNT, int NT, bool SPLIT = false>
+__device__ __forceinline__ void stage_resident(_Float16* const (&dst)[COUNT], const WSrc* const (&src)[COUNT],
+                                               int tid, _Float16* const (&dst2)[COUNT] = {}) {
+  const int dt = src[0]->v.dtype;
+  bool uniform = true;
+#pragma unroll
+  for (int m = 0; m < COUNT; ++m) uniform = uniform && src[m]->v.dtype == dt && src[m]->v.run != WRUN_GATHER;
+  if (uniform) {
+    switch (dt) {
+      case DT_F32: stage_resident_as<COUNT, NT, SPLIT, DT_F32>(dst, src, tid, dst2); return;
+      case DT_F16: stage_resident_as<COUNT, NT, SPLIT, DT_F16>(dst, src, tid, dst2); return;
+      case DT_BF16: stage_resident_as<COUNT, NT, SPLIT, DT_BF16>(dst, src, tid, dst2); return;
+      case DT_I8: stage_resident_as<COUNT, NT, SPLIT, DT_I8>(dst, src, tid, dst2); return;
+      default: stage_resident_as<COUNT, NT, SPLIT, DT_I5>(dst, src, tid, dst2); return;
+    }
+  }
+  stage_resident_as<COUNT, NT, SPLIT, -1>(dst, src, tid, dst2);
 }
 
 // The a/b projection and gate weights of the project kernels: blocks [a-proj, a-gate, b-proj,
