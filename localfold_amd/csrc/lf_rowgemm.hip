@@ -611,6 +611,99 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
   }
 }
 
+// Weight-resident form for K = 32 KS <= 256 and N = 64 NP <= 256 (the attention output
+// projections): a block stages the whole expanded W (N x K f16, up to 132 KB) in LDS once, and
+// each of its 8 waves then walks 16-row tiles w, w + nw, ... with no block barrier.  A tile's
+// A fragments come straight from memory into registers (the next tile's are loaded during
+// this one's MFMAs), its residual and row denominator are loaded at the top of the tile, and
+// the columns run in passes of 64 (4 accumulator tiles), each followed by its epilogue.
+// W is the MFMA A operand, so a lane holds 4 consecutive columns of one row: one 8- or
+// 16-byte store per column tile.  Rows past the end are clamped for the loads and not stored.
+template <int DACT, int KS, int NP>
+__global__ __launch_bounds__(512) void rowgemm_res_kernel(RowGemmParams p) {
+  constexpr int K = 32 * KS, N = 64 * NP, LDW = K + 8;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[N * LDW];
+  __shared__ __attribute__((aligned(16))) float Bs[N];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
+  const int ntiles = (p.rows + 15) >> 4, nw = (int)gridDim.x * 8;
+  auto aload = [&](int tl, h8 (&a)[KS]) __attribute__((always_inline)) {
+    const int row = min(tl * 16 + r16, p.rows - 1);
+    const _Float16* ar = p.A + (size_t)row * p.K + kq;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) a[j] = *reinterpret_cast<const h8*>(ar + 32 * j);
+  };
+  int tile = (int)blockIdx.x * 8 + wave;
+  h8 a[KS];
+  aload(tile < ntiles ? tile : 0, a);
+  // the whole W, 16-byte pieces of E[n][k] (row pitch p.w.kp >= K)
+  for (int i = tid; i < N * K / 8; i += 512) {
+    const int n = i / (K / 8), k = (i - n * (K / 8)) * 8;
+    const uint4 v = n < p.w.N ? *reinterpret_cast<const uint4*>(p.w.p + (size_t)n * p.w.kp + k) : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(Ws + n * LDW + k) = v;
+  }
+  for (int i = tid; i < N; i += 512) Bs[i] = (p.bias && i < p.N) ? p.bias[i] : 0.f;
+  __syncthreads();
+  for (; tile < ntiles; tile += nw) {
+    const int row = tile * 16 + r16;
+    const bool valid = row < p.rows;
+    const int rc = valid ? row : p.rows - 1;
+    const unsigned q = (unsigned)p.dst.Q;
+    const unsigned b = (unsigned)rc / q, nn = (unsigned)rc - b * q;
+    const int rowpart = (int)b * (int)p.dst.sB + (int)nn * (int)p.dst.sN;
+    typename Raw4v<DACT>::T rr[NP][4];
+    if (p.resid) {
+#pragma unroll
+      for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) rr[pp][t] = Raw4v<DACT>::load(p.resid, rowpart + pp * 64 + t * 16 + 4 * g4);
+    }
+    const float inv = p.rowden ? 1.f / p.rowden[rc] : 1.f;
+    // the next tile's A fragments (clamped, never skipped), after this tile's other loads
+    const int nt = tile + nw < ntiles ? tile + nw : tile;
+    h8 an[KS];
+    aload(nt, an);
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      f4 acc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const h8 w = *reinterpret_cast<const h8*>(Ws + (pp * 64 + t * 16 + r16) * LDW + 32 * j + kq);
+          acc[t] = mfma16(w, a[j], acc[t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // one k step's weight fragments live at a time
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int c = pp * 64 + t * 16 + 4 * g4;
+        const float4 bb = *reinterpret_cast<const float4*>(&Bs[c]);
+        const float bs[4] = {bb.x, bb.y, bb.z, bb.w};
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float y = acc[t][i] + bs[i];
+          if (p.op == OP_RELU) y = fmaxf(y, 0.f);
+          v[i] = y * inv;
+        }
+        if (p.resid) {
+          float r[4];
+          Raw4v<DACT>::unpack(rr[pp][t], r);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += r[i];
+        }
+        if (valid && c < p.N) st4<DACT>(p.dst.ptr, rowpart + c, v);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < KS; ++j) a[j] = an[j];
+  }
+}
+
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   if (p.rows <= 0) return LF_OK;
   const std::string l(label);
@@ -620,9 +713,28 @@ int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
     return set_error(LF_ERR_INVALID, l + ": rowgemm destination columns must be contiguous and 4-aligned");
   const long long span = (long long)((p.rows - 1) / d.Q) * d.sB + (long long)std::min(p.rows - 1, d.Q - 1) * d.sN + p.N;
   if (span >= (1LL << 31)) return set_error(LF_ERR_INVALID, l + ": destination above 2^31 elements");
+  LaunchScope ls(ctx, label);
+  // weight-resident form: the whole W in LDS, N and K whole multiples of the tiles
+  const int np = p.N / 64, ks = p.K / 32;
+  if (p.N % 64 == 0 && p.K % 32 == 0 && (np == 2 || np == 4) && (ks == 4 || ks == 8) && p.w.kp >= p.K &&
+      p.dst.D >= 64 * np && (p.rows + 15) / 16 >= 8 * ctx->num_cus) {
+    const int per_cu = np * ks <= 8 ? 2 : 1;   // LDS: 34 KB (128 x 128) or up to 132 KB
+    dim3 g((unsigned)std::min((p.rows + 127) / 128, per_cu * ctx->num_cus));
+#define LF_RR(D, KS_, NP_) hipLaunchKernelGGL((rowgemm_res_kernel<D, KS_, NP_>), g, dim3(512), 0, ctx->stream, p)
+#define LF_RRD(D)                                      \
+  if (ks == 4 && np == 2) LF_RR(D, 4, 2);               \
+  else if (ks == 4) LF_RR(D, 4, 4);                     \
+  else if (np == 2) LF_RR(D, 8, 2);                     \
+  else LF_RR(D, 8, 4);
+    if (d.dtype == DT_F32) { LF_RRD(DT_F32) }
+    else if (d.dtype == DT_F16) { LF_RRD(DT_F16) }
+    else { LF_RRD(DT_BF16) }
+#undef LF_RRD
+#undef LF_RR
+    return check_hip(hipGetLastError(), label);
+  }
   const int nt = p.N <= 128 ? 4 : 8;
   dim3 grid((p.rows + 127) / 128, (p.N + 32 * nt - 1) / (32 * nt));
-  LaunchScope ls(ctx, label);
 #define LF_RG(D, T) hipLaunchKernelGGL((rowgemm_kernel<D, T>), grid, dim3(512), 0, ctx->stream, p)
   if (d.dtype == DT_F32) { if (nt == 4) LF_RG(DT_F32, 4); else LF_RG(DT_F32, 8); }
   else if (d.dtype == DT_F16) { if (nt == 4) LF_RG(DT_F16, 4); else LF_RG(DT_F16, 8); }
