@@ -619,30 +619,30 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
 // the columns run in passes of 64 (4 accumulator tiles), each followed by its epilogue.
 // W is the MFMA A operand, so a lane holds 4 consecutive columns of one row: one 8- or
 // 16-byte store per column tile.  Rows past the end are clamped for the loads and not stored.
-template <int DACT, int KS, int NP>
-__global__ __launch_bounds__(512) void rowgemm_res_kernel(RowGemmParams p) {
-  constexpr int K = 32 * KS, N = 64 * NP, LDW = K + 8;
+template <int DACT, int KS, int NP, int NWV>
+__global__ __launch_bounds__(64 * NWV) void rowgemm_res_kernel(RowGemmParams p) {
+  constexpr int NT = 64 * NWV, K = 32 * KS, N = 64 * NP, LDW = K + 8;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[N * LDW];
   __shared__ __attribute__((aligned(16))) float Bs[N];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
-  const int ntiles = (p.rows + 15) >> 4, nw = (int)gridDim.x * 8;
+  const int ntiles = (p.rows + 15) >> 4, nw = (int)gridDim.x * NWV;
   auto aload = [&](int tl, h8 (&a)[KS]) __attribute__((always_inline)) {
     const int row = min(tl * 16 + r16, p.rows - 1);
     const _Float16* ar = p.A + (size_t)row * p.K + kq;
 #pragma unroll
     for (int j = 0; j < KS; ++j) a[j] = *reinterpret_cast<const h8*>(ar + 32 * j);
   };
-  int tile = (int)blockIdx.x * 8 + wave;
+  int tile = (int)blockIdx.x * NWV + wave;
   h8 a[KS];
   aload(tile < ntiles ? tile : 0, a);
   // the whole W, 16-byte pieces of E[n][k] (row pitch p.w.kp >= K)
-  for (int i = tid; i < N * K / 8; i += 512) {
+  for (int i = tid; i < N * K / 8; i += NT) {
     const int n = i / (K / 8), k = (i - n * (K / 8)) * 8;
     const uint4 v = n < p.w.N ? *reinterpret_cast<const uint4*>(p.w.p + (size_t)n * p.w.kp + k) : make_uint4(0, 0, 0, 0);
     *reinterpret_cast<uint4*>(Ws + n * LDW + k) = v;
   }
-  for (int i = tid; i < N; i += 512) Bs[i] = (p.bias && i < p.N) ? p.bias[i] : 0.f;
+  for (int i = tid; i < N; i += NT) Bs[i] = (p.bias && i < p.N) ? p.bias[i] : 0.f;
   __syncthreads();
   for (; tile < ntiles; tile += nw) {
     const int row = tile * 16 + r16;
@@ -704,6 +704,22 @@ __global__ __launch_bounds__(512) void rowgemm_res_kernel(RowGemmParams p) {
   }
 }
 
+// As many blocks as are resident at once (the tiles are dealt out by block id, so every
+// launched block must be resident together).
+template <int DACT, int KS, int NP>
+static void launch_rowgemm_res(lf_context* ctx, const RowGemmParams& p) {
+  constexpr int NWV = 8;   // 12 measured no faster at config 4, 16 slower
+  static const int per_cu = [] {
+    int n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, rowgemm_res_kernel<DACT, KS, NP, NWV>, 64 * NWV, 0) !=
+        hipSuccess)
+      n = 1;
+    return n < 1 ? 1 : n;
+  }();
+  const dim3 g((unsigned)std::min((p.rows + 16 * NWV - 1) / (16 * NWV), per_cu * ctx->num_cus));
+  hipLaunchKernelGGL((rowgemm_res_kernel<DACT, KS, NP, NWV>), g, dim3(64 * NWV), 0, ctx->stream, p);
+}
+
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   if (p.rows <= 0) return LF_OK;
   const std::string l(label);
@@ -718,9 +734,7 @@ int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   const int np = p.N / 64, ks = p.K / 32;
   if (p.N % 64 == 0 && p.K % 32 == 0 && (np == 2 || np == 4) && (ks == 4 || ks == 8) && p.w.kp >= p.K &&
       p.dst.D >= 64 * np && (p.rows + 15) / 16 >= 8 * ctx->num_cus) {
-    const int per_cu = np * ks <= 8 ? 2 : 1;   // LDS: 34 KB (128 x 128) or up to 132 KB
-    dim3 g((unsigned)std::min((p.rows + 127) / 128, per_cu * ctx->num_cus));
-#define LF_RR(D, KS_, NP_) hipLaunchKernelGGL((rowgemm_res_kernel<D, KS_, NP_>), g, dim3(512), 0, ctx->stream, p)
+#define LF_RR(D, KS_, NP_) launch_rowgemm_res<D, KS_, NP_>(ctx, p)
 #define LF_RRD(D)                                      \
   if (ks == 4 && np == 2) LF_RR(D, 4, 2);               \
   else if (ks == 4) LF_RR(D, 4, 4);                     \
