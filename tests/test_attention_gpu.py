@@ -129,6 +129,35 @@ def test_accumulate_in_place_transposed(ctx, blockw):
     H.assert_close(z.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("act_dt", ["float32", "bfloat16"])
+def test_output_projection_many_rows(ctx, blockw, transpose, act_dt):
+    """131 x 257 = 33667 rows (above 8 waves x 16 rows per CU, and not a multiple of 16): the
+    output projection runs as the weight-resident row GEMM and ends on a partial tile; the
+    update is accumulated in place, through the transposed row map for column attention."""
+    import torch
+    from localfold_amd import device as D
+    s, n = 131, 257
+    act = S.synthetic_activations(s, n, 256, 128, seed=21)
+    mask = act["msaMask"].copy()
+    mask[:, -5:] = 0
+    col = blockw["msaColumnAttention"]
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, col["attention"])
+    x = _dev(ctx, act["msa"], getattr(torch, act_dt))
+    ain = x.float().cpu().numpy()
+    D.attention(ctx, x, _dev(ctx, mask), ws, 8, transpose, out=x, accumulate=True)
+    torch.cuda.synchronize()
+    ref = ain.astype(np.float64) + ops.attention_af2(ain, mask, col["attention"], 8, transpose)
+    m = H.metrics(x.float().cpu().numpy(), ref)
+    print(f"{act_dt} transpose={transpose}: {m}", flush=True)
+    if act_dt == "float32":
+        H.assert_close(x.cpu().numpy(), ref, label=f"many rows {act_dt} {transpose}")
+    else:   # bf16 storage of the result: its rounding (|x| ~ 4, 2^-9 relative) on top of the bound
+        H.assert_close(x.float().cpu().numpy(), ref, max_abs=H.MAX_ABS + float(np.abs(ref).max()) * 2.0 ** -8,
+                       label=f"many rows {act_dt} {transpose}")
+
+
 @pytest.mark.parametrize("transpose,swap", [(False, False), (True, False), (True, True)])
 def test_af3_grid_attention(ctx, transpose, swap):
     from localfold_amd import capi, device as D
