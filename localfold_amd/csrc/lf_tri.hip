@@ -997,10 +997,13 @@ template <int ACT, int NWV>
 __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectParams p) {
   constexpr int NT = 64 * NWV;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate', b-proj, b-gate' [h][k]
-  __shared__ __attribute__((aligned(16))) float Bs[4 * 128];              // the four bias vectors (gates scaled)
+  __shared__ __attribute__((aligned(16))) h4 Bt[4 * 128];                 // the four bias vectors (gates scaled), f16 hi + lo
   __shared__ __attribute__((aligned(16))) float Gs[2 * 128];              // LN_in scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4, q4 = g4 * 4, kq = g4 * 8;
+  // A operand of the bias MFMA: ones at k = 0, 1 (lanes 0-15 supply k 0..3), zeros elsewhere
+  const _Float16 one = (_Float16)(g4 == 0 ? 1.f : 0.f);
+  const h4 ones = h4{one, one, (_Float16)0.f, (_Float16)0.f};
   const int ntiles = p.kmajor_out ? p.N * (p.N >> 4) : p.P >> 4, nw = gridDim.x * NWV;
   auto fetch = [&](int tl, FragTile<ACT, 4>& t, float (&m)[4]) __attribute__((always_inline)) {
     const TileGeom g = tile_geom(p, tl);
@@ -1014,11 +1017,17 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   float mc[4];
   fetch(tile < ntiles ? tile : 0, tc, mc);
   stage_project_weights<NT>(Ws, p, tid);
+  // a bias b as the B operand of a 16x16x16 MFMA: k rows 0 and 1 hold hi = f16(b) and
+  // lo = f16(b - hi), which the ones in the A operand sum back to b within 2^-22 relative
+  auto split = [](float b) {
+    const _Float16 hi = (_Float16)b;
+    return h4{hi, (_Float16)(b - (float)hi), (_Float16)0.f, (_Float16)0.f};
+  };
   for (int i = tid; i < 128; i += NT) {
-    Bs[i] = p.bp[0] ? p.bp[0][i] : 0.f;
-    Bs[128 + i] = p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f;
-    Bs[256 + i] = p.bp[1] ? p.bp[1][i] : 0.f;
-    Bs[384 + i] = p.bg[1] ? TRI_NLOG2E * p.bg[1][i] : 0.f;
+    Bt[i] = split(p.bp[0] ? p.bp[0][i] : 0.f);
+    Bt[128 + i] = split(p.bg[0] ? TRI_NLOG2E * p.bg[0][i] : 0.f);
+    Bt[256 + i] = split(p.bp[1] ? p.bp[1][i] : 0.f);
+    Bt[384 + i] = split(p.bg[1] ? TRI_NLOG2E * p.bg[1][i] : 0.f);
   }
   stage_vec(Gs, p.ln_s, 128, 1.f, 128, tid, NT);
   stage_vec(Gs + 128, p.ln_o, 128, 0.f, 128, tid, NT);
@@ -1026,6 +1035,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   if (tile >= ntiles) return;
   for (; tile < ntiles; tile += nw) {
     const int out0 = tile_geom(p, tile).out0;
+    const uint32_t lofs = ((uint32_t)r16 * (uint32_t)p.P + (uint32_t)(out0 + q4)) * (uint32_t)sizeof(_Float16);
     h8 xa[4];
     frag_ln_raw1(tc, xa, 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
     const int nt = tile + nw < ntiles ? tile + nw : tile;   // the last step reloads its own tile
@@ -1036,14 +1046,13 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
       constexpr int PS = decltype(pass_tag)::value, which = PS >> 1, hh = (PS & 1) * 64;
       const _Float16* Wp = Ws + (which * 2) * 128 * RS_LD;
       const _Float16* Wg = Wp + 128 * RS_LD;
-      const float* bp = Bs + which * 256 + hh;
-      const float* bg = bp + 128;
+      // the accumulators start at the biases, through the matrix core (no per-register moves)
+      const h4* btp = Bt + which * 256 + hh + r16;
       f4 acc[8];
 #pragma unroll
       for (int t4 = 0; t4 < 4; ++t4) {
-        const float b0 = bp[t4 * 16 + r16], b1 = bg[t4 * 16 + r16];
-        acc[t4] = f4{b0, b0, b0, b0};
-        acc[4 + t4] = f4{b1, b1, b1, b1};
+        acc[t4] = mfma16k16(ones, btp[t4 * 16], f4{0.f, 0.f, 0.f, 0.f});
+        acc[4 + t4] = mfma16k16(ones, btp[128 + t4 * 16], f4{0.f, 0.f, 0.f, 0.f});
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -1061,15 +1070,16 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
         launder(tn);
         asm volatile("" : "+v"(mn[0]), "+v"(mn[1]), "+v"(mn[2]), "+v"(mn[3]));
       }
-      _Float16* dst = which ? p.out[1] : p.out[0];
+      // a wave-uniform base per 16 channels plus one 32-bit lane offset (P < 2^27): scalar
+      // base + vector offset stores, no 64-bit address arithmetic per store
+      char* dst = reinterpret_cast<char*>(which ? p.out[1] : p.out[0]);
 #pragma unroll
       for (int t4 = 0; t4 < 4; ++t4) {
-        const int h = hh + t4 * 16 + r16;
         h4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           o[i] = (_Float16)(mc[i] * acc[t4][i] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(acc[4 + t4][i])));
-        *reinterpret_cast<h4*>(dst + (size_t)h * p.P + out0 + q4) = o;
+        *reinterpret_cast<h4*>(dst + (size_t)(hh + t4 * 16) * p.P * sizeof(_Float16) + lofs) = o;
       }
     };
     pass(std::integral_constant<int, 0>{});
@@ -1281,7 +1291,7 @@ static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool res
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_P_NWV - 1) / TRI_P_NWV)));
     const bool whole = pp.kmajor_out ? pp.N % 16 == 0 : P % 16 == 0;
-    if (whole)
+    if (whole && P < (1 << 27))   // 32-bit per-lane store offsets
       hipLaunchKernelGGL((tri_project_v3_kernel<ACT, TRI_P_NWV>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
     else
       hipLaunchKernelGGL((tri_project_v2_kernel<ACT, TRI_P_NWV, TRI_P_TPW>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
