@@ -280,13 +280,14 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], in
 // chunks of 64 are staged in double-buffered LDS two chunks ahead (K rows, V^T rows, key
 // bias); the pair-bias values a lane needs come straight from global memory, also ahead.
 //
-// Online softmax with a lazy running max: after the first chunk, the S accumulators start at
-// bias - m (m = the query's running max), so the MFMA yields x - m directly; when no query's
-// maximum rose by more than FA_RESCALE (a wave-uniform vote) p = exp2(x - m) needs no
-// subtraction and O no rescale: the standard update with a stale max m, which only scales
-// numerator and denominator alike.  Otherwise (and in the first
-// chunk, and in chunks holding masked or past-the-end keys) the general update runs.  The
-// row sums come from the PV MFMAs themselves, through an all-ones operand (third d tile).
+// Online softmax with a lazy running max: the S accumulators start at bias - m (m = the
+// query's running max, 0 before the first chunk), so the MFMA yields x - m directly; when no
+// query's maximum rose by more than FA_RESCALE (a wave-uniform vote; in the first chunk, or
+// lies more than FA_RESCALE below 0) p = exp2(x - m) needs no subtraction and O no rescale:
+// the standard update with a stale max m, which only scales numerator and denominator alike.
+// Otherwise m moves to the new maximum (O rescaled).  Chunks holding masked or past-the-end
+// keys take the general update (explicit key bias, clamp, max).  The row sums come from the
+// PV MFMAs themselves, through an all-ones operand (third d tile).
 //
 // Key order within a chunk: row 4*g + i of S^T tile kt is key 16*g + 4*kt + i (K rows are
 // stored to LDS in that order), so the 16 scores a lane holds per query are the contiguous
@@ -400,7 +401,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       const int cn = c + 2 < nkc ? c + 2 : nkc - 1;
       if constexpr (rs == 0) kv_load(cn, st0, kb0);
       else kv_load(cn, st1, kb1);
-      const bool general = c == 0 || Kmasked[buf] != 0;   // wave-uniform
+      const bool general = Kmasked[buf] != 0;   // wave-uniform
       _Float16 pv[QT][4][4];
       if (general) {
         f4 s[QT][4];
@@ -441,9 +442,12 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       } else {
         // S accumulators start at bias - m, so the MFMA yields x - m; the bias lands through an
         // identity MFMA (D = I B + C, B = the lane's bias h4 in the accumulator layout)
+        // (a first chunk measures against m = 0 and re-bases on its own maximum below unless
+        // that lies within FA_RESCALE of 0)
         f4 s[QT][4];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
+          if (c == 0) m_run[qt] = 0.f;
           const f4 negm = f4{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) s[qt][kt] = BIAS ? mfma16k16(ident, bq[qt][kt], negm) : negm;
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) v = fmaxf(v, s[qt][kt][i]);
           mx[qt] = v;
-          rose |= v > FA_RESCALE;
+          rose |= v > FA_RESCALE || (c == 0 && v < -FA_RESCALE);
         }
         if (!__any(rose)) {
 #pragma unroll
@@ -476,8 +480,10 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         } else {
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
-            const float d = fmaxf(lanes4_max(mx[qt]), 0.f);   // rise of this query's max
-            const float corr = __builtin_amdgcn_exp2f(-d);
+            // rise of this query's max (in a first chunk the offset from 0 either way, with
+            // nothing accumulated to rescale)
+            const float d = c == 0 ? lanes4_max(mx[qt]) : fmaxf(lanes4_max(mx[qt]), 0.f);
+            const float corr = c == 0 ? 1.f : __builtin_amdgcn_exp2f(-d);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
