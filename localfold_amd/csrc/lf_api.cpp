@@ -49,6 +49,31 @@ int workspace(lf_context* ctx, const size_t* sizes, void** out, int n) {
   return LF_OK;
 }
 
+int mask_table(lf_context* ctx, const void* mask, int kind, long long a, long long b, float f, size_t bytes,
+               void** out, bool* filled) {
+  *out = nullptr;
+  *filled = false;
+  if (ctx->mask_scope <= 0) return LF_OK;
+  for (auto& t : ctx->mask_tables)
+    if (t.valid && t.mask == mask && t.kind == kind && t.a == a && t.b == b && t.f == f && t.bytes >= bytes) {
+      *out = t.buf;
+      *filled = true;
+      return LF_OK;
+    }
+  for (auto& t : ctx->mask_tables)   // a buffer of an earlier scope
+    if (!t.valid && t.bytes >= bytes) {
+      t = lf_context::MaskTable{mask, kind, a, b, f, true, t.buf, t.bytes};
+      *out = t.buf;
+      return LF_OK;
+    }
+  void* buf = nullptr;
+  LF_TRY(check_hip(hipMalloc(&buf, bytes), "mask table allocation"));
+  ctx->mask_tables.push_back(lf_context::MaskTable{mask, kind, a, b, f, true, buf, bytes});
+  ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->user_bytes + ctx->ws_bytes);
+  *out = buf;
+  return LF_OK;
+}
+
 LaunchScope::LaunchScope(lf_context* c, const char* label) : ctx(c) {
   if (!ctx->profile) return;
   lf_context::Rec r;
@@ -183,6 +208,7 @@ void lf_context_destroy(lf_context* ctx) {
     hipEventDestroy(r.stop);
   }
   for (auto& a : ctx->user_allocs) hipFree(a.first);
+  for (auto& t : ctx->mask_tables) hipFree(t.buf);
   if (ctx->ws) hipFree(ctx->ws);
   if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
   delete ctx;

@@ -692,17 +692,27 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
   }
 
-  // 3. key-mask bias, f16 copy of the pair bias
+  // 3. key-mask bias (inside a stack call, computed by the first block and reused), f16 copy
+  // of the pair bias
   {
-    LaunchScope ls(ctx, "attention.keybias");
-    if (shared_key_mask)
-      hipLaunchKernelGGL(keymax_kernel, dim3((unsigned)(Qp / 64)), dim3(1024), 0, ctx->stream, a.mask, keyb, B, Q,
-                         Qp);
-    else
-      hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0,
-                         ctx->stream, a.mask, keyb, B, Q, Qp, a.transpose);
+    void* cached;
+    bool filled;
+    LF_TRY(mask_table(ctx, a.mask, shared_key_mask ? 1 : 2 + (a.transpose ? 1 : 0), B, Q, 0.f, sizes[5], &cached,
+                      &filled));
+    if (cached) keyb = static_cast<float*>(cached);
+    if (!filled) {
+      {
+        LaunchScope ls(ctx, "attention.keybias");
+        if (shared_key_mask)
+          hipLaunchKernelGGL(keymax_kernel, dim3((unsigned)(Qp / 64)), dim3(1024), 0, ctx->stream, a.mask, keyb, B,
+                             Q, Qp);
+        else
+          hipLaunchKernelGGL(keybias_kernel, dim3((unsigned)(((long long)B * Qp + 255) / 256)), dim3(256), 0,
+                             ctx->stream, a.mask, keyb, B, Q, Qp, a.transpose);
+      }
+      LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
+    }
   }
-  LF_TRY(check_hip(hipGetLastError(), "keybias launch"));
   // caller-supplied f32 logits are converted (and transposed per head when swapped); the
   // projected biases were written as f16 by lnproj
   if (a.bias_mode == LF_BIAS_LOGITS)

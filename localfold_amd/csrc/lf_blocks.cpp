@@ -428,6 +428,7 @@ int lf_af2_recycle(lf_context* ctx, const lf_af2_recycle_args* args) {
     lf::StageScope stage(ctx, "input_embedder");
     LF_TRY(lf::input_embedder(ctx, a.embed));
   }
+  lf::MaskScope masks(ctx);   // the stacks' masks are inputs: their derived tables, once
   for (int b = 0; b < a.extra_block_count; ++b)
     LF_TRY(lf::evoformer_block(ctx, a.extra, a.extra_blocks[b].base, &a.extra_blocks[b].column_global,
                                a.extra_blocks[b].column_global_heads));
@@ -452,6 +453,7 @@ int lf_evoformer_stack(lf_context* ctx, const lf_evoformer_block_args* args, con
   if (!ctx || !args || (!blocks && block_count > 0)) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_stack: NULL argument");
   if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_stack: negative block count");
   hipSetDevice(ctx->device);
+  lf::MaskScope masks(ctx);   // the masks' key-bias rows and OPM normalisers, once per stack
   for (int i = 0; i < block_count; ++i) LF_TRY(lf::evoformer_block(ctx, *args, blocks[i]));
   return LF_OK;
 }
@@ -467,6 +469,7 @@ int lf_extra_msa_stack(lf_context* ctx, const lf_evoformer_block_args* args, con
   if (!ctx || !args || (!blocks && block_count > 0)) return lf::set_error(LF_ERR_INVALID, "lf_extra_msa_stack: NULL argument");
   if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_extra_msa_stack: negative block count");
   hipSetDevice(ctx->device);
+  lf::MaskScope masks(ctx);
   for (int b = 0; b < block_count; ++b)
     LF_TRY(lf::evoformer_block(ctx, *args, blocks[b].base, &blocks[b].column_global, blocks[b].column_global_heads));
   return LF_OK;

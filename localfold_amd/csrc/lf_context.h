@@ -19,6 +19,21 @@ struct lf_context {
   // caller allocations through lf_malloc
   size_t user_bytes = 0, peak_bytes = 0, alloc_count = 0;
   std::vector<std::pair<void*, size_t>> user_allocs;
+  // Tables derived from a mask alone (attention key-bias rows, OPM pair normalisers), kept
+  // while `mask_scope` > 0 -- a stack call, whose masks do not change -- so that the later
+  // blocks reuse the first block's tables instead of recomputing them.  The buffers are kept
+  // for the context's lifetime and refilled by the next scope.
+  struct MaskTable {
+    const void* mask;
+    int kind;
+    long long a, b;
+    float f;
+    bool valid;
+    void* buf;
+    size_t bytes;
+  };
+  int mask_scope = 0;
+  std::vector<MaskTable> mask_tables;
   // profiling
   bool profile = false;
   const char* label_prefix = nullptr;   // block stage naming the launches (profiling only)
@@ -37,6 +52,22 @@ int check_hip(hipError_t e, const char* what);
 // Carves `n` buffers from the context workspace (256-byte aligned), growing it if needed.
 // Growing synchronises the stream first, so earlier kernels finish with the old buffer.
 int workspace(lf_context* ctx, const size_t* sizes, void** out, int n);
+
+// A table derived from `mask` (kind and shape a, b, f) for the current stack scope: returns
+// its buffer in *out, and whether it is already filled (*filled; false: the caller computes it
+// into *out now).  Outside a stack scope *out is null and the caller uses its workspace.
+int mask_table(lf_context* ctx, const void* mask, int kind, long long a, long long b, float f, size_t bytes,
+               void** out, bool* filled);
+
+// Opens a stack scope for mask tables (nested scopes share the outer one).
+struct MaskScope {
+  lf_context* ctx;
+  explicit MaskScope(lf_context* c) : ctx(c) { ++c->mask_scope; }
+  ~MaskScope() {
+    if (--ctx->mask_scope == 0)
+      for (auto& t : ctx->mask_tables) t.valid = false;
+  }
+};
 
 // Brackets a kernel launch with events when profiling is on.
 struct LaunchScope {

@@ -476,12 +476,20 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   pp.g[0].dst = Dst{L, DT_F16, S, (long long)co * S, 1, co, 0, S};
   pp.g[1].dst = Dst{R, DT_F16, S, (long long)co * S, 1, co, 0, S};
   LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, bufs[5], "opm.project"));
-  {
-    LaunchScope ls(ctx, "opm.count");
-    hipLaunchKernelGGL(opm_count_kernel, dim3((N + 15) / 16, (N + 15) / 16), dim3(256), 0, ctx->stream, a.mask, den,
-                       S, N, a.norm_epsilon);
+  {  // the pair normalisers (inside a stack call, computed by the first block and reused)
+    void* cached;
+    bool filled;
+    LF_TRY(mask_table(ctx, a.mask, 10, S, N, a.norm_epsilon, sizes[3], &cached, &filled));
+    if (cached) den = static_cast<float*>(cached);
+    if (!filled) {
+      {
+        LaunchScope ls(ctx, "opm.count");
+        hipLaunchKernelGGL(opm_count_kernel, dim3((N + 15) / 16, (N + 15) / 16), dim3(256), 0, ctx->stream, a.mask,
+                           den, S, N, a.norm_epsilon);
+      }
+      LF_TRY(check_hip(hipGetLastError(), "opm count launch"));
+    }
   }
-  LF_TRY(check_hip(hipGetLastError(), "opm count launch"));
   if (fused) {
     OpmFusedParams f{OuterParams{L, R, nullptr, N, co, S}, wo.p, wo.kp, w.bo, den,
                      a.accumulate ? a.pair_in : nullptr, a.out};
