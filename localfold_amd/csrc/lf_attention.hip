@@ -598,7 +598,7 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   const size_t hd = (size_t)rows * HD * sizeof(_Float16);
   const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Qp * sizeof(_Float16);
   // buffers: q, k, v, g, o, key bias, f16 pair bias, output weights, packed lnproj weights x 2
-  void* bufs[9];
+  void* bufs[10];
 
   // 1. pair bias from a separate pair tensor: bias[h][i][j] = LN(pair_ij) . W[:, h]
   LnProjParams pb{};
@@ -653,16 +653,18 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   const bool pwa = no_qk && shared_key_mask && d % 4 == 0 && !a.transpose && a.bias_mode != LF_BIAS_NONE;
   const size_t vsize = pwa ? (size_t)B * HD * Qp * sizeof(_Float16) : qkv;
   const size_t qksize = pwa ? 256 : qkv;
-  size_t sizes[9] = {qksize, qksize, vsize, hd, hd, (size_t)(shared_key_mask ? 1 : B) * Qp * sizeof(float), biash, expanded_bytes(views[4]),
-                     std::max(lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb)
-                                                                                       : (size_t)0)};
-  LF_TRY(workspace(ctx, sizes, bufs, 9));
+  size_t sizes[10] = {qksize, qksize, vsize, hd, hd, (size_t)(shared_key_mask ? 1 : B) * Qp * sizeof(float), biash, expanded_bytes(views[4]),
+                     lnproj_packed_bytes(pp), a.bias_mode == LF_BIAS_SEPARATE ? lnproj_packed_bytes(pb) : (size_t)0};
+  LF_TRY(workspace(ctx, sizes, bufs, 10));
   _Float16 *qb = (_Float16*)bufs[0], *kb = (_Float16*)bufs[1], *vb = (_Float16*)bufs[2];
   _Float16 *gb = (_Float16*)bufs[3], *ob = (_Float16*)bufs[4];
   float* keyb = (float*)bufs[5];
   _Float16* bias16 = (_Float16*)bufs[6];
+  // every weight of the op (output projection, pair-bias and q/k/v/g projections) decoded
+  // in one launch
+  ExpandList xl;
   WExp wo;
-  LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[7], &wo, "attention.expand"));
+  LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[7], &wo, 1.f, "attention.expand"));
   // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
   // exact 0, which must not meet a non-finite value)
   if (pwa) {
@@ -677,7 +679,7 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
                                    : Dst{bias16, DT_F16, Q, Qp, 1, 1, (long long)Q * Qp, 0};
   if (a.bias_mode == LF_BIAS_SEPARATE) {
     pb.g[0].dst = bias_dst;
-    LF_TRY(launch_lnproj(ctx, pb, a.pair_dtype, bufs[8], "attention.pair_bias"));
+    LF_TRY(lnproj_prepare(ctx, pb, bufs[9], &xl, "attention.pair_bias"));
   }
   {
     const long long hq = (long long)Qp * FA_DP;
@@ -689,8 +691,11 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     // which is then whole lines
     pp.g[gg].dst = Dst{gb, DT_F16, Q, (long long)Q * d, d, d, (long long)B * Q * d, 1};
     if (gbias >= 0) pp.g[gbias].dst = bias_dst;
-    LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[8], "attention.project"));
+    LF_TRY(lnproj_prepare(ctx, pp, bufs[8], &xl, "attention.project"));
   }
+  LF_TRY(expand_flush(ctx, xl, "attention.expand"));
+  if (a.bias_mode == LF_BIAS_SEPARATE) LF_TRY(lnproj_run(ctx, pb, a.pair_dtype, "attention.pair_bias"));
+  LF_TRY(lnproj_run(ctx, pp, a.act_dtype, "attention.project"));
 
   // 3. key-mask bias (inside a stack call, computed by the first block and reused), f16 copy
   // of the pair bias

@@ -38,55 +38,60 @@ __global__ __launch_bounds__(256) void expand_weights_kernel(ExpandBatch b) {
   }
 }
 
+int expand_flush(lf_context* ctx, ExpandList& l, const char* label) {
+  if (l.b.count == 0) return LF_OK;
+  {
+    LaunchScope ls(ctx, label);
+    dim3 grid((unsigned)std::min<long>(std::max<long>((l.most / 8 + 255) / 256, 1), 1024), l.b.count);
+    hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, l.b);
+  }
+  l = ExpandList{};
+  return check_hip(hipGetLastError(), "expand launch");
+}
+
+static int expand_add(lf_context* ctx, ExpandList& l, const WView& v, _Float16* dst, int kp, int W, int off, int ncols,
+                      float scale, const char* label) {
+  if (l.b.count == 8) LF_TRY(expand_flush(ctx, l, label));
+  const int i = l.b.count++;
+  l.b.v[i] = v;
+  l.b.dst[i] = dst;
+  l.b.kp[i] = kp;
+  l.b.W[i] = W;
+  l.b.off[i] = off;
+  l.b.ncols[i] = ncols;
+  l.b.scale[i] = scale;
+  l.most = std::max(l.most, (long)ncols * kp);
+  return LF_OK;
+}
+
+int expand_add_plain(lf_context* ctx, ExpandList& l, const WView& v, void* dst, WExp* out, float scale,
+                     const char* label) {
+  const int kp = (v.K + 31) & ~31;
+  *out = WExp{static_cast<_Float16*>(dst), kp, v.N};
+  return expand_add(ctx, l, v, static_cast<_Float16*>(dst), kp, std::max(v.N, 1), 0, v.N, scale, label);
+}
+
+int expand_add_packed(lf_context* ctx, ExpandList& l, const WView* views, const int* W, const int* off,
+                      const long long* row0, int count, _Float16* dst, int kp, const char* label) {
+  for (int m = 0; m < count; ++m)
+    LF_TRY(expand_add(ctx, l, views[m], dst + row0[m] * kp, kp, W[m], off[m], (views[m].N + W[m] - 1) / W[m] * W[m],
+                      1.f, label));
+  return LF_OK;
+}
+
 int expand_weights(lf_context* ctx, const WView* views, int count, void* const* dst, WExp* out, const char* label,
                    const float* scales) {
-  for (int base = 0; base < count; base += 8) {
-    ExpandBatch b{};
-    b.count = std::min(8, count - base);
-    long most = 0;
-    for (int i = 0; i < b.count; ++i) {
-      const WView& v = views[base + i];
-      b.v[i] = v;
-      b.kp[i] = (v.K + 31) & ~31;
-      b.dst[i] = static_cast<_Float16*>(dst[base + i]);
-      b.W[i] = std::max(v.N, 1);
-      b.off[i] = 0;
-      b.scale[i] = scales ? scales[base + i] : 1.f;
-      b.ncols[i] = v.N;
-      out[base + i] = WExp{b.dst[i], b.kp[i], v.N};
-      most = std::max(most, (long)v.N * b.kp[i]);
-    }
-    LaunchScope ls(ctx, label);
-    dim3 grid((unsigned)std::min<long>((most / 8 + 255) / 256, 1024), b.count);
-    hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
-    LF_TRY(check_hip(hipGetLastError(), "expand_weights launch"));
-  }
-  return LF_OK;
+  ExpandList l;
+  for (int i = 0; i < count; ++i)
+    LF_TRY(expand_add_plain(ctx, l, views[i], dst[i], &out[i], scales ? scales[i] : 1.f, label));
+  return expand_flush(ctx, l, label);
 }
 
 int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
                   int count, _Float16* dst, int kp, const char* label) {
-  for (int base = 0; base < count; base += 8) {
-    ExpandBatch b{};
-    b.count = std::min(8, count - base);
-    long most = 0;
-    for (int i = 0; i < b.count; ++i) {
-      const int m = base + i;
-      b.v[i] = views[m];
-      b.kp[i] = kp;
-      b.dst[i] = dst + row0[m] * kp;
-      b.W[i] = W[m];
-      b.off[i] = off[m];
-      b.scale[i] = 1.f;
-      b.ncols[i] = (views[m].N + W[m] - 1) / W[m] * W[m];
-      most = std::max(most, (long)b.ncols[i] * kp);
-    }
-    LaunchScope ls(ctx, label);
-    dim3 grid((unsigned)std::min<long>((most / 8 + 255) / 256, 1024), b.count);
-    hipLaunchKernelGGL(expand_weights_kernel, grid, dim3(256), 0, ctx->stream, b);
-    LF_TRY(check_hip(hipGetLastError(), "expand_packed launch"));
-  }
-  return LF_OK;
+  ExpandList l;
+  LF_TRY(expand_add_packed(ctx, l, views, W, off, row0, count, dst, kp, label));
+  return expand_flush(ctx, l, label);
 }
 
 // dst = (f16) (scale * src), n elements; with tq > 0 every [tq][tq] plane is transposed.

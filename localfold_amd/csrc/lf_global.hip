@@ -214,7 +214,13 @@ int global_attention(lf_context* ctx, const lf_global_attention_args& a) {
   pp.g[1].dst = Dst{K, DT_F16, N, (long long)d, (long long)S * d, d, 0, 1};
   pp.g[2].dst = Dst{V, DT_F16, N, (long long)d, (long long)S * d, d, 0, 1};
   pp.g[3].dst = dst_rowmajor(G, DT_F16, (int)rows, Hd);
-  LF_TRY(launch_lnproj(ctx, pp, a.act_dtype, bufs[5], "global.project"));
+  // the projections and the output weights decoded in one launch
+  ExpandList xl;
+  WExp wo;
+  LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[4], &wo, 1.f, "global.expand"));
+  LF_TRY(lnproj_prepare(ctx, pp, bufs[5], &xl, "global.project"));
+  LF_TRY(expand_flush(ctx, xl, "global.expand"));
+  LF_TRY(lnproj_run(ctx, pp, a.act_dtype, "global.project"));
 
   GlobalColumnParams gp{QM, K, V, G, a.mask, S, N, H, d, 1.f / std::sqrt((float)d)};
   {
@@ -225,8 +231,6 @@ int global_attention(lf_context* ctx, const lf_global_attention_args& a) {
   }
   LF_TRY(check_hip(hipGetLastError(), "global column launch"));
 
-  WExp wo;
-  LF_TRY(expand_weights(ctx, &views[4], 1, &bufs[4], &wo, "global.expand"));
   RowGemmParams rp{};
   rp.A = G;
   rp.rows = (int)rows;

@@ -470,12 +470,16 @@ int outer_product_mean(lf_context* ctx, const lf_opm_args& a) {
   LF_TRY(workspace(ctx, sizes, bufs, 6));
   _Float16 *L = (_Float16*)bufs[0], *R = (_Float16*)bufs[1], *O = (_Float16*)bufs[2];
   float* den = (float*)bufs[3];
+  // the output projection and the l / r projections decoded in one launch
+  ExpandList xl;
   WExp wo;
-  LF_TRY(expand_weights(ctx, &views[2], 1, &bufs[4], &wo, "opm.expand"));
+  LF_TRY(expand_add_plain(ctx, xl, views[2], bufs[4], &wo, 1.f, "opm.expand"));
   // logical row r = i*S + s, column a -> (i*co + a)*S + s
   pp.g[0].dst = Dst{L, DT_F16, S, (long long)co * S, 1, co, 0, S};
   pp.g[1].dst = Dst{R, DT_F16, S, (long long)co * S, 1, co, 0, S};
-  LF_TRY(launch_lnproj(ctx, pp, a.msa_dtype, bufs[5], "opm.project"));
+  LF_TRY(lnproj_prepare(ctx, pp, bufs[5], &xl, "opm.project"));
+  LF_TRY(expand_flush(ctx, xl, "opm.expand"));
+  LF_TRY(lnproj_run(ctx, pp, a.msa_dtype, "opm.project"));
   {  // the pair normalisers (inside a stack call, computed by the first block and reused)
     void* cached;
     bool filled;

@@ -27,6 +27,18 @@ size_t expanded_bytes(const WView& v);
 // row0[m] + (n / W[m]) * 64 + off[m] + n % W[m], pitch kp, padding columns zeroed.
 int expand_packed(lf_context* ctx, const WView* views, const int* W, const int* off, const long long* row0,
                   int count, _Float16* dst, int kp, const char* label);
+// Expansions collected for one launch: an op queues every matrix it decodes (plain views
+// and packed chunk layouts alike), then flushes once -- one expand launch per op instead of
+// one per weight group.  A full batch (8 matrices) launches as it fills.
+struct ExpandList {
+  ExpandBatch b{};
+  long most = 0;
+};
+int expand_add_plain(lf_context* ctx, ExpandList& l, const WView& v, void* dst, WExp* out, float scale,
+                     const char* label);
+int expand_add_packed(lf_context* ctx, ExpandList& l, const WView* views, const int* W, const int* off,
+                      const long long* row0, int count, _Float16* dst, int kp, const char* label);
+int expand_flush(lf_context* ctx, ExpandList& l, const char* label);
 // dst = scale * src as f16; tq > 0 transposes each tq x tq plane; ld > 0 writes rows of rowlen
 // values at a row stride of ld
 int f32_to_f16(lf_context* ctx, const float* src, _Float16* dst, long long n, int tq, float scale = 1.f,

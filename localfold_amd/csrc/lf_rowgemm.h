@@ -83,6 +83,11 @@ struct RowGemmParams {
 // the same weights (row chunks) pass decode = false after the first.
 size_t lnproj_packed_bytes(const LnProjParams& p);
 int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode = true);
+// launch_lnproj in two steps, so that an op decodes all its weights in one launch: prepare
+// validates p, fills its chunk tables and queues the decode of its weights into `packed` on
+// xl (null: the caller decoded them before); run launches the kernel once they are decoded.
+int lnproj_prepare(lf_context* ctx, LnProjParams& p, void* packed, ExpandList* xl, const char* label);
+int lnproj_run(lf_context* ctx, const LnProjParams& p, int act, const char* label);
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label);
 
 inline Dst dst_rowmajor(void* ptr, int dtype, int rows, int cols) {

@@ -340,7 +340,7 @@ size_t lnproj_packed_bytes(const LnProjParams& p) {
   return (size_t)lnproj_chunks(p) * 64 * 32 * lnproj_ks(p.C) * sizeof(_Float16);
 }
 
-int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode) {
+int lnproj_prepare(lf_context* ctx, LnProjParams& p, void* packed, ExpandList* xl, const char* label) {
   if (p.C > 384) return set_error(LF_ERR_INVALID, std::string(label) + ": LayerNorm width above 384");
   if (p.rows <= 0) return LF_OK;
   if (!packed) return set_error(LF_ERR_INVALID, std::string(label) + ": no packed-weight workspace");
@@ -392,9 +392,14 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
       p.chunk_c0[p.nchunks++] = c0;
     }
   }
-  if (decode)
-    LF_TRY(expand_packed(ctx, views, W, off, row0, nv, static_cast<_Float16*>(packed), KP,
-                       (std::string(label) + ".expand").c_str()));
+  if (xl)
+    LF_TRY(expand_add_packed(ctx, *xl, views, W, off, row0, nv, static_cast<_Float16*>(packed), KP,
+                             (std::string(label) + ".expand").c_str()));
+  return LF_OK;
+}
+
+int lnproj_run(lf_context* ctx, const LnProjParams& p, int act, const char* label) {
+  if (p.rows <= 0) return LF_OK;
   const int ks = lnproj_ks(p.C);
   // few row blocks (the single track): split the column chunks over grid.y so about two blocks
   // per CU run; each re-does the LayerNorm of its rows
@@ -415,6 +420,14 @@ int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const 
 #undef LF_LPK
 #undef LF_LP
   return check_hip(hipGetLastError(), label);
+}
+
+int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode) {
+  if (p.rows <= 0) return LF_OK;
+  ExpandList xl;
+  LF_TRY(lnproj_prepare(ctx, p, packed, decode ? &xl : nullptr, label));
+  LF_TRY(expand_flush(ctx, xl, (std::string(label) + ".expand").c_str()));
+  return lnproj_run(ctx, p, act, label);
 }
 
 // ---------------------------------------------------------------------------------------
