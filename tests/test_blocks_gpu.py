@@ -87,6 +87,40 @@ def test_evoformer_stack_two_blocks(ctx):
     H.assert_close(pair.cpu().numpy(), rp, label="stack pair")
 
 
+def test_evoformer_stack_mask_tables_follow_the_masks(ctx):
+    """A stack call computes its mask tables (key-bias rows, OPM normalisers) in the first block
+    and reuses them: two stacks in a row on the same mask buffers with different contents (the
+    second masks the last residues and sequences) must each equal block-by-block calls, which
+    compute every table afresh -- bit for bit, the kernels being the same."""
+    import torch
+    from localfold_amd import device as D
+    s, n = 5, 24
+    w1, act = _evo_inputs(s, n, 4)
+    w2, _ = _evo_inputs(s, n, 5)
+    dw = D.DeviceWeights(ctx.device)
+    ws = [D.evoformer_weights(dw, w1), D.evoformer_weights(dw, w2)]
+    mm, pm = _dev(ctx, act["msaMask"]), _dev(ctx, act["pairMask"])
+    for variant in range(2):
+        if variant == 1:   # new contents in the same buffers
+            mm[-1, :] = 0
+            mm[:, -3:] = 0
+            pm[-3:, :] = 0
+            pm[:, -3:] = 0
+        msa, pair = _dev(ctx, act["msa"]), _dev(ctx, act["pair"])
+        D.evoformer_stack(ctx, msa, pair, mm, pm, ws, w1)
+        msa2, pair2 = _dev(ctx, act["msa"]), _dev(ctx, act["pair"])
+        for wsk, w in zip(ws, (w1, w2)):
+            D.evoformer_block(ctx, msa2, pair2, mm, pm, wsk, w)
+        torch.cuda.synchronize()
+        assert torch.equal(msa, msa2), f"variant {variant}: stack msa differs from its blocks"
+        assert torch.equal(pair, pair2), f"variant {variant}: stack pair differs from its blocks"
+        rm, rp = act["msa"], act["pair"]
+        for w in (w1, w2):
+            rm, rp = blocks.evoformer_block_af2(rm, rp, mm.cpu().numpy(), pm.cpu().numpy(), w)
+        H.assert_close(msa.cpu().numpy(), rm, label=f"stack msa, masks {variant}")
+        H.assert_close(pair.cpu().numpy(), rp, label=f"stack pair, masks {variant}")
+
+
 def test_config1_af2_block_full_size(ctx):
     """one AF2 block, N_res=64, N_seq=1, c_m 256, c_z 128, fp32 weights
     ~N(0, 1/fan_in), activations ~N(0, 1), seed 0."""
