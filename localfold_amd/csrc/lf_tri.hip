@@ -842,9 +842,12 @@ constexpr float TRI_NLOG2E = -1.4426950408889634f;
 #ifndef TRI_P_TPW
 #define TRI_P_TPW 1
 #endif
-#ifndef TRI_O_NWV
-#define TRI_O_NWV 8
-#endif
+// waves per block of the output kernel: 12 (three per SIMD, one X buffer each) for 2-byte
+// activations; f32 rows need more registers than three waves per SIMD leave, so 8 (two X
+// buffers each).  Measured at config 2: 43.9 -> 39.9 us with 12 waves for bf16, while f32 at
+// 12 waves spills and is 4-7% slower than at 8.
+template <int ACT>
+constexpr int tri_o_nwv() { return ACT == DT_F32 ? 8 : 12; }
 
 // The 16 pairs of a project tile: row r is pair src0 + r * sstride, stored at out0 + r of every
 // channel plane, r < nvalid.  Tile t normally holds pairs 16t .. 16t + 15 in place.  With
@@ -1130,9 +1133,10 @@ __device__ __forceinline__ void x_put(_Float16* Xw, const h8 (&xv)[4], int lane)
 
 // Output kernel for c_z = c_hidden = 128, one 16-pair tile per wave step.  The steady-state
 // loop runs whole tiles as straight-line code: the next tile's z rows and X columns are loaded
-// at the top of a step (clamped, never skipped), its X columns are transposed into the wave's
-// other LDS buffer between the second pass's MFMAs and that pass's stores, and the residual
-// comes from the z rows already held.  Every wait on the in-order vector-memory counter then
+// (clamped, never skipped) at the top of a step and transposed into the wave's other LDS
+// buffer between the second pass's MFMAs and that pass's stores (two X buffers, 8 waves), or
+// loaded between the two passes and transposed after the tile into its one buffer (12 waves,
+// whose LDS and registers allow only that); the residual comes from the z rows already held.  Every wait on the in-order vector-memory counter then
 // covers loads issued earlier in the same step and none of the stores issued after them.  A
 // partial last tile (P % 16 pairs) runs once after the loop, masked, on the wave owning it.
 // The weights are the MFMA A operand (resident in LDS), so a lane's accumulators hold four
@@ -1141,9 +1145,13 @@ __device__ __forceinline__ void x_put(_Float16* Xw, const h8 (&xv)[4], int lane)
 template <int ACT, int NWV, bool VECX>
 __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams p) {
   constexpr int NT = 64 * NWV;
+  // X patch buffers per wave: two (the next tile's X is transposed during the current tile's
+  // second pass) with 8 waves; one with more waves (it is transposed after the tile, into the
+  // buffer the tile has finished with), which the LDS budget requires
+  constexpr int XB = NWV <= 8 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) _Float16 Wz[128 * RS_LD];   // [c][h]
   __shared__ __attribute__((aligned(16))) _Float16 Wg[128 * RS_LD];   // [c][k], pre-scaled
-  __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][2][16 * O2_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[NWV][XB][16 * O2_LD];
   __shared__ __attribute__((aligned(16))) float Vs[6 * 128];         // bz, bg', centre-norm s/o, LN_in s/o
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nfull = p.P >> 4, nw = gridDim.x * NWV;
@@ -1178,7 +1186,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   // channels.  A pass stages its f32 update in Xc (the X fragments are in registers by then)
   // and each lane writes its own pair r16, channels c0 + 32jj + 8*g4 .. +7: the layout of its
   // z fragment, which holds the residual.  `between` runs after the second pass's MFMAs.
-  auto run_tile = [&](auto full_tag, const FragTile<ACT, 4>& zc, _Float16* Xc, int row0, int nval,
+  auto run_tile = [&](auto full_tag, const FragTile<ACT, 4>& zc, _Float16* Xc, int row0, int nval, auto&& mid,
                       auto&& between) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full_tag)::value;
     h8 ax[4], az[4];
@@ -1203,20 +1211,26 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
         accz[t4] = f4{bz.x, bz.y, bz.z, bz.w};
         accg[t4] = f4{bg.x, bg.y, bg.z, bg.w};
       }
+      // one k step's weight fragments live at a time (with one X buffer, the budget of three
+      // waves per SIMD: half a k step's)
+      constexpr int TH = XB == 2 ? 4 : 2;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        h8 wz[4], wg[4];
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          wz[t4] = *reinterpret_cast<const h8*>(Wz + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq);
-          wg[t4] = *reinterpret_cast<const h8*>(Wg + (c0 + t4 * 16 + r16) * RS_LD + 32 * j + kq);
-        }
+        for (int th = 0; th < 4; th += TH) {
+          h8 wz[TH], wg[TH];
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          accz[t4] = mfma16(wz[t4], ax[j], accz[t4]);
-          accg[t4] = mfma16(wg[t4], az[j], accg[t4]);
+          for (int u = 0; u < TH; ++u) {
+            wz[u] = *reinterpret_cast<const h8*>(Wz + (c0 + (th + u) * 16 + r16) * RS_LD + 32 * j + kq);
+            wg[u] = *reinterpret_cast<const h8*>(Wg + (c0 + (th + u) * 16 + r16) * RS_LD + 32 * j + kq);
+          }
+#pragma unroll
+          for (int u = 0; u < TH; ++u) {
+            accz[th + u] = mfma16(wz[u], ax[j], accz[th + u]);
+            accg[th + u] = mfma16(wg[u], az[j], accg[th + u]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);   // one k-step's weight fragments live at a time
       }
 #pragma unroll
       for (int t4 = 0; t4 < 4; ++t4) {
@@ -1227,7 +1241,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
         v.w = accz[t4][3] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(accg[t4][3]));
         *reinterpret_cast<float4*>(Us + r16 * 68 + t4 * 16 + 4 * g4) = v;
       }
-      if constexpr (PS == 1) between();
+      if constexpr (PS == 1 && XB == 2) between();
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const float4 u0 = *reinterpret_cast<const float4*>(Us + r16 * 68 + 32 * jj + 8 * g4);
@@ -1247,7 +1261,9 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     };
     pass(std::integral_constant<int, 0>{});
     __builtin_amdgcn_sched_barrier(0);
+    mid();
     pass(std::integral_constant<int, 1>{});
+    if constexpr (XB == 1) between();
   };
 
   if (tile < nfull) {
@@ -1261,10 +1277,17 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
       const int nt = tile + nw < nfull ? tile + nw : tile;   // the last step reloads its own tile
       FragTile<ACT, 4> zn;
       h8 xn[4];
-      frag_load(zn, p.z, (size_t)nt * 16, 16, 128, lane);
-      if constexpr (VECX) x_fetch(xn, p.X, p.P, nt * 16, lane);
-      _Float16* Xn = Xs[wave][cur ^ 1];
-      run_tile(std::true_type{}, zc, Xs[wave][cur], tile * 16, 16, [&]() __attribute__((always_inline)) {
+      // the next tile's rows load at the top of the step (two X buffers), or between the two
+      // passes (one buffer: fewer registers live through the first pass)
+      auto fetch_next = [&]() __attribute__((always_inline)) {
+        frag_load(zn, p.z, (size_t)nt * 16, 16, 128, lane);
+        if constexpr (VECX) x_fetch(xn, p.X, p.P, nt * 16, lane);
+      };
+      if constexpr (XB == 2) fetch_next();
+      _Float16* Xn = Xs[wave][XB == 2 ? cur ^ 1 : 0];
+      run_tile(std::true_type{}, zc, Xs[wave][XB == 2 ? cur : 0], tile * 16, 16, [&]() __attribute__((always_inline)) {
+        if constexpr (XB == 1) fetch_next();
+      }, [&]() __attribute__((always_inline)) {
         if constexpr (VECX) x_put(Xn, xn, lane);
         else x_transpose<ACT>(Xn, p.X, p.P, nt * 16, 16, lane);
       });
@@ -1272,7 +1295,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
       // counter wait cannot cover this step's stores), not at their first use next step
       launder(zn);
       zc = zn;
-      cur ^= 1;
+      if constexpr (XB == 2) cur ^= 1;
     }
   }
   if (tile == nfull && nfull * 16 < p.P) {
@@ -1280,7 +1303,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     FragTile<ACT, 4> zc;
     frag_load(zc, p.z, (size_t)row0, nval, 128, lane);
     x_transpose<ACT>(Xs[wave][0], p.X, p.P, row0, nval, lane);
-    run_tile(std::false_type{}, zc, Xs[wave][0], row0, nval, []() {});
+    run_tile(std::false_type{}, zc, Xs[wave][0], row0, nval, []() {}, []() {});
   }
 }
 
@@ -1313,12 +1336,13 @@ template <int ACT>
 static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resident, int kz, int kh) {
   const int P = op.P;
   if (resident && op.C == 128 && op.H == 128) {
+    constexpr int NWV = tri_o_nwv<ACT>();
     const int tiles = (P + 15) / 16;
-    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_O_NWV - 1) / TRI_O_NWV)));
+    dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + NWV - 1) / NWV)));
     if ((P & 7) == 0)
-      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, TRI_O_NWV, true>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, true>), g, dim3(64 * NWV), 0, ctx->stream, op);
     else
-      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, TRI_O_NWV, false>), g, dim3(64 * TRI_O_NWV), 0, ctx->stream, op);
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, false>), g, dim3(64 * NWV), 0, ctx->stream, op);
     return;
   }
   if (resident) {
