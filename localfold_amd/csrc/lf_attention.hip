@@ -25,16 +25,10 @@
 namespace lf {
 
 constexpr int FA_DP = 32;       // padded head dim (d <= 32)
-constexpr int FA_QPB = 128;          // queries per block (8 / QT waves of QT 16-query tiles)
-#ifndef FA_QT_BIAS
-#define FA_QT_BIAS 1                 // query tiles per wave with a pair bias
-#endif
-#ifndef FA_QT_PLAIN
-#define FA_QT_PLAIN 1                // ... and without
-#endif
-#ifndef FA_BIASADD
-#define FA_BIASADD 0
-#endif
+constexpr int FA_QPB = 128;     // queries per block (8 / QT waves of QT 16-query tiles)
+// 16-query tiles per wave, with and without a pair bias: one (two measured 60% slower at
+// config 3: 155 VGPRs, half the waves)
+constexpr int FA_QT_BIAS = 1, FA_QT_PLAIN = 1;
 constexpr int FA_KC = 64;       // keys per chunk
 constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
 
@@ -244,17 +238,7 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
 
 // (float)v[i] + c in one instruction (i is a constant once the caller's loop is unrolled)
 __device__ __forceinline__ float bias_add(const h4& v, int i, float c) {
-#if FA_BIASADD == 2
-  return c;
-#endif
   const uint2 u = __builtin_bit_cast(uint2, v);
-#if FA_BIASADD == 1
-  const uint32_t w1 = i < 2 ? u.x : u.y;
-  float r;
-  if (i & 1) asm("v_cvt_f32_f16_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w1));
-  else asm("v_cvt_f32_f16_e32 %0, %1" : "=v"(r) : "v"(w1));
-  return r + c;
-#endif
   const uint32_t w = i < 2 ? u.x : u.y;
   return (i & 1) ? f16_add<1>(w, c) : f16_add<0>(w, c);
 }

@@ -828,20 +828,16 @@ __global__ __launch_bounds__(512) void tri_output_resident_kernel(TriOutputParam
   }
 }
 
-// Project kernel for c_z = c_hidden = 128 (every AF2/AF3 pair width at production size).
-// Weights stay resident in LDS as before; each wave now carries two 16-row tiles, so every
-// weight fragment read from LDS feeds two MFMAs.  The biases are the MFMA accumulators'
-// initial values and the gate weights/biases arrive pre-multiplied by -log2(e), so a gate
-// is rcp(1 + exp2(acc)).  A wave walks tiles w, w + nw, w + 2nw, ... two at a time; when its
-// count is odd the last step runs the first tile's MFMAs only.
+// Project kernels for c_z = c_hidden = 128 (every AF2/AF3 pair width at production size),
+// weights resident in LDS.  The gate weights and biases arrive pre-multiplied by -log2(e),
+// so a gate is rcp(1 + exp2(acc)).  tri_project_v2_kernel (partial tiles) carries TPW 16-row
+// tiles per wave, so with TPW = 2 every weight fragment read from LDS feeds two MFMAs; a wave
+// walks tiles w, w + nw, w + 2nw, ... TPW at a time, the last step running only the tiles it
+// has.  One tile per wave at 12 waves is what runs: two tiles need registers that leave two
+// waves per SIMD, measured slower.
 constexpr float TRI_NLOG2E = -1.4426950408889634f;
-// waves per block and 16-row tiles per wave of the 128-wide project / output kernels
-#ifndef TRI_P_NWV
-#define TRI_P_NWV 12
-#endif
-#ifndef TRI_P_TPW
-#define TRI_P_TPW 1
-#endif
+// waves per block and 16-row tiles per wave of the 128-wide project kernels (16 waves spill)
+constexpr int TRI_P_NWV = 12, TRI_P_TPW = 1;
 // waves per block of the output kernel: 12 (three per SIMD, one X buffer each) for 2-byte
 // activations; f32 rows need more registers than three waves per SIMD leave, so 8 (two X
 // buffers each).  Measured at config 2: 43.9 -> 39.9 us with 12 waves for bf16, while f32 at
