@@ -375,25 +375,27 @@ __global__ __launch_bounds__(256, MINW) void tri_contract_kernel(TriContractPara
 }
 
 // The outgoing-layout contraction (k contiguous in both operands) when N is a multiple of BK:
-// 128 x 128 tiles, K steps of BK double-buffered in LDS and filled by direct global -> LDS
+// TM x TM tiles (TM = 128 or 96), K steps of BK double-buffered in LDS and filled by direct global -> LDS
 // loads (16 bytes a lane, no register staging), one barrier a step, the next step's loads in
 // flight during the current step's MFMAs.  A wave's load instruction fills 1 KB of LDS
 // contiguously, so the 16-byte chunks of a row are XOR-swizzled by the row (chunk c of row r
 // sits in slot c ^ swz(r)) to keep the MFMA fragment reads of 16 rows off a single bank group.
 // Rows past N are clamped to row N - 1: they only feed output rows or columns that are never
 // stored.
-// The two 32 KB stages hold the LDS at two blocks (8 waves) per CU; measured at N = 384 it
-// beats the register-staged kernel above (30.9 against 33.1 us), and 8-wave blocks or 32-wide
-// K steps with four blocks per CU were no faster.
+// At TM = 128 the two 32 KB stages hold the LDS at two blocks (8 waves) per CU, at TM = 96
+// (24 KB stages) three.  Measured at N = 384 the 128-row kernel beats the register-staged
+// kernel above (30.9 against 33.1 us), and 8-wave blocks or 32-wide K steps with four blocks
+// per CU were no faster.
 template <int BK>
 __device__ __forceinline__ int ct_swz(int r) {
   return BK == 64 ? (r & 7) : ((r >> 1) & 3);
 }
 
-template <int BK>
-__global__ __launch_bounds__(256, 2) void tri_contract_dma_kernel(TriContractParams p) {
-  constexpr int NT = 256, TM = 128, FM = 4, FN = 4, WT = 64, WTN = 64, CH = BK / 8, PER = TM * CH / NT,
-                STAGE = TM * BK;
+template <int BK, int TM>
+__global__ __launch_bounds__(256, TM == 128 ? 2 : 3) void tri_contract_dma_kernel(TriContractParams p) {
+  constexpr int NT = 256, FM = TM / 32, FN = TM / 32, WT = TM / 2, WTN = TM / 2, CH = BK / 8,
+                PER = TM * CH / NT, STAGE = TM * BK;
+  static_assert(TM % 32 == 0 && (TM * CH) % NT == 0, "tile rows must split into whole load rounds");
   __shared__ __attribute__((aligned(16))) _Float16 S[2][2][STAGE];   // [stage][L, R][row][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -480,7 +482,19 @@ static void launch_contract(lf_context* ctx, const TriContractParams& cp, int H,
   const bool vec = (cp.N % 8) == 0;
   if (!kmajor) {
     if (TM == 128 && cp.N % 64 == 0) {
-      hipLaunchKernelGGL((tri_contract_dma_kernel<64>), grid, dim3(256), 0, ctx->stream, cp);
+      // 128-row tiles at two blocks per CU, or, when the grid is only a few waves of blocks
+      // and the last one would run mostly empty, 96-row tiles at three per CU.  Measured: at
+      // N = 384 (1152 tiles of 128 in 512 slots: 2.25 waves) the 96-row kernel is 3-4%
+      // faster; at N = 1024 (16 full waves) it is 11% slower, its operands re-read more often.
+      const long long slots = 2LL * ctx->num_cus;
+      const int t96 = (cp.N + 95) / 96;
+      const long long b128 = (long long)tm * tm * H, b96 = (long long)t96 * t96 * H;
+      const double w128 = (double)((b128 + slots - 1) / slots);
+      const double w96 = (double)((b96 + slots * 3 / 2 - 1) / (slots * 3 / 2)) * (96.0 * 96.0) / (128.0 * 128.0);
+      if (b128 <= 4 * slots && w96 < 0.85 * w128)
+        hipLaunchKernelGGL((tri_contract_dma_kernel<64, 96>), dim3((unsigned)b96), dim3(256), 0, ctx->stream, cp);
+      else
+        hipLaunchKernelGGL((tri_contract_dma_kernel<64, 128>), grid, dim3(256), 0, ctx->stream, cp);
       return;
     }
     if (vec) hipLaunchKernelGGL((tri_contract_kernel<TM, BK, MINW, false, true>), grid, dim3(256), 0, ctx->stream, cp);

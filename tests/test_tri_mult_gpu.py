@@ -71,11 +71,12 @@ def test_quantised_weights_and_activation_dtypes(ctx, dtype, per_channel, act):
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 @pytest.mark.parametrize("divide", [False, True])
-@pytest.mark.parametrize("n", [64, 40, 12])
+@pytest.mark.parametrize("n", [256, 64, 40, 12])
 def test_af3_dialect(ctx, direction, divide, n):
-    """n = 64 and 40: the resident kernels (interleaved tensors split in LDS), at 64 with the
-    direct-to-LDS contraction (N a multiple of 64); n = 12: the chunked kernels (the
-    interleaved columns decoded weight by weight)."""
+    """n = 256, 64 and 40: the resident kernels (interleaved tensors split in LDS), at 256 and
+    64 with the direct-to-LDS contraction (N a multiple of 64: 128-row tiles at 256, 96-row
+    tiles at 64, as at 384); n = 12: the chunked kernels (the interleaved columns decoded
+    weight by weight)."""
     c = 128
     w = H.af3_tri_weights(c, 21)
     s = S.Stream(77)
