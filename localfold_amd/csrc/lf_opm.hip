@@ -316,6 +316,19 @@ __global__ __launch_bounds__(512) void opm_fused_kernel(OpmFusedParams f) {
   const int wm = wave >> 2, wn = wave & 3, r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   int mt, nt;
   opm_big_order(f.o, mt, nt);
+  // the epilogue's normalisers and residual rows do not depend on the GEMMs: their loads are
+  // issued first and land during the outer GEMM (lane: channels c .. c + 3 of pair 16 pt + r16)
+  const int N = f.o.N;
+  const int c = wave * 16 + 4 * g4;
+  float inv[4], res[4][4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) {
+    const int pl = pt * 16 + r16;
+    const size_t row = (size_t)(mt * 8 + (pl >> 3)) * N + nt * 8 + (pl & 7);
+    inv[pt] = f.den[row];
+    if (f.resid) ld4v<ACT>(f.resid, row * 128 + c, res[pt]);
+    else res[pt][0] = res[pt][1] = res[pt][2] = res[pt][3] = 0.f;
+  }
   {
     f4 acc[8][4];
     opm_big_tile(f.o, mt * OB, nt * OB, acc, obs);
@@ -363,8 +376,6 @@ __global__ __launch_bounds__(512) void opm_fused_kernel(OpmFusedParams f) {
     for (int u = 0; u < 8; ++u) wcur[u] = wnext[u];
   }
   // lane: channels c = 16 w + 4 g4 + i of pair 16 pt + r16 of the tile
-  const int N = f.o.N;
-  const int c = wave * 16 + 4 * g4;
   float bias[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) bias[i] = f.bias ? f.bias[c + i] : 0.f;
@@ -372,20 +383,11 @@ __global__ __launch_bounds__(512) void opm_fused_kernel(OpmFusedParams f) {
   for (int pt = 0; pt < 4; ++pt) {
     const int pl = pt * 16 + r16;
     const size_t row = (size_t)(mt * 8 + (pl >> 3)) * N + nt * 8 + (pl & 7);
-    const float inv = 1.f / f.den[row];
-    {
-      const size_t idx = row * 128 + c;
-      float v[4];
+    const float rinv = 1.f / inv[pt];
+    float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (d[pt][i] + bias[i]) * inv;
-      if (f.resid) {
-        float r[4];
-        ld4v<ACT>(f.resid, idx, r);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += r[i];
-      }
-      st4v<ACT>(f.out, idx, v);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = (d[pt][i] + bias[i]) * rinv + res[pt][i];
+    st4v<ACT>(f.out, row * 128 + c, v);
   }
 }
 
