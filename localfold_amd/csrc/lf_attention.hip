@@ -498,16 +498,18 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
           o[2][qt] = mfma16(ones, pf, o[2][qt]);
         }
       }
-      if (c + 1 < nkc) {
-        if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1);
-        else kv_store(buf ^ 1, st0, kb0);
-        __syncthreads();
-      }
+      // unconditional (after the last chunk it stores a repeat that nothing reads): with no
+      // branch around the store the compiler's waits on the loads stay exact
+      if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1);
+      else kv_store(buf ^ 1, st0, kb0);
+      __syncthreads();
   };
-  for (int c0 = 0; c0 < nkc; c0 += 2) {
+  int c0 = 0;
+  for (; c0 + 2 <= nkc; c0 += 2) {
     chunk(c0, std::integral_constant<int, 0>{});
-    if (c0 + 1 < nkc) chunk(c0 + 1, std::integral_constant<int, 1>{});
+    chunk(c0 + 1, std::integral_constant<int, 1>{});
   }
+  if (c0 < nkc) chunk(c0, std::integral_constant<int, 0>{});
   // o[query][h*d + dd] = O / l * g
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
