@@ -18,6 +18,10 @@ import time
 import numpy as np
 
 N, CZ, CH, MASKED = 384, 128, 128, 16
+# bf16 residual storage (the config's "bf16 activations" taken literally): timed, but outside
+# the north-star tolerance; the f32-residual lines are the ones whose parity is tested.
+BF16_PARITY = ("outside tolerance: bf16 residual storage meets the relative Frobenius bound per block but "
+               "not max abs <= 2e-2, and drifts to rel. Frobenius 1.6e-2 over 48 blocks")
 PEAK_F16_TFLOPS = 2500.0    # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
@@ -125,6 +129,24 @@ def measured_traffic(kind):
         return None, "no profile"
 
 
+def rocprof_avg_us(kind):
+    """Average launch duration (us) of the dominant kernel in the committed rocprofv3 trace
+    of the same workload, while the triangle source still matches the traced one; else None.
+    The live figure comes from the library's hipEvents, which add 1-4 us per launch."""
+    import hashlib
+    try:
+        line = next(l for l in open(TRAFFIC_FILE) if l.startswith("traffic_json: "))
+        data = json.loads(line[len("traffic_json: "):])
+        src = os.path.join(os.path.dirname(TRAFFIC_FILE), "..", "localfold_amd", "csrc", "lf_tri.hip")
+        if data.get("csrc_sha16") != hashlib.sha256(open(src, "rb").read()).hexdigest()[:16]:
+            return None
+        prefix = TRAFFIC_KERNELS.get(kind)
+        vals = [v["avg_us"] for k, v in data["kernels"].items() if prefix and k.startswith(prefix)]
+        return round(sum(vals) / len(vals), 2) if vals else None
+    except (OSError, StopIteration, ValueError, KeyError):
+        return None
+
+
 def tri_attention_flops(n, c=128, heads=4, d=32):
     """One triangle-attention direction: q/k/v/gate + bias projections, QK^T and PV, output."""
     p = n * n
@@ -172,6 +194,29 @@ def timed(fn, reps):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / reps
+
+
+def timed_restored(fn, restore, reps):
+    """Mean ms of `reps` calls of fn, each on the same inputs: `restore` (device copies of the
+    saved inputs) runs before every call, outside the event window, so an in-place block is
+    timed on fixed activations and not on ever-growing ones (a block's attention kernels take
+    a data-dependent path, the lazy rescale of the running maximum)."""
+    import torch
+
+    def once():
+        restore()
+        fn()
+
+    ramp(once)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        restore()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / reps
 
 
 def triangle_attention_config3(ctx, D, synthetic, reps):
@@ -230,11 +275,13 @@ def evoformer_block_config4(ctx, D, synthetic, reps, storage="f32"):
     def block():
         D.evoformer_block(ctx, msa, pair, mm, pm, ws, w)
 
+    def restore():
+        msa.copy_(msa0)
+        pair.copy_(pair0)
+
     block()
-    msa.copy_(msa0)
-    pair.copy_(pair0)
-    ms = timed(block, reps)
-    kern = profile_ops(ctx, block, 2)
+    ms = timed_restored(block, restore, reps)
+    kern = profile_ops(ctx, lambda: (restore(), block()), 2)
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     return {"workload": f"BASELINE config 4, one AF2 Evoformer block: N_res={n}, N_seq={s_}, c_m=256, c_z=128, "
                         f"int8 weights (fp16 scales, groups of 64), bf16 inputs, {storage} residual stream",
@@ -263,11 +310,13 @@ def extra_msa_block_n384(ctx, D, synthetic, reps):
     def block():
         D.extra_msa_block(ctx, msa, pair, mm, pm, ws, w)
 
+    def restore():
+        msa.copy_(msa0)
+        pair.copy_(pair0)
+
     block()
-    msa.copy_(msa0)
-    pair.copy_(pair0)
-    ms = timed(block, reps)
-    kern = profile_ops(ctx, block, 2)
+    ms = timed_restored(block, restore, reps)
+    kern = profile_ops(ctx, lambda: (restore(), block()), 2)
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     return {"workload": f"one AF2 extra-MSA block: N_res={n}, N_extra_seq={s_}, c_m={cm}, c_z={cz}, row attention "
                         "8x8 with pair bias, global column attention 8x8, int8 weights (fp16 scales, groups of 64), "
@@ -295,11 +344,13 @@ def msa_module_block_n384(ctx, D, synthetic, reps):
     def block():
         D.msa_module_block(ctx, msa, pair, mm, pm, ws, False)
 
+    def restore():
+        msa.copy_(msa0)
+        pair.copy_(pair0)
+
     block()
-    msa.copy_(msa0)
-    pair.copy_(pair0)
-    ms = timed(block, reps)
-    kern = profile_ops(ctx, block, 2)
+    ms = timed_restored(block, restore, reps)
+    kern = profile_ops(ctx, lambda: (restore(), block()), 2)
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     return {"workload": f"one AF3 MSA-module block (AF3 order): N_tokens={n}, N_msa={s_}, c_m={cm}, c_z={cz}, "
                         "pair-weighted averaging 8x8, pair attention 4 heads, int8 weights (fp16 scales, groups "
@@ -354,17 +405,20 @@ def evoformer_stack_config4(ctx, D, synthetic, reps, storage="f32"):
     del c4
 
     def stack():
-        msa.copy_(msa0)
-        pair.copy_(pair0)
         D.evoformer_stack(ctx, msa, pair, mm, pm, ws, weights[0])
 
+    def restore():
+        msa.copy_(msa0)
+        pair.copy_(pair0)
+
+    restore()
     stack()   # grows the workspace once
-    ms = timed(stack, reps)
+    ms = timed_restored(stack, restore, reps)
     finite = bool(torch.isfinite(msa).all().item() and torch.isfinite(pair).all().item())
     gflop = 48 * 1076.5
     return {"workload": f"BASELINE config 4, the 48-block AF2 Evoformer stack: N_res={n}, N_seq={s_}, c_m=256, "
                         f"c_z=128, 48 distinct int8 weight sets (fp16 scales, groups of 64), bf16 inputs, {storage} "
-                        "residual stream, one pass; time includes restoring the inputs (2 device copies)",
+                        "residual stream, one pass; the inputs restored before each timed pass, outside the timing",
             "ms_per_stack": round(ms, 2), "ms_per_block": round(ms / 48, 3),
             "tflops": round(gflop / ms, 1), "algorithmic_gflop": gflop, "outputs_finite": finite}
 
@@ -392,11 +446,13 @@ def pairformer_block_config5(ctx, D, synthetic, reps, storage="f32"):
     def block():
         D.pairformer_block(ctx, pair, single, pm, sm, ws)
 
+    def restore():
+        pair.copy_(pair0)
+        single.copy_(single0)
+
     block()
-    pair.copy_(pair0)
-    single.copy_(single0)
-    ms = timed(block, reps)
-    kern = profile_ops(ctx, block, 2)
+    ms = timed_restored(block, restore, reps)
+    kern = profile_ops(ctx, lambda: (restore(), block()), 2)
     finite = bool(torch.isfinite(pair).all().item() and torch.isfinite(single).all().item())
     gflop = 2692.0
     return {"workload": f"BASELINE config 5, one AF3 Pairformer block: N_tokens={n}, c_z={cz}, c_s={cs}, "
@@ -514,6 +570,10 @@ def main():
     roof["ms_per_launch"] = round(dom_ms, 4)
     roof["mfma_tflops"] = round(a["flops"] / (dom_ms * 1e-3) / 1e12, 2)
     roof["traffic"], roof["traffic_source"] = measured_traffic(dom)
+    rp_us = rocprof_avg_us(dom)
+    if rp_us:   # the same kernel's average from the committed rocprofv3 trace, and the fraction it gives
+        roof["rocprof_us_per_launch"] = rp_us
+        roof["frac_rocprof"] = round(roof["frac"] * dom_ms * 1e3 / rp_us, 4)
 
     extras = {}
     if not args.no_extras and not args.only:
@@ -522,9 +582,11 @@ def main():
         log("config 4: one Evoformer block ...")
         extras["evoformer_block"] = evoformer_block_config4(ctx, D, synthetic, 5)
         extras["evoformer_block_bf16"] = evoformer_block_config4(ctx, D, synthetic, 5, "bf16")
+        extras["evoformer_block_bf16"]["parity"] = BF16_PARITY
         log("config 4: the 48-block stack ...")
         extras["evoformer_stack"] = evoformer_stack_config4(ctx, D, synthetic, 2)
         extras["evoformer_stack_bf16"] = evoformer_stack_config4(ctx, D, synthetic, 2, "bf16")
+        extras["evoformer_stack_bf16"]["parity"] = BF16_PARITY
         log("extra-MSA block ...")
         extras["extra_msa_block"] = extra_msa_block_n384(ctx, D, synthetic, 5)
         log("input embedder ...")
@@ -534,6 +596,7 @@ def main():
         log("config 5: one Pairformer block ...")
         extras["pairformer_block"] = pairformer_block_config5(ctx, D, synthetic, 5)
         extras["pairformer_block_bf16"] = pairformer_block_config5(ctx, D, synthetic, 5, "bf16")
+        extras["pairformer_block_bf16"]["parity"] = BF16_PARITY
 
     cpu = None
     if not args.no_cpu_baseline and not args.only:

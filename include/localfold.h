@@ -54,7 +54,9 @@ typedef struct {
   int layout;           /* LF_IN_OUT or LF_OUT_IN */
   int rows, cols;
   int group;            /* quantised only: flat group size, or 0 = per output channel */
-  const void* data;     /* values, or codes */
+  const void* data;     /* values, or codes; int5 codes must stay readable for 4 bytes past
+                           the last code byte (the reference's records hold a slack byte and
+                           the scale table there; the kernels fetch aligned word pairs) */
   const void* scales;   /* fp16, one per group (quantised) */
   const void* zeros;    /* fp16, one per group (int5) */
 } lf_weight;
@@ -78,7 +80,9 @@ int lf_memcpy_dtoh(lf_context* ctx, void* dst, const void* src, size_t bytes);
 int lf_memset(lf_context* ctx, void* dst, int value, size_t bytes);
 int lf_synchronize(lf_context* ctx);
 /* {currentBytes, peakBytes, allocationCount} of webgpu/runtime/allocator.js:188-194,
- * counting caller allocations and the context's scratch workspace. */
+ * counting caller allocations, the context's scratch workspace and its mask tables.  Not
+ * counted: the library's static LF_TRI_NOALLOC_SCRATCH_BYTES array, which every device the
+ * library loads on holds until the process ends (see lf_tri_mult_noalloc). */
 int lf_memory_stats(lf_context* ctx, size_t* current_bytes, size_t* peak_bytes, size_t* allocation_count);
 
 /* Per-kernel timestamps (webgpu/runtime/execution.js:673-727 readTimestampProfile):
@@ -130,8 +134,10 @@ int lf_tri_mult(lf_context* ctx, const lf_tri_mult_args* args);
 /* No counterpart in the reference: lf_tri_mult for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as lf_tri_mult, but its scratch (the a, b and X planes,
- * 3 * c_hidden * N^2 f16, plus the decoded weights) lives in a static per-device array of
- * LF_TRI_NOALLOC_SCRATCH_BYTES, looked up once per device by lf_context_create; nothing is
+ * 3 * c_hidden * N^2 f16; weights are decoded while being staged into LDS, so they take no
+ * scratch) lives in a static per-device array of LF_TRI_NOALLOC_SCRATCH_BYTES (reserved on
+ * every device the library loads on, used or not), looked up once per device by
+ * lf_context_create; nothing is
  * allocated or freed.  Shapes needing more scratch are rejected with LF_ERR_INVALID (c_hidden
  * 128 fits N <= 417).  Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two threads, two contexts) race, so serialise them. */
@@ -313,6 +319,14 @@ int lf_extra_msa_block(lf_context* ctx, const lf_evoformer_block_args* args, con
  * extra-MSA blocks in order on the same msa and pair. */
 int lf_extra_msa_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_extra_msa_weights* blocks,
                        int block_count);
+
+/* Replaces ExtraMsaPairStackGpu.run (webgpu/af2/evoformer/stack.js:163-247), whose blocks
+ * are encodeEvoformerPairBlock (webgpu/af2/evoformer/block.js:1663-1713): per block the outer
+ * product mean of the (unchanged) msa into the pair, triangle multiplication out/in, triangle
+ * attention start/end and the pair transition.  The msa is read, never written; the weights'
+ * MSA-side records (row/column attention, MSA transition) are not read. */
+int lf_evoformer_pair_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_evoformer_weights* blocks,
+                            int block_count);
 
 typedef struct {
   lf_tri_mult_weights tri_out, tri_in;

@@ -215,6 +215,7 @@ PROTOTYPES = [
     ("lf_extra_msa_block", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights)]),
     ("lf_extra_msa_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_extra_msa_weights), C.c_int]),
     ("lf_evoformer_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
+    ("lf_evoformer_pair_stack", C.c_int, [P, C.POINTER(lf_evoformer_block_args), C.POINTER(lf_evoformer_weights), C.c_int]),
     ("lf_pairformer_block", C.c_int, [P, C.POINTER(lf_pairformer_block_args)]),
     ("lf_input_embedder", C.c_int, [P, C.POINTER(lf_input_embedder_args)]),
     ("lf_af2_recycle", C.c_int, [P, C.POINTER(lf_af2_recycle_args)]),

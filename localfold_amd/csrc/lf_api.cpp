@@ -39,7 +39,7 @@ int workspace(lf_context* ctx, const size_t* sizes, void** out, int n) {
     const size_t grow = std::max(total, size_t(1) << 20);
     LF_TRY(check_hip(hipMalloc(&ctx->ws, grow), "workspace allocation"));
     ctx->ws_bytes = grow;
-    ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->user_bytes + ctx->ws_bytes);
+    ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->resident());
   }
   char* p = static_cast<char*>(ctx->ws);
   for (int i = 0; i < n; ++i) {
@@ -69,7 +69,8 @@ int mask_table(lf_context* ctx, const void* mask, int kind, long long a, long lo
   void* buf = nullptr;
   LF_TRY(check_hip(hipMalloc(&buf, bytes), "mask table allocation"));
   ctx->mask_tables.push_back(lf_context::MaskTable{mask, kind, a, b, f, true, buf, bytes});
-  ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->user_bytes + ctx->ws_bytes);
+  ctx->mask_bytes += bytes;
+  ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->resident());
   *out = buf;
   return LF_OK;
 }
@@ -229,7 +230,7 @@ int lf_malloc(lf_context* ctx, size_t bytes, void** out) {
   ctx->user_allocs.emplace_back(p, bytes);
   ctx->user_bytes += bytes;
   ctx->alloc_count += 1;
-  ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->user_bytes + ctx->ws_bytes);
+  ctx->peak_bytes = std::max(ctx->peak_bytes, ctx->resident());
   *out = p;
   return LF_OK;
 }
@@ -273,9 +274,9 @@ int lf_synchronize(lf_context* ctx) {
 
 int lf_memory_stats(lf_context* ctx, size_t* current_bytes, size_t* peak_bytes, size_t* allocation_count) {
   if (!ctx) return set_error(LF_ERR_INVALID, "NULL context");
-  if (current_bytes) *current_bytes = ctx->user_bytes + ctx->ws_bytes;
+  if (current_bytes) *current_bytes = ctx->resident();
   if (peak_bytes) *peak_bytes = ctx->peak_bytes;
-  if (allocation_count) *allocation_count = ctx->alloc_count + (ctx->ws ? 1 : 0);
+  if (allocation_count) *allocation_count = ctx->alloc_count + (ctx->ws ? 1 : 0) + ctx->mask_tables.size();
   return LF_OK;
 }
 

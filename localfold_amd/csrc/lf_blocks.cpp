@@ -13,14 +13,17 @@ namespace lf {
 
 // The Evoformer block; with `global` the extra-MSA block (encodeExtraMsaBlock,
 // webgpu/af2/evoformer/block.js:1715-1744), whose step 2 is the global column attention.
+// With `pair_only` only steps 4-9 run, the MSA being read and not written
+// (encodeEvoformerPairBlock, block.js:1663-1713).
 static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, const lf_evoformer_weights& w,
-                           const lf_global_attention_weights* global = nullptr, int global_heads = 0) {
+                           const lf_global_attention_weights* global = nullptr, int global_heads = 0,
+                           bool pair_only = false) {
   LF_REQUIRE(a.sequences > 0 && a.length > 0 && a.c_m > 0 && a.c_z > 0, "evoformer block dimensions must be positive");
   LF_REQUIRE(a.msa && a.pair && a.msa_mask && a.pair_mask, "evoformer block: NULL activation or mask");
   const float eps = a.epsilon > 0.f ? a.epsilon : 1e-5f;
   const long long chunk = 1LL << 30;   // transition hidden budget per chunk on a 288 GB device
 
-  {  // 1. MSA row attention with pair bias
+  if (!pair_only) {  // 1. MSA row attention with pair bias
     lf_attention_args x{};
     x.batch = a.sequences;
     x.queries = a.length;
@@ -40,7 +43,8 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     StageScope stage(ctx, "row_attention");
     LF_TRY(attention(ctx, x));
   }
-  if (global) {  // 2. global column attention (extra-MSA block)
+  if (pair_only) {
+  } else if (global) {  // 2. global column attention (extra-MSA block)
     lf_global_attention_args x{};
     x.sequences = a.sequences;
     x.length = a.length;
@@ -72,7 +76,7 @@ static int evoformer_block(lf_context* ctx, const lf_evoformer_block_args& a, co
     StageScope stage(ctx, "column_attention");
     LF_TRY(attention(ctx, x));
   }
-  {  // 3. MSA transition
+  if (!pair_only) {  // 3. MSA transition
     lf_transition_args x{};
     x.kind = LF_TRANSITION_RELU;
     x.rows = a.sequences * a.length;
@@ -472,6 +476,17 @@ int lf_extra_msa_stack(lf_context* ctx, const lf_evoformer_block_args* args, con
   lf::MaskScope masks(ctx);
   for (int b = 0; b < block_count; ++b)
     LF_TRY(lf::evoformer_block(ctx, *args, blocks[b].base, &blocks[b].column_global, blocks[b].column_global_heads));
+  return LF_OK;
+}
+
+int lf_evoformer_pair_stack(lf_context* ctx, const lf_evoformer_block_args* args, const lf_evoformer_weights* blocks,
+                            int block_count) {
+  if (!ctx || !args || (!blocks && block_count > 0))
+    return lf::set_error(LF_ERR_INVALID, "lf_evoformer_pair_stack: NULL argument");
+  if (block_count < 0) return lf::set_error(LF_ERR_INVALID, "lf_evoformer_pair_stack: negative block count");
+  hipSetDevice(ctx->device);
+  lf::MaskScope masks(ctx);
+  for (int b = 0; b < block_count; ++b) LF_TRY(lf::evoformer_block(ctx, *args, blocks[b], nullptr, 0, true));
   return LF_OK;
 }
 

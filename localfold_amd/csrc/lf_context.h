@@ -18,6 +18,8 @@ struct lf_context {
   size_t ws_bytes = 0;
   // caller allocations through lf_malloc
   size_t user_bytes = 0, peak_bytes = 0, alloc_count = 0;
+  size_t mask_bytes = 0;   // mask tables below (kept for the context's lifetime)
+  size_t resident() const { return user_bytes + ws_bytes + mask_bytes; }
   std::vector<std::pair<void*, size_t>> user_allocs;
   // Tables derived from a mask alone (attention key-bias rows, OPM pair normalisers), kept
   // while `mask_scope` > 0 -- a stack call, whose masks do not change -- so that the later

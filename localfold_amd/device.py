@@ -127,7 +127,10 @@ class DeviceWeights:
             self.keep.append(t)
             w.data = t.data_ptr()
         else:
-            w.data = self._tensor(np.asarray(rec["data"]))
+            codes = np.asarray(rec["data"])
+            if dt == "int5":   # the kernels' aligned word-pair fetch reads <= 3 bytes past the codes
+                codes = np.concatenate([codes.view(np.uint8).reshape(-1), np.zeros(4, np.uint8)])
+            w.data = self._tensor(codes)
             w.scales = self._tensor(np.asarray(rec["scales"], np.float16))
             if rec.get("zeros") is not None:
                 w.zeros = self._tensor(np.asarray(rec["zeros"], np.float16))
@@ -474,6 +477,15 @@ def evoformer_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: 
     a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w0, epsilon)
     arr = (capi.lf_evoformer_weights * len(wstructs))(*wstructs)
     check(ctx.lib.lf_evoformer_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
+
+
+def evoformer_pair_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: dict, epsilon: float = 1e-5):
+    """`len(wstructs)` pair halves of Evoformer blocks (ExtraMsaPairStackGpu.run): OPM of the
+    unchanged msa, triangle multiplication out/in, triangle attention start/end, pair
+    transition; the pair is updated in place, the msa is only read."""
+    a = evoformer_block_args(msa, pair, msa_mask, pair_mask, w0, epsilon)
+    arr = (capi.lf_evoformer_weights * len(wstructs))(*wstructs)
+    check(ctx.lib.lf_evoformer_pair_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
 
 
 def extra_msa_weights(dw: DeviceWeights, w: dict) -> capi.lf_extra_msa_weights:

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -24,10 +25,25 @@ namespace {
 // order), so the holder outlives the context: once the context is gone a finalizer frees
 // nothing (lf_context_destroy released every allocation), and the last reference deletes
 // the holder.
+//
+// One lf_context is not safe for concurrent use (its workspace, mask tables, allocation list
+// and profile records are unguarded), so every use of it from this addon holds `mu`: a run on
+// a worker thread holds it for the whole run, and a call on the JS thread (an op, an upload,
+// a free, a finalizer, contextDestroy) waits for a pending run to finish.  index.js also
+// queues the runs of one device, so the JS thread does not normally wait here.
 struct CtxHolder {
   lf_context* ctx;
   bool alive;
   long refs;
+  std::mutex mu;
+};
+
+// Holds the context's lock for the scope of a JS-thread call.
+struct CtxGuard {
+  std::unique_lock<std::mutex> lock;
+  explicit CtxGuard(CtxHolder* h) {
+    if (h) lock = std::unique_lock<std::mutex>(h->mu);
+  }
 };
 
 void holder_release(CtxHolder* h) {
@@ -60,11 +76,11 @@ napi_value throw_lf(napi_env env, int rc, const char* what) {
 // and waits for the stream, and completion (back on the JS thread) resolves the promise or
 // rejects it with the worker's lf_last_error().  The call owns copies of its argument
 // structs (plain device pointers and sizes); the JS side keeps the device buffers alive until
-// the promise settles.  The context is not to be used from JS until then.
+// the promise settles.  The worker holds the context's lock for the whole run (CtxHolder).
 struct AsyncRun {
   napi_async_work work = nullptr;
   napi_deferred deferred = nullptr;
-  lf_context* ctx = nullptr;
+  CtxHolder* h = nullptr;
   std::function<int(lf_context*)> fn;
   int rc = LF_OK;
   std::string err;
@@ -73,8 +89,14 @@ struct AsyncRun {
 
 void async_execute(napi_env, void* data) {
   AsyncRun* r = static_cast<AsyncRun*>(data);
-  r->rc = r->fn(r->ctx);
-  if (r->rc == LF_OK) r->rc = lf_synchronize(r->ctx);
+  std::lock_guard<std::mutex> g(r->h->mu);
+  if (!r->h->alive) {
+    r->rc = LF_ERR_INVALID;
+    r->err = "the context was destroyed";
+    return;
+  }
+  r->rc = r->fn(r->h->ctx);
+  if (r->rc == LF_OK) r->rc = lf_synchronize(r->h->ctx);
   if (r->rc != LF_OK) r->err = lf_last_error();
 }
 
@@ -93,16 +115,18 @@ void async_complete(napi_env env, napi_status status, void* data) {
     napi_reject_deferred(env, r->deferred, e);
   }
   napi_delete_async_work(env, r->work);
+  holder_release(r->h);
   delete r;
 }
 
-napi_value start_async(napi_env env, lf_context* ctx, std::function<int(lf_context*)> fn, const char* what) {
-  if (!ctx) {
+napi_value start_async(napi_env env, CtxHolder* h, std::function<int(lf_context*)> fn, const char* what) {
+  if (!h || !h->alive) {
     napi_throw_error(env, nullptr, "the context was destroyed");
     return nullptr;
   }
   AsyncRun* r = new AsyncRun();
-  r->ctx = ctx;
+  ++h->refs;   // released in async_complete
+  r->h = h;
   r->fn = std::move(fn);
   r->what = what;
   napi_value promise, name;
@@ -110,6 +134,7 @@ napi_value start_async(napi_env env, lf_context* ctx, std::function<int(lf_conte
       napi_create_string_utf8(env, what, NAPI_AUTO_LENGTH, &name) != napi_ok ||
       napi_create_async_work(env, nullptr, name, async_execute, async_complete, r, &r->work) != napi_ok ||
       napi_queue_async_work(env, r->work) != napi_ok) {
+    holder_release(h);
     delete r;
     napi_throw_error(env, nullptr, "could not queue the async work");
     return nullptr;
@@ -119,7 +144,10 @@ napi_value start_async(napi_env env, lf_context* ctx, std::function<int(lf_conte
 
 void buf_finalize(napi_env, void* data, void*) {
   DevBuf* b = static_cast<DevBuf*>(data);
-  if (b->ptr && b->h->alive) lf_free(b->h->ctx, b->ptr);
+  {
+    CtxGuard g(b->h);
+    if (b->ptr && b->h->alive) lf_free(b->h->ctx, b->ptr);
+  }
   holder_release(b->h);
   delete b;
 }
@@ -127,9 +155,12 @@ void buf_finalize(napi_env, void* data, void*) {
 // a context object collected without contextDestroy releases its device memory here
 void ctx_finalize(napi_env, void* data, void*) {
   CtxHolder* h = static_cast<CtxHolder*>(data);
-  if (h->alive) {
-    lf_context_destroy(h->ctx);
-    h->alive = false;
+  {
+    CtxGuard g(h);
+    if (h->alive) {
+      lf_context_destroy(h->ctx);
+      h->alive = false;
+    }
   }
   holder_release(h);
 }
@@ -315,7 +346,7 @@ napi_value ContextCreate(napi_env env, napi_callback_info info) {
   if (get_args(env, info, 1, argv)) napi_get_value_int32(env, argv[0], &dev);
   lf_context* ctx = lf_context_create(dev);
   if (!ctx) return throw_lf(env, LF_ERR_DEVICE, "lf_context_create");
-  CtxHolder* h = new CtxHolder{ctx, true, 1};
+  CtxHolder* h = new CtxHolder{ctx, true, 1, {}};
   napi_value ext;
   NAPI_OK(napi_create_external(env, h, ctx_finalize, nullptr, &ext));
   return ext;
@@ -325,6 +356,7 @@ napi_value ContextDestroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
   CtxHolder* h = as_holder(env, argv[0]);
+  CtxGuard g(h);
   if (h && h->alive) {
     lf_context_destroy(h->ctx);
     h->alive = false;
@@ -339,6 +371,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
     napi_throw_type_error(env, nullptr, "upload(ctx, typedArray)");
     return nullptr;
   }
+  CtxGuard guard(as_holder(env, argv[0]));
   lf_context* ctx = as_ctx(env, argv[0]);
   if (!ctx) return throw_lf(env, LF_ERR_INVALID, "upload: the context was destroyed");
   void* data = nullptr;
@@ -384,6 +417,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
 napi_value Alloc(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!get_args(env, info, 2, argv)) return nullptr;
+  CtxGuard guard(as_holder(env, argv[0]));
   lf_context* ctx = as_ctx(env, argv[0]);
   if (!ctx) return throw_lf(env, LF_ERR_INVALID, "alloc: the context was destroyed");
   double bytes = 0;
@@ -403,6 +437,7 @@ napi_value Alloc(napi_env env, napi_callback_info info) {
 napi_value Download(napi_env env, napi_callback_info info) {
   napi_value argv[3];
   if (!get_args(env, info, 3, argv)) return nullptr;
+  CtxGuard guard(as_holder(env, argv[0]));
   lf_context* ctx = as_ctx(env, argv[0]);
   if (!ctx) {
     napi_throw_error(env, nullptr, "download: the context was destroyed");
@@ -441,6 +476,7 @@ napi_value Free(napi_env env, napi_callback_info info) {
   void* p = nullptr;
   napi_get_value_external(env, argv[0], &p);
   DevBuf* b = static_cast<DevBuf*>(p);
+  CtxGuard g(b ? b->h : nullptr);
   if (b && b->ptr) {
     if (b->h->alive) lf_free(b->h->ctx, b->ptr);
     b->ptr = nullptr;
@@ -451,6 +487,7 @@ napi_value Free(napi_env env, napi_callback_info info) {
 napi_value Synchronize(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_synchronize(as_ctx(env, argv[0]));
   if (rc != LF_OK) return throw_lf(env, rc, "lf_synchronize");
   return undefined_value(env);
@@ -460,6 +497,7 @@ napi_value MemoryStats(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
   size_t cur = 0, peak = 0, cnt = 0;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_memory_stats(as_ctx(env, argv[0]), &cur, &peak, &cnt);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_memory_stats");
   napi_value o, v;
@@ -478,6 +516,7 @@ napi_value ProfileEnable(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 2, argv)) return nullptr;
   bool on = false;
   napi_get_value_bool(env, argv[1], &on);
+  CtxGuard guard(as_holder(env, argv[0]));
   lf_profile_enable(as_ctx(env, argv[0]), on ? 1 : 0);
   return undefined_value(env);
 }
@@ -488,6 +527,7 @@ napi_value ProfileRead(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, argv)) return nullptr;
   const int cap = 4096;
   lf_kernel_timing* recs = static_cast<lf_kernel_timing*>(calloc(cap, sizeof(lf_kernel_timing)));
+  CtxGuard guard(as_holder(env, argv[0]));
   int n = lf_profile_read(as_ctx(env, argv[0]), recs, cap);
   napi_value arr;
   napi_create_array_with_length(env, n > 0 ? n : 0, &arr);
@@ -531,6 +571,7 @@ napi_value TriMult(napi_env env, napi_callback_info info) {
   a.accumulate = get_int(env, o, "accumulate");
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_tri_mult(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_tri_mult");
   return undefined_value(env);
@@ -565,6 +606,7 @@ napi_value Attention(napi_env env, napi_callback_info info) {
   lf_attention_args a{};
   fill_attention(env, argv[1], a);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_attention(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_attention");
   return undefined_value(env);
@@ -588,6 +630,7 @@ napi_value Transition(napi_env env, napi_callback_info info) {
   a.chunk_bytes = (long long)get_num(env, o, "chunkBytes", 0);
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_transition(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_transition");
   return undefined_value(env);
@@ -615,6 +658,7 @@ napi_value OuterProductMean(napi_env env, napi_callback_info info) {
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   a.norm_epsilon = (float)get_num(env, o, "normEpsilon", 1e-3);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_outer_product_mean(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_outer_product_mean");
   return undefined_value(env);
@@ -622,13 +666,15 @@ napi_value OuterProductMean(napi_env env, napi_callback_info info) {
 
 lf_evoformer_weights evo_weights(napi_env env, napi_value w) {
   lf_evoformer_weights e{};
-  e.row_attention = att_weights(env, prop(env, w, "rowAttention"));
-  e.row_heads = get_int(env, w, "rowHeads");
+  if (has(env, w, "rowAttention")) {   // absent for the pair halves only
+    e.row_attention = att_weights(env, prop(env, w, "rowAttention"));
+    e.row_heads = get_int(env, w, "rowHeads");
+  }
   if (has(env, w, "columnAttention")) {   // absent in an extra-MSA block
     e.column_attention = att_weights(env, prop(env, w, "columnAttention"));
     e.column_heads = get_int(env, w, "columnHeads");
   }
-  e.msa_transition = tr_weights(env, prop(env, w, "msaTransition"));
+  if (has(env, w, "msaTransition")) e.msa_transition = tr_weights(env, prop(env, w, "msaTransition"));
   e.outer_product_mean = opm_w(env, prop(env, w, "outerProductMean"));
   e.tri_out = tri_weights(env, prop(env, w, "triOut"));
   e.tri_in = tri_weights(env, prop(env, w, "triIn"));
@@ -672,6 +718,7 @@ napi_value GlobalColumnAttention(napi_env env, napi_callback_info info) {
   a.accumulate = get_int(env, o, "accumulate");
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_global_column_attention(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_global_column_attention");
   return undefined_value(env);
@@ -711,9 +758,27 @@ napi_value EvoformerStack(napi_env env, napi_callback_info info) {
     ws[i] = evo_weights(env, e);
   }
   // returns a promise: the stack runs on a worker thread (see start_async)
-  return start_async(env, as_ctx(env, argv[0]), [a, ws, n](lf_context* c) {
+  return start_async(env, as_holder(env, argv[0]), [a, ws, n](lf_context* c) {
     return lf_evoformer_stack(c, &a, ws.data(), (int)n);
   }, "lf_evoformer_stack");
+}
+
+// evoformerPairStack(ctx, args, [blockWeights...]): the pair halves only (msa read, not written)
+napi_value EvoformerPairStack(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return nullptr;
+  lf_evoformer_block_args a = evo_args(env, argv[1]);
+  uint32_t n = 0;
+  napi_get_array_length(env, argv[2], &n);
+  std::vector<lf_evoformer_weights> ws(n > 0 ? n : 1);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, argv[2], i, &e);
+    ws[i] = evo_weights(env, e);
+  }
+  return start_async(env, as_holder(env, argv[0]), [a, ws, n](lf_context* c) {
+    return lf_evoformer_pair_stack(c, &a, ws.data(), (int)n);
+  }, "lf_evoformer_pair_stack");
 }
 
 // extraMsaStack(ctx, args, [blockWeights...]): Evoformer block weights with columnGlobal
@@ -732,7 +797,7 @@ napi_value ExtraMsaStack(napi_env env, napi_callback_info info) {
     ws[i].column_global_heads = get_int(env, e, "columnGlobalHeads");
   }
   // returns a promise: the stack runs on a worker thread (see start_async)
-  return start_async(env, as_ctx(env, argv[0]), [a, ws, n](lf_context* c) {
+  return start_async(env, as_holder(env, argv[0]), [a, ws, n](lf_context* c) {
     return lf_extra_msa_stack(c, &a, ws.data(), (int)n);
   }, "lf_extra_msa_stack");
 }
@@ -771,7 +836,7 @@ napi_value PairformerBlock(napi_env env, napi_callback_info info) {
   a.transition_chunk_bytes = (long long)get_num(env, o, "transitionChunkBytes", 0);
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   // returns a promise: the block runs on a worker thread (see start_async)
-  return start_async(env, as_ctx(env, argv[0]), [a, w](lf_context* c) {
+  return start_async(env, as_holder(env, argv[0]), [a, w](lf_context* c) {
     lf_pairformer_block_args args = a;
     args.w = &w;
     return lf_pairformer_block(c, &args);
@@ -824,7 +889,7 @@ napi_value MsaModuleBlock(napi_env env, napi_callback_info info) {
   a.transition_chunk_bytes = (long long)get_num(env, o, "transitionChunkBytes", 0);
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   // returns a promise: the block runs on a worker thread (see start_async)
-  return start_async(env, as_ctx(env, argv[0]), [a, w](lf_context* c) {
+  return start_async(env, as_holder(env, argv[0]), [a, w](lf_context* c) {
     lf_msa_block_args args = a;
     args.w = &w;
     return lf_msa_module_block(c, &args);
@@ -874,6 +939,7 @@ napi_value InputEmbedder(napi_env env, napi_callback_info info) {
   a.extra = get_dev(env, o, "extra");
   a.epsilon = (float)get_num(env, o, "epsilon", 1e-5);
   a.w = &w;
+  CtxGuard guard(as_holder(env, argv[0]));
   int rc = lf_input_embedder(as_ctx(env, argv[0]), &a);
   if (rc != LF_OK) return throw_lf(env, rc, "lf_input_embedder");
   return undefined_value(env);
@@ -888,7 +954,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"alloc", Alloc}, {"download", Download}, {"free", Free}, {"synchronize", Synchronize},
       {"memoryStats", MemoryStats}, {"profileEnable", ProfileEnable}, {"profileRead", ProfileRead},
       {"version", Version}, {"triMult", TriMult}, {"attention", Attention}, {"transition", Transition},
-      {"outerProductMean", OuterProductMean}, {"evoformerStack", EvoformerStack},
+      {"outerProductMean", OuterProductMean}, {"evoformerStack", EvoformerStack}, {"evoformerPairStack", EvoformerPairStack},
       {"pairformerBlock", PairformerBlock}, {"globalColumnAttention", GlobalColumnAttention},
       {"extraMsaStack", ExtraMsaStack}, {"msaModuleBlock", MsaModuleBlock}, {"inputEmbedder", InputEmbedder},
   };

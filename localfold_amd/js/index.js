@@ -40,6 +40,7 @@ function createDevice(ordinal) {
     addon: a,
     resident: new WeakMap(),   // weight object -> device-resident records (uploaded once)
     profile: false,
+    tail: Promise.resolve(),   // the last queued run (one run at a time per context)
     destroy: function destroy() { a.contextDestroy(ctx); },
   };
 }
@@ -154,6 +155,77 @@ function validateOuterProductMeanInput(input) {
   for (let i = 0; i < expected.length; i += 1) expectLength(expected[i][0], expected[i][1], expected[i][2]);
 }
 
+// ---- CPU reference of the outgoing update ----------------------------------------------
+
+// webgpu/kernels/triangle/cpu-reference.js:55-99, exported as the reference exports it
+// (webgpu/index.js:60) for callers that check a device result on the host.  No GPU class calls
+// it.  Values are stored as float32 at the points the reference stores them (layer-norm
+// outputs, each projection, the gated a/b, the contraction, the output), with double sums in
+// between.  a and b are kept channel-major so that the contraction walks contiguous memory.
+function triangleMultiplicationOutgoingReference(input) {
+  validateTriangleInput(input);
+  const n = input.shape.length;
+  const cZ = input.shape.cZ;
+  const cH = input.shape.cHidden;
+  const eps = input.epsilon === undefined ? 1e-5 : input.epsilon;
+  const w = input.weights;
+  const pairs = n * n;
+  const sig = function sig(x) { return 1 / (1 + Math.exp(-x)); };
+  const rowNorm = function rowNorm(src, rows, c, scale, offset) {
+    const dst = new Float32Array(rows * c);
+    for (let r = 0; r < rows; r += 1) {
+      const o = r * c;
+      let sum = 0;
+      for (let k = 0; k < c; k += 1) sum += src[o + k];
+      const mean = sum / c;
+      let sq = 0;
+      for (let k = 0; k < c; k += 1) { const d = src[o + k] - mean; sq += d * d; }
+      const rstd = 1 / Math.sqrt(sq / c + eps);
+      for (let k = 0; k < c; k += 1) dst[o + k] = (src[o + k] - mean) * rstd * scale[k] + offset[k];
+    }
+    return dst;
+  };
+  // one (out,in) matrix row against one input row
+  const dot = function dot(x, xo, m, mo, c) {
+    let v = 0;
+    for (let k = 0; k < c; k += 1) v += x[xo + k] * m[mo + k];
+    return v;
+  };
+  const zn = rowNorm(input.z, pairs, cZ, w.layerNormInWeight, w.layerNormInBias);
+  const a = new Float32Array(cH * pairs);
+  const b = new Float32Array(cH * pairs);
+  const f = Math.fround;
+  for (let p = 0; p < pairs; p += 1) {
+    const m = input.mask[p];
+    for (let h = 0; h < cH; h += 1) {
+      const ap = f(w.linearAPBias[h] + dot(zn, p * cZ, w.linearAPWeight, h * cZ, cZ));
+      const ag = f(w.linearAGBias[h] + dot(zn, p * cZ, w.linearAGWeight, h * cZ, cZ));
+      const bp = f(w.linearBPBias[h] + dot(zn, p * cZ, w.linearBPWeight, h * cZ, cZ));
+      const bg = f(w.linearBGBias[h] + dot(zn, p * cZ, w.linearBGWeight, h * cZ, cZ));
+      a[h * pairs + p] = ap * sig(ag) * m;
+      b[h * pairs + p] = bp * sig(bg) * m;
+    }
+  }
+  // x[i, j, h] = sum_k a[h, i, k] b[h, j, k]
+  const x = new Float32Array(pairs * cH);
+  for (let h = 0; h < cH; h += 1) {
+    const base = h * pairs;
+    for (let i = 0; i < n; i += 1) {
+      for (let j = 0; j < n; j += 1) x[(i * n + j) * cH + h] = dot(a, base + i * n, b, base + j * n, n);
+    }
+  }
+  const xn = rowNorm(x, pairs, cH, w.layerNormOutWeight, w.layerNormOutBias);
+  const out = new Float32Array(pairs * cZ);
+  for (let p = 0; p < pairs; p += 1) {
+    for (let c = 0; c < cZ; c += 1) {
+      const y = f(w.linearZBias[c] + dot(xn, p * cH, w.linearZWeight, c * cH, cH));
+      const g = f(w.linearGBias[c] + dot(zn, p * cZ, w.linearGWeight, c * cZ, cZ));
+      out[p * cZ + c] = y * sig(g);
+    }
+  }
+  return out;
+}
+
 // webgpu/kernels/triangle/types.js:50-69, plus the relative Frobenius error
 function errorMetrics(actual, expected) {
   if (actual.length !== expected.length || actual.length === 0) {
@@ -246,6 +318,16 @@ Uploads.prototype.vec = function vec(values) {
   if (values === undefined || values === null) return null;
   return this.buffer(values instanceof Float32Array ? values : Float32Array.from(values));
 };
+// The kernels fetch int5 codes as aligned 32-bit word pairs, which reads up to 3 bytes past
+// the last code byte; the reference's records carry those bytes (a slack byte, then the scale
+// table), a bare code array gets 4 zero bytes appended.
+function padCodes(codes) {
+  const bytes = codes instanceof Uint8Array ? codes : new Uint8Array(codes.buffer, codes.byteOffset, codes.byteLength);
+  const out = new Uint8Array(bytes.length + 4);
+  out.set(bytes);
+  return out;
+}
+
 // A weight matrix stored rows x cols in `layout` ('in_out' or 'out_in'): Float32Array values
 // or a quantised record {dtype, codes, scales, zeros?, block}.
 Uploads.prototype.weight = function weight(value, layout, rows, cols) {
@@ -253,7 +335,7 @@ Uploads.prototype.weight = function weight(value, layout, rows, cols) {
   if (value.codes !== undefined) {
     return {
       dtype: value.dtype, layout: layout, rows: rows, cols: cols, group: value.block || 0,
-      data: this.buffer(value.codes), scales: this.buffer(value.scales),
+      data: this.buffer(value.dtype === 'int5' ? padCodes(value.codes) : value.codes), scales: this.buffer(value.scales),
       zeros: value.zeros ? this.buffer(value.zeros) : null,
     };
   }
@@ -468,14 +550,16 @@ function evoformerBlockWeights(up, w, dims) {
   const col = w.msaColumnAttention;   // absent in an extra-MSA block
   const st = w.triangleAttentionStarting;
   const en = w.triangleAttentionEnding;
+  // the MSA-side records are absent when only the pair halves run (ExtraMsaPairStackGpu)
   const out = {
-    rowAttention: attentionWeights(up, row.attention, dims.cM, dims.cM,
+    rowAttention: row ? attentionWeights(up, row.attention, dims.cM, dims.cM,
       { source: 'separate', channels: dims.cZ, layerNormScale: row.pairBias.layerNormScale,
-        layerNormOffset: row.pairBias.layerNormOffset, projectionWeight: row.pairBias.projectionWeight }, row.heads),
-    rowHeads: row.heads,
+        layerNormOffset: row.pairBias.layerNormOffset, projectionWeight: row.pairBias.projectionWeight }, row.heads)
+      : undefined,
+    rowHeads: row ? row.heads : 0,
     columnAttention: col ? attentionWeights(up, col.attention, dims.cM, dims.cM, null, col.heads) : undefined,
     columnHeads: col ? col.heads : 0,
-    msaTransition: transitionWeights(up, w.msaTransition, dims.cM, dims.msaHidden),
+    msaTransition: w.msaTransition ? transitionWeights(up, w.msaTransition, dims.cM, dims.msaHidden) : undefined,
     outerProductMean: opmWeights(up, w.outerProductMean, dims.cM, dims.cOuter, dims.cZ),
     triOut: triangleWeights(up, w.triangleMultiplicationOutgoing, dims.cZ, dims.triangleHidden),
     triIn: triangleWeights(up, w.triangleMultiplicationIncoming, dims.cZ, dims.triangleHidden),
@@ -488,6 +572,8 @@ function evoformerBlockWeights(up, w, dims) {
     pairTransition: transitionWeights(up, w.pairTransition, dims.cZ, dims.pairHidden),
   };
   if (!col) delete out.columnAttention;
+  if (!row) delete out.rowAttention;
+  if (!w.msaTransition) delete out.msaTransition;
   return out;
 
 }
@@ -495,7 +581,7 @@ function evoformerBlockWeights(up, w, dims) {
 function blockDims(input, w) {
   return {
     cM: input.cM, cZ: input.cZ, cOuter: input.cOuter, triangleHidden: input.triangleHidden,
-    msaHidden: input.msaHidden || (w.msaTransition.firstBias.length),
+    msaHidden: input.msaHidden || (w.msaTransition ? w.msaTransition.firstBias.length : 4 * input.cM),
     pairHidden: input.pairHidden || (w.pairTransition.firstBias.length),
   };
 }
@@ -658,6 +744,42 @@ function pairformerBlockWeights(up, w, cZ, cS) {
   }
   return out;
 }
+
+// webgpu/af2/evoformer/stack.js:163-247: run(input) with input.blockWeights, running the pair
+// half of each block (encodeEvoformerPairBlock, block.js:1663-1713): the outer product mean of
+// the msa, which is read and not updated, then the pair steps.  Returns {pair,
+// elapsedMilliseconds, memory}.
+function ExtraMsaPairStackGpu(device) { this.device = device; }
+ExtraMsaPairStackGpu.prototype.run = async function run(input) {
+  const device = this.device;
+  let up = null;
+  try {
+    const blocks = input.blockWeights;
+    if (!Array.isArray(blocks) || blocks.length === 0) throw new RangeError('blockWeights must be a non-empty array');
+    const dims = blockDims(input, blocks[0]);
+    up = new Uploads(device);
+    const start = performance.now();
+    const ws = blocks.map(function each(w) {
+      return resident(device, w, function build(wu) { return evoformerBlockWeights(wu, w, dims); });
+    });
+    const msaElements = input.sequences * input.length * input.cM;
+    const pairElements = input.length * input.length * input.cZ;
+    expectLength('msa', input.msa, msaElements);
+    expectLength('pair', input.pair, pairElements);
+    const msa = up.vec(input.msa);
+    const pair = up.vec(input.pair);
+    await device.addon.evoformerPairStack(device.ctx, {
+      sequences: input.sequences, length: input.length, cM: dims.cM, cZ: dims.cZ, cOuter: dims.cOuter,
+      triangleHidden: dims.triangleHidden, msaHidden: dims.msaHidden, pairHidden: dims.pairHidden,
+      msaDtype: ACT.float32, msa: msa, pairDtype: ACT.float32, pair: pair,
+      msaMask: up.vec(input.msaMask), pairMask: up.vec(input.pairMask), epsilon: 1e-5,
+    }, ws);
+    const r = finish(device, up, [{ buffer: pair, elements: pairElements }], start);
+    return { pair: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels };
+  } finally {
+    if (up) up.release();
+  }
+};
 
 // webgpu/af3/trunk/pairformer-block.js:246-300: run(state, blocks, dialect, options) with
 // state {pair, single, pairMask, seqMask, tokens}; dialect.swapTransposedBias has no default.
@@ -858,7 +980,11 @@ const TRIANGLE_WEIGHT_NAMES = [
 ];
 
 function loadTriangleReferenceBundleFromFiles(manifestPath) {
-  return new Promise(function load(resolve) {
+  return new Promise(function load(resolve) { resolve(loadTriangleReferenceBundleFromFilesSync(manifestPath)); });
+}
+
+function loadTriangleReferenceBundleFromFilesSync(manifestPath) {
+  {
     const manifest = JSON.parse(fs.readFileSync(manifestPath, 'utf8'));
     if (manifest.formatVersion !== 1 || manifest.operator !== 'TriangleMultiplicationOutgoing') {
       throw new Error('unsupported triangle reference manifest');
@@ -874,16 +1000,39 @@ function loadTriangleReferenceBundleFromFiles(manifestPath) {
     };
     const weights = {};
     TRIANGLE_WEIGHT_NAMES.forEach(function each(name) { weights[name] = tensor(name); });
-    resolve({
+    return {
       source: manifest.source,
       input: { shape: manifest.shape, epsilon: manifest.epsilon, z: tensor('z'), mask: tensor('mask'), weights: weights },
       expected: tensor('expected'),
-    });
-  });
+    };
+  }
 }
+
+// ---- one run at a time per device -------------------------------------------------------
+
+// A device's context serves one run at a time: the stacks run on a libuv worker thread, and a
+// second run on the same context (Promise.all over two runs, say) must not upload, allocate
+// or launch while the first is pending.  Every run() therefore waits for the device's
+// previous run to settle (the addon also locks the context, so an unqueued call blocks
+// rather than races).
+function serialiseRuns(Cls) {
+  const inner = Cls.prototype.run;
+  Cls.prototype.run = function run() {
+    const self = this;
+    const args = arguments;
+    const dev = this.device;
+    const go = function go() { return inner.apply(self, args); };
+    const p = (dev.tail || Promise.resolve()).then(go);
+    dev.tail = p.then(function settled() {}, function settled() {});
+    return p;
+  };
+}
+[TriangleMultiplicationGpu, AttentionGpu, TransitionGpu, OuterProductMeanGpu, EvoformerBlockGpu, EvoformerStackGpu,
+  ExtraMsaStackGpu, ExtraMsaPairStackGpu, Af3PairformerStackGpu, Af3MsaStackGpu, InputEmbedderGpu].forEach(serialiseRuns);
 
 module.exports = {
   loadTriangleReferenceBundleFromFiles: loadTriangleReferenceBundleFromFiles,
+  loadTriangleReferenceBundleFromFilesSync: loadTriangleReferenceBundleFromFilesSync,
   createDevice: createDevice,
   TriangleMultiplicationOutgoingGpu: TriangleMultiplicationOutgoingGpu,
   TriangleMultiplicationIncomingGpu: TriangleMultiplicationIncomingGpu,
@@ -893,6 +1042,7 @@ module.exports = {
   EvoformerBlockGpu: EvoformerBlockGpu,
   EvoformerStackGpu: EvoformerStackGpu,
   ExtraMsaStackGpu: ExtraMsaStackGpu,
+  ExtraMsaPairStackGpu: ExtraMsaPairStackGpu,
   Af3PairformerStackGpu: Af3PairformerStackGpu,
   Af3MsaStackGpu: Af3MsaStackGpu,
   InputEmbedderGpu: InputEmbedderGpu,
@@ -901,6 +1051,7 @@ module.exports = {
   validateTransitionInput: validateTransitionInput,
   validateOuterProductMeanInput: validateOuterProductMeanInput,
   errorMetrics: errorMetrics,
+  triangleMultiplicationOutgoingReference: triangleMultiplicationOutgoingReference,
   generator: generator,
   createDeterministicTriangleInput: createDeterministicTriangleInput,
   addon: addon,

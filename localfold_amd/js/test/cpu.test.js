@@ -2,7 +2,7 @@
 // CPU checks of the Node host (no GPU): the reference's validation errors and errorMetrics
 // (test/cpu-reference.test.js:29-41), the generator against Python's vectorised restatement
 // (values passed in a JSON file), and the addon's exported functions.
-//   node cpu.test.js <generator-expectations.json>
+//   node cpu.test.js <generator-expectations.json> [fixture-directory]
 const assert = require('assert');
 const fs = require('fs');
 const lf = require('../index.js');
@@ -61,10 +61,47 @@ check('generator matches the vectorised restatement', function t() {
   });
 });
 
+check('CPU reference matches the committed fixtures', function t() {
+  const dir = process.argv[3];
+  if (!dir) return;
+  // bounds of test/cpu-reference.test.js:18-27 for the OpenFold capture; 1e-5 / 1e-4 for the
+  // AlphaFold captures, whose expected values come from an f32 run of a different program
+  const bounds = { openfold_triangle_small: [1e-7, 1e-6] };
+  fs.readdirSync(dir).forEach(function each(name) {
+    const manifest = dir + '/' + name + '/manifest.json';
+    if (!fs.existsSync(manifest)) return;
+    const f = lf.loadTriangleReferenceBundleFromFilesSync(manifest);
+    const actual = lf.triangleMultiplicationOutgoingReference(f.input);
+    const again = lf.triangleMultiplicationOutgoingReference(f.input);
+    assert.deepStrictEqual(Array.from(actual), Array.from(again));
+    const m = lf.errorMetrics(actual, f.expected);
+    const b = bounds[name] || [1e-5, 1e-4];
+    console.log('     ' + name + ' mean ' + m.meanAbsoluteError + ' max ' + m.maxAbsoluteError);
+    assert.ok(m.meanAbsoluteError < b[0] && m.maxAbsoluteError < b[1], name + ' ' + JSON.stringify(m));
+  });
+});
+
+check('CPU reference is deterministic and finite on the deterministic input', function t() {
+  const input = lf.createDeterministicTriangleInput({ length: 3, cZ: 4, cHidden: 5 }, 42);
+  const first = lf.triangleMultiplicationOutgoingReference(input);
+  assert.strictEqual(first.length, 36);
+  assert.ok(Array.from(first).every(Number.isFinite));
+  assert.deepStrictEqual(Array.from(first), Array.from(lf.triangleMultiplicationOutgoingReference(input)));
+});
+
+check('library exports the reference surface', function t() {
+  ['TriangleMultiplicationOutgoingGpu', 'TriangleMultiplicationIncomingGpu', 'TransitionGpu', 'OuterProductMeanGpu',
+    'AttentionGpu', 'EvoformerBlockGpu', 'EvoformerStackGpu', 'ExtraMsaPairStackGpu', 'ExtraMsaStackGpu',
+    'InputEmbedderGpu', 'Af3PairformerStackGpu', 'triangleMultiplicationOutgoingReference', 'errorMetrics',
+    'validateTriangleInput', 'createDeterministicTriangleInput'].forEach(function each(n) {
+    assert.strictEqual(typeof lf[n], 'function', n);
+  });
+});
+
 check('addon exports every entry point', function t() {
   const names = ['contextCreate', 'contextDestroy', 'upload', 'alloc', 'download', 'free', 'synchronize', 'memoryStats',
     'profileEnable', 'profileRead', 'triMult', 'attention', 'transition', 'outerProductMean', 'evoformerStack',
-    'pairformerBlock', 'version'];
+    'evoformerPairStack', 'extraMsaStack', 'pairformerBlock', 'version'];
   const a = lf.addon();
   names.forEach(function each(n) { assert.strictEqual(typeof a[n], 'function', n); });
 });

@@ -94,6 +94,34 @@ async function main() {
   report('extra-MSA stack msa', lf.errorMetrics(exOut.msa, ex.expectedMsa), { mean: 2e-3, max: 2e-2 });
   report('extra-MSA stack pair', lf.errorMetrics(exOut.pair, ex.expectedPair), { mean: 2e-3, max: 2e-2 });
 
+  // ExtraMsaPairStackGpu: the pair halves only, from weights that carry no MSA-side records
+  const pairOnly = ex.input.blockWeights.map(function strip(w) {
+    const o = Object.assign({}, w);
+    delete o.msaRowAttention;
+    delete o.msaColumnGlobalAttention;
+    delete o.msaTransition;
+    return o;
+  });
+  const psOut = await new lf.ExtraMsaPairStackGpu(device).run(Object.assign({}, ex.input, { blockWeights: pairOnly }));
+  report('extra-MSA pair stack pair', lf.errorMetrics(psOut.pair, ex.expectedPairOnly), { mean: 2e-3, max: 2e-2 });
+
+  // Runs started together on one device are queued: each result equals the serial one.
+  const together = await Promise.all([
+    new lf.ExtraMsaStackGpu(device).run(ex.input), new lf.ExtraMsaStackGpu(device).run(ex.input),
+    new lf.EvoformerBlockGpu(device).run(ev.input), new lf.ExtraMsaPairStackGpu(device).run(
+      Object.assign({}, ex.input, { blockWeights: pairOnly })),
+  ]);
+  const same = function same(name, a, b) {
+    const m = lf.errorMetrics(a, b);
+    const ok = m.maxAbsoluteError === 0;
+    if (!ok) failures += 1;
+    console.log((ok ? 'ok   ' : 'FAIL ') + 'concurrent runs: ' + name + ' ' + JSON.stringify(m));
+  };
+  same('extra stack #1 pair', together[0].pair, exOut.pair);
+  same('extra stack #2 msa', together[1].msa, exOut.msa);
+  same('evoformer block pair', together[2].pair, evOut.pair);
+  same('pair stack pair', together[3].pair, psOut.pair);
+
   const pf = revive(JSON.parse(fs.readFileSync(path.join(dir, 'pairformer.json'), 'utf8')));
   const pfOut = await new lf.Af3PairformerStackGpu(device).run(pf.state, pf.blocks, { swapTransposedBias: false });
   report('pairformer pair', lf.errorMetrics(pfOut.pair, pf.expectedPair), { mean: 2e-3, max: 2e-2 });

@@ -34,10 +34,20 @@ functions, tests/test_oracle_af3.py):
 * attention (all modes)   - brute-force per-element softmax loops on tiny inputs;
                             invariants: one unmasked key -> that value row; transpose
                             identity; zero bias -> plain attention
-* outer_product_mean_af2  - S=1 closed form and the count identity
+* outer_product_mean_af2  - S=1 closed form; the count identity at S=5 with ragged
+                            masks (constant LN output, so the sum over sequences is the
+                            coverage count times one outer product); a per-element loop
+                            at S=4
 * outer_product_mean_af3  - the reference's hand-computed cases (`test/af3-msa.test.js:40-107`:
                             sum before divide, per-pair coverage, uncovered pair = 0,
                             asymmetry) plus channel order and bias-before-divide
+* global_column_attention_af2 - per-element loops of the four kernels of
+                            `webgpu/af2/evoformer/block.js:101-400` (64-lane online softmax);
+                            a two-sequence closed form that fixes 1/sqrt(d), the masked mean
+                            and the -1e9; permutation and masked-sequence invariants
+* msa_pair_weighted_averaging_af3 - a per-element loop of `msaAttention` on an asymmetric
+                            pair (the [h][i][j] orientation); one-token, zero-logit, deleted-
+                            token and all-masked closed forms
 * single_attention_af3    - per-element loops of `singleAttention` on tiny inputs; a
                             two-token closed form that fixes the 1/sqrt(d) scale, the q bias
                             and the pair logit; masked-key and one-unmasked-key invariants

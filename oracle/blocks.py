@@ -45,6 +45,13 @@ def extra_msa_block_af2(msa, pair, msa_mask, pair_mask, w, eps=1e-5):
     return msa, _pair_steps(msa, pair, msa_mask, pair_mask, w, eps)
 
 
+def evoformer_pair_block_af2(msa, pair, msa_mask, pair_mask, w, eps=1e-5):
+    """The pair half of an Evoformer block (`encodeEvoformerPairBlock`,
+    `webgpu/af2/evoformer/block.js:1663-1713`), a block of `ExtraMsaPairStackGpu`
+    (`webgpu/af2/evoformer/stack.js:163-247`): the msa is read, not updated.  Returns the pair."""
+    return _pair_steps(msa, pair, msa_mask, pair_mask, w, eps)
+
+
 def _pair_steps(msa, pair, msa_mask, pair_mask, w, eps):
     """OPM, triangle multiplication out/in, triangle attention start/end, pair transition."""
     pair = _add(pair, ops.outer_product_mean_af2(msa, msa_mask, w["outerProductMean"], eps))

@@ -148,6 +148,38 @@ def test_config4_stack_48_blocks(ctx, stack48):
         print(f"48-block stack {name}: rms(expected) {rms:.2f} {m}", flush=True)
 
 
+# ---- config 4: later blocks of the full-shape stack ----------------------------------------
+
+@pytest.mark.parametrize("k", [23, 47])
+def test_config4_full_shape_stack_block_k(ctx, config4, k):
+    """The 48-block stack at the full config-4 shape (N_res = 384, N_seq = 512, 48 distinct
+    int8 weight sets, f32 residual stream): the GPU stack runs blocks 0 .. k-1, and block k
+    then runs once on the GPU and once in the oracle from that same GPU state, held to the
+    unscaled north-star bound (max abs <= 2e-2, relative Frobenius <= 5e-3).  Block k sees
+    activations grown by k blocks (pair rms ~ 6-12), which the block-0 test does not."""
+    import torch
+    from localfold_amd import device as D
+    weights = [config4["weights"]] + [S.quantise_tree(S.config1_inputs(seed=300 + b, n=1)[0], "int8", 64)
+                                      for b in range(k)]
+    dw = D.DeviceWeights(ctx.device)
+    ws = [D.evoformer_weights(dw, w) for w in weights]
+    mm, pm = _dev(ctx, config4["msa_mask"]), _dev(ctx, config4["pair_mask"])
+    msa, pair = _dev(ctx, config4["msa"]), _dev(ctx, config4["pair"])
+    D.evoformer_stack(ctx, msa, pair, mm, pm, ws[:k], weights[0])
+    torch.cuda.synchronize()
+    m0, p0 = msa.cpu().numpy(), pair.cpu().numpy()
+    assert np.isfinite(m0).all() and np.isfinite(p0).all()
+    D.evoformer_block(ctx, msa, pair, mm, pm, ws[k], weights[k])
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    rm, rp = blocks.evoformer_block_af2(m0, p0, config4["msa_mask"], config4["pair_mask"], _decoded(weights[k]))
+    print(f"config 4 oracle block {k}: {time.perf_counter() - t:.1f} s; input pair rms "
+          f"{float(np.sqrt(np.mean(np.square(p0, dtype=np.float64)))):.2f}", flush=True)
+    for name, got, ref in (("msa", msa, rm), ("pair", pair, rp)):
+        print(f"full-shape stack block {k} {name}: {H.metrics(got.cpu().numpy(), ref)}", flush=True)
+        H.assert_close(got.cpu().numpy(), ref, label=f"full-shape stack block {k} {name}")
+
+
 # ---- config 5: the AF3 Pairformer block ---------------------------------------------------
 
 def _config5(n, seed=21, padded=32):

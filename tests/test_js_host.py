@@ -32,7 +32,14 @@ def test_js_cpu_suite(tmp_path):
     cases = [{"seed": s, "values": S.uniform_stream(s, 300).tolist()} for s in (0, 7, 1000 + 384, 0xFFFFFFFF)]
     p = tmp_path / "gen.json"
     p.write_text(json.dumps(cases))
-    r = _run_node("cpu.test.js", p)
+    fx = tmp_path / "fixtures"
+    fx.mkdir()
+    for name in H.FIXTURES:
+        _write_fixture_dir(name, fx)
+    r = subprocess.run([NODE, str(JS / "test" / "cpu.test.js"), str(p), str(fx)], capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout)
+    print(r.stderr[-3000:])
     assert r.returncode == 0 and "FAIL" not in r.stdout
 
 
@@ -130,6 +137,10 @@ def test_js_gpu_suite(tmp_path):
                     "sequences": 5, "length": 14, "cM": 64, "cZ": 32, "cOuter": 8, "triangleHidden": 32,
                     "blockWeights": xws},
           "expectedMsa": xm, "expectedPair": xp}
+    xp2 = xa["pair"]
+    for xw in xws:
+        xp2 = blocks.evoformer_pair_block_af2(xa["msa"], xp2, xa["msaMask"], xa["pairMask"], xw)
+    ex["expectedPairOnly"] = xp2
     (tmp_path / "extra.json").write_text(json.dumps(_dump_tree(ex, tmp_path, "ex")))
 
     # Af3PairformerStackGpu: two blocks

@@ -203,3 +203,74 @@ def test_msa_module_block(ctx, s, n, before):
     rm, rp = blocks.msa_block_af3(act["msa"], act["pair"], act["msaMask"], act["pairMask"], w, before)
     H.assert_close(msa.cpu().numpy(), rm, label=f"msa module msa before={before}")
     H.assert_close(pair.cpu().numpy(), rp, label=f"msa module pair before={before}")
+
+
+def _fast_ln_loop(row, scale, offset, eps=1e-5):
+    """AF3 layerNorm of one row with the fast variance E[x^2] - E[x]^2
+    (cpu/af3/trunk/pairformer.js:68-87), element by element."""
+    c = len(row)
+    mean = sum(float(v) for v in row) / c
+    var = sum(float(v) * float(v) for v in row) / c - mean * mean
+    inv = 1.0 / np.sqrt(var + eps)
+    return [(float(row[k]) - mean) * inv * float(scale[k]) + float(offset[k]) for k in range(c)]
+
+
+def _msa_attention_loop(msa, mask, pair, w):
+    """`msaAttention` (cpu/af3/trunk/msa.js:157-219) element by element: logits
+    flat[(i*N + j)*H + h] into weightsByHead[h][i][j] plus 1e9 (keyMask[j] - 1), softmax over
+    j, then averaged[s][i][h*d + e] = sum_j weightsByHead[h][i][j] v[s][j][h*d + e], gated and
+    projected."""
+    s_, n, c = msa.shape
+    cz = pair.shape[-1]
+    heads, d = w["heads"], w["dimension"]
+    hd = heads * d
+    x = [[_fast_ln_loop(msa[s, t], w["actNormScale"], w["actNormOffset"]) for t in range(n)] for s in range(s_)]
+    pn = [[_fast_ln_loop(pair[i, j], w["pairNormScale"], w["pairNormOffset"]) for j in range(n)] for i in range(n)]
+    pl = np.asarray(w["pairLogits"], np.float64)
+    flat = [0.0] * (n * n * heads)
+    for i in range(n):
+        for j in range(n):
+            for h in range(heads):
+                flat[(i * n + j) * heads + h] = sum(pn[i][j][k] * pl[k, h] for k in range(cz))
+    key_mask = [max([0.0] + [float(mask[s, t]) for s in range(s_)]) for t in range(n)]
+    weights = np.zeros((heads, n, n))
+    for h in range(heads):
+        for i in range(n):
+            row = [flat[(i * n + j) * heads + h] + 1e9 * (key_mask[j] - 1) for j in range(n)]
+            top = max(row)
+            e = [np.exp(v - top) for v in row]
+            tot = sum(e)
+            weights[h, i] = [v / tot for v in e]
+    vp, gq, op = (np.asarray(w[k], np.float64) for k in ("vProjection", "gatingQuery", "outputProjection"))
+    out = np.zeros((s_, n, c))
+    for s in range(s_):
+        values = [[sum(x[s][t][k] * vp[k, o] for k in range(c)) for o in range(hd)] for t in range(n)]
+        for i in range(n):
+            gated = []
+            for h in range(heads):
+                for e in range(d):
+                    tot = sum(weights[h, i, j] * values[j][h * d + e] for j in range(n))
+                    g = sum(x[s][i][k] * gq[k, h * d + e] for k in range(c))
+                    gated.append(tot / (1.0 + np.exp(-g)))
+            for o in range(c):
+                out[s, i, o] = sum(gated[q] * op[q, o] for q in range(hd))
+    return out
+
+
+def test_oracle_per_element_loop_asymmetric_logits():
+    """The oracle against a per-element loop of msaAttention on an asymmetric pair (so that
+    the logits' [h][i][j] orientation matters: swapping i and j fails), with logits scaled up
+    so the softmax is far from uniform, a token covered by one sequence only and one covered
+    by none."""
+    w, msa, pair, mask = _avg_inputs(3, 5, 12, 6, 2, 3, 11)
+    w = dict(w, pairLogits=(w["pairLogits"] * 4).astype(np.float32))
+    st = S.Stream(99)
+    pair = (pair + 2.0 * np.triu(st.normal(25).reshape(5, 5))[..., None]).astype(np.float32)
+    mask[:, 3] = 0
+    mask[1:, 1] = 0
+    got = ops.msa_pair_weighted_averaging_af3(msa, mask, pair, w)
+    ref = _msa_attention_loop(msa, mask, pair, w)
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
+    # the orientation is pinned: the transposed pair gives a different answer
+    swapped = ops.msa_pair_weighted_averaging_af3(msa, mask, pair.transpose(1, 0, 2).copy(), w)
+    assert np.abs(swapped - ref).max() > 1e-2

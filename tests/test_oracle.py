@@ -249,6 +249,68 @@ def test_opm_single_sequence_closed_form():
             np.testing.assert_allclose(out[i, j], o / (1e-3 + mask[0, i] * mask[0, j]), rtol=1e-5, atol=1e-5)
 
 
+def _opm_weights(s, cm, co, cz):
+    return {"layerNormScale": s.values(cm, 0.2, 1), "layerNormOffset": s.values(cm, 0.1),
+            "leftWeight": s.values(cm * co, 0.4).reshape(cm, co), "leftBias": s.values(co, 0.1),
+            "rightWeight": s.values(cm * co, 0.4).reshape(cm, co), "rightBias": s.values(co, 0.1),
+            "outputWeight": s.values(co * co * cz, 0.3).reshape(co * co, cz), "outputBias": s.values(cz, 0.05)}
+
+
+def test_opm_count_identity():
+    """S = 5 with ragged masks.  With the LN scale 0, every normalised row is the offset
+    beta, so l_si = m_si L and r_sj = m_sj R for fixed vectors L = beta Wl + bl and
+    R = beta Wr + br; the sum over sequences is then count_ij (L outer R), with
+    count_ij = sum_s m_si m_sj, and the update is ((count_ij vec(L outer R)) W + b) /
+    (1e-3 + count_ij) (outer-product-mean.js:702-742: bias, then the divide).  This fixes
+    the coverage denominator (not the sequence count, not the product of per-token counts),
+    the a*c + b flattening (L != R) and the bias-before-divide order."""
+    s = S.Stream(16)
+    n, cm, co, cz, seqs = 5, 8, 3, 4, 5
+    w = _opm_weights(s, cm, co, cz)
+    w["layerNormScale"] = np.zeros(cm, np.float32)
+    msa = s.values(seqs * n * cm, 1.0).reshape(seqs, n, cm)
+    mask = np.array([[1, 1, 1, 1, 1], [1, 0, 1, 1, 0], [0, 1, 1, 0, 0], [1, 1, 0, 1, 0], [1, 0, 1, 1, 0]],
+                    np.float32)
+    beta = np.asarray(w["layerNormOffset"], np.float64)
+    L = beta @ w["leftWeight"] + w["leftBias"]
+    R = beta @ w["rightWeight"] + w["rightBias"]
+    out = ops.outer_product_mean_af2(msa, mask, w)
+    for i in range(n):
+        for j in range(n):
+            count = sum(mask[t, i] * mask[t, j] for t in range(seqs))
+            o = (count * np.outer(L, R).reshape(-1)) @ w["outputWeight"] + w["outputBias"]
+            np.testing.assert_allclose(out[i, j], o / (1e-3 + count), rtol=1e-5, atol=1e-6)
+    # the pairs (0, 4), (4, 4) ... are covered by one sequence, (1, 2) by two, (0, 0) by four
+    assert {float(sum(mask[:, i] * mask[:, j])) for i in range(n) for j in range(n)} >= {1.0, 2.0, 4.0}
+
+
+def test_opm_per_element_loop_several_sequences():
+    """S = 4, ragged masks, general LN: the oracle against an element-by-element loop over
+    sequences, channel pairs (a, b) and outputs."""
+    s = S.Stream(17)
+    n, cm, co, cz, seqs = 4, 6, 3, 5, 4
+    w = _opm_weights(s, cm, co, cz)
+    msa = s.values(seqs * n * cm, 1.0).reshape(seqs, n, cm)
+    mask = np.array([[1, 1, 0, 1], [0, 1, 1, 1], [1, 1, 1, 0], [1, 0, 1, 1]], np.float32)
+    x = ops.layer_norm(msa, w["layerNormScale"], w["layerNormOffset"]).astype(np.float64)
+    out = ops.outer_product_mean_af2(msa, mask, w)
+    for i in range(n):
+        for j in range(n):
+            acc = np.zeros(co * co)
+            count = 0.0
+            for t in range(seqs):
+                count += mask[t, i] * mask[t, j]
+                for a in range(co):
+                    la = mask[t, i] * (sum(x[t, i, k] * w["leftWeight"][k, a] for k in range(cm)) + w["leftBias"][a])
+                    for b in range(co):
+                        rb = mask[t, j] * (sum(x[t, j, k] * w["rightWeight"][k, b] for k in range(cm))
+                                           + w["rightBias"][b])
+                        acc[a * co + b] += la * rb
+            for z in range(cz):
+                v = w["outputBias"][z] + sum(acc[q] * w["outputWeight"][q, z] for q in range(co * co))
+                np.testing.assert_allclose(out[i, j, z], v / (1e-3 + count), rtol=1e-5, atol=1e-6)
+
+
 # ---- codecs -------------------------------------------------------------------------------
 
 def _int5_record(codes_by_group, scales, zeros):
