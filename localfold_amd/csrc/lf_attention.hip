@@ -649,8 +649,12 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
   // every weight of the op (output projection, pair-bias and q/k/v/g projections) decoded
   // in one launch
   ExpandList xl;
-  WExp wo;
-  LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[7], &wo, 1.f, "attention.expand"));
+  WExp wo{};
+  // the output projection decodes its stored weights itself when it runs weight-resident
+  const Dst out_dst = a.transpose ? Dst{a.out, a.act_dtype, Q, C, (long long)B * C, C, 0, 1}
+                                  : dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+  const bool wo_inkernel = rowgemm_resident(ctx, (int)rows, HD, C, out_dst);
+  if (!wo_inkernel) LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[7], &wo, 1.f, "attention.expand"));
   // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
   // exact 0, which must not meet a non-finite value)
   if (pwa) {
@@ -772,11 +776,12 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     rp.K = HD;
     rp.N = C;
     rp.w = wo;
+    rp.wv = views[4];
+    rp.wview = wo_inkernel ? 1 : 0;
     rp.bias = w.o_bias;
     rp.op = OP_STORE;
     rp.resid = a.accumulate ? a.act : nullptr;
-    rp.dst = a.transpose ? Dst{a.out, a.act_dtype, Q, C, (long long)B * C, C, 0, 1}
-                         : dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+    rp.dst = out_dst;
     LF_TRY(launch_rowgemm(ctx, rp, "attention.output"));
   }
   return LF_OK;

@@ -216,8 +216,10 @@ int global_attention(lf_context* ctx, const lf_global_attention_args& a) {
   pp.g[3].dst = dst_rowmajor(G, DT_F16, (int)rows, Hd);
   // the projections and the output weights decoded in one launch
   ExpandList xl;
-  WExp wo;
-  LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[4], &wo, 1.f, "global.expand"));
+  WExp wo{};
+  const Dst out_dst = dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+  const bool wo_inkernel = rowgemm_resident(ctx, (int)rows, Hd, C, out_dst);
+  if (!wo_inkernel) LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[4], &wo, 1.f, "global.expand"));
   LF_TRY(lnproj_prepare(ctx, pp, bufs[5], &xl, "global.project"));
   LF_TRY(expand_flush(ctx, xl, "global.expand"));
   LF_TRY(lnproj_run(ctx, pp, a.act_dtype, "global.project"));
@@ -237,10 +239,12 @@ int global_attention(lf_context* ctx, const lf_global_attention_args& a) {
   rp.K = Hd;
   rp.N = C;
   rp.w = wo;
+  rp.wv = views[4];
+  rp.wview = wo_inkernel ? 1 : 0;
   rp.bias = w.o_bias;
   rp.op = OP_STORE;
   rp.resid = a.accumulate ? a.act : nullptr;
-  rp.dst = dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
+  rp.dst = out_dst;
   return launch_rowgemm(ctx, rp, "global.output");
 }
 

@@ -70,7 +70,9 @@ struct LnProjParams {
 struct RowGemmParams {
   const _Float16* A;  // [rows][K] f16 (logical rows)
   int rows, K, N;
-  WExp w;             // [N][kp]
+  WExp w;             // [N][kp]; or, with wview set, the stored weights
+  WView wv;           // decoded inside the kernel (weight-resident form only: rowgemm_resident)
+  int wview;
   const float* bias;  // [N] nullable
   int op;             // OP_STORE or OP_RELU
   const float* rowden;  // divide row r by rowden[r] (nullable; OPM's norm_eps + sum_s m_si m_sj)
@@ -82,6 +84,10 @@ struct RowGemmParams {
 // workspace of lnproj_packed_bytes(p) bytes for the decoded weights; repeated launches with
 // the same weights (row chunks) pass decode = false after the first.
 size_t lnproj_packed_bytes(const LnProjParams& p);
+// Whether launch_rowgemm takes the weight-resident form for this shape: then the caller may
+// pass the stored weights (RowGemmParams::wv, wview = 1) instead of an f16 expansion, and each
+// block decodes them into LDS once.
+bool rowgemm_resident(const lf_context* ctx, int rows, int K, int N, const Dst& dst);
 int launch_lnproj(lf_context* ctx, LnProjParams p, int act, void* packed, const char* label, bool decode = true);
 // launch_lnproj in two steps, so that an op decodes all its weights in one launch: prepare
 // validates p, fills its chunk tables and queues the decode of its weights into `packed` on

@@ -625,7 +625,9 @@ __global__ __launch_bounds__(512) void rowgemm_kernel(RowGemmParams p) {
 }
 
 // Weight-resident form for K = 32 KS <= 256 and N = 64 NP <= 256 (the attention output
-// projections): a block stages the whole expanded W (N x K f16, up to 132 KB) in LDS once, and
+// projections): a block stages the whole W (N x K f16, up to 132 KB) in LDS once -- copied from
+// the f16 expansion, or decoded from the stored codes (int8 / int5 / f16 runs, the codec
+// arithmetic of lf_gemm.h) -- and
 // each of its 8 waves then walks 16-row tiles w, w + nw, ... with no block barrier.  A tile's
 // A fragments come straight from memory into registers (the next tile's are loaded during
 // this one's MFMAs), its residual and row denominator are loaded at the top of the tile, and
@@ -649,11 +651,16 @@ __global__ __launch_bounds__(64 * NWV) void rowgemm_res_kernel(RowGemmParams p) 
   int tile = (int)blockIdx.x * NWV + wave;
   h8 a[KS];
   aload(tile < ntiles ? tile : 0, a);
-  // the whole W, 16-byte pieces of E[n][k] (row pitch p.w.kp >= K)
-  for (int i = tid; i < N * K / 8; i += NT) {
-    const int n = i / (K / 8), k = (i - n * (K / 8)) * 8;
-    const uint4 v = n < p.w.N ? *reinterpret_cast<const uint4*>(p.w.p + (size_t)n * p.w.kp + k) : make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(Ws + n * LDW + k) = v;
+  if (p.wview) {
+    // the whole W decoded from its stored codes (zeros past the view's columns)
+    stage_view(Ws, LDW, p.wv, N, 0, K, 1.f, tid, NT);
+  } else {
+    // the whole W, 16-byte pieces of E[n][k] (row pitch p.w.kp >= K)
+    for (int i = tid; i < N * K / 8; i += NT) {
+      const int n = i / (K / 8), k = (i - n * (K / 8)) * 8;
+      const uint4 v = n < p.w.N ? *reinterpret_cast<const uint4*>(p.w.p + (size_t)n * p.w.kp + k) : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(Ws + n * LDW + k) = v;
+    }
   }
   for (int i = tid; i < N; i += NT) Bs[i] = (p.bias && i < p.N) ? p.bias[i] : 0.f;
   __syncthreads();
@@ -733,6 +740,12 @@ static void launch_rowgemm_res(lf_context* ctx, const RowGemmParams& p) {
   hipLaunchKernelGGL((rowgemm_res_kernel<DACT, KS, NP, NWV>), g, dim3(64 * NWV), 0, ctx->stream, p);
 }
 
+bool rowgemm_resident(const lf_context* ctx, int rows, int K, int N, const Dst& dst) {
+  const int np = N / 64, ks = K / 32;
+  return N % 64 == 0 && K % 32 == 0 && (np == 2 || np == 4) && (ks == 4 || ks == 8) && dst.D >= 64 * np &&
+         (rows + 15) / 16 >= 8 * ctx->num_cus;
+}
+
 int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   if (p.rows <= 0) return LF_OK;
   const std::string l(label);
@@ -745,8 +758,9 @@ int launch_rowgemm(lf_context* ctx, const RowGemmParams& p, const char* label) {
   LaunchScope ls(ctx, label);
   // weight-resident form: the whole W in LDS, N and K whole multiples of the tiles
   const int np = p.N / 64, ks = p.K / 32;
-  if (p.N % 64 == 0 && p.K % 32 == 0 && (np == 2 || np == 4) && (ks == 4 || ks == 8) && p.w.kp >= p.K &&
-      p.dst.D >= 64 * np && (p.rows + 15) / 16 >= 8 * ctx->num_cus) {
+  const bool resident = rowgemm_resident(ctx, p.rows, p.K, p.N, p.dst);
+  if (p.wview && !resident) return set_error(LF_ERR_INVALID, l + ": stored weights need the weight-resident form");
+  if (resident && (p.wview || p.w.kp >= p.K)) {
 #define LF_RR(D, KS_, NP_) launch_rowgemm_res<D, KS_, NP_>(ctx, p)
 #define LF_RRD(D)                                      \
   if (ks == 4 && np == 2) LF_RR(D, 4, 2);               \

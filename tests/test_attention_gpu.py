@@ -112,6 +112,40 @@ def test_dtypes(ctx, blockw, act_dt, wdt):
     H.assert_close(out, ref, label=f"{act_dt}/{wdt}")
 
 
+@pytest.mark.parametrize("wdt,ending", [("int8", False), ("int5", True), ("float16", False)])
+def test_output_projection_decoded_in_kernel(ctx, blockw, wdt, ending):
+    """N = 192 gives 36,864 rows, enough 16-row tiles for the weight-resident output projection,
+    which then decodes the stored output weights itself (no expansion of them)."""
+    from localfold_amd import capi, device as D
+    n = 192
+    act = S.synthetic_activations(1, n, 256, 128, seed=13)
+    key = "triangleAttentionEnding" if ending else "triangleAttentionStarting"
+    tw = blockw[key]
+    names = ["queryWeight", "keyWeight", "valueWeight", "gatingWeight", "outputWeight"]
+    rec, dec = H.quantise_weights(tw["attention"], names, wdt, False, 1)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, rec, tw["pairBias"])
+    out, _, _ = _run(ctx, act["pair"], act["pairMask"], ws, 4, ending, capi.LF_BIAS_NORMALIZED_INPUT)
+    ref = ops.attention_af2(act["pair"], act["pairMask"], dec, 4, ending, dict(tw["pairBias"], source="normalized-input"))
+    H.assert_close(out, ref, label=f"in-kernel output decode {wdt}")
+
+
+def test_msa_row_attention_output_decoded_in_kernel(ctx, blockw):
+    """c_m = 256 (K = N = 256 output projection) over 36,864 rows, int8 weights in groups of 64."""
+    from localfold_amd import capi, device as D
+    s_, n = 192, 192
+    act = S.synthetic_activations(s_, n, 256, 128, seed=17)
+    row = blockw["msaRowAttention"]
+    names = ["queryWeight", "keyWeight", "valueWeight", "gatingWeight", "outputWeight"]
+    rec, dec = H.quantise_weights(row["attention"], names, "int8", False, 1)
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, rec, row["pairBias"])
+    out, _, _ = _run(ctx, act["msa"], act["msaMask"], ws, 8, False, capi.LF_BIAS_SEPARATE, act["pair"])
+    pb = dict(row["pairBias"], source="separate", activations=act["pair"])
+    ref = ops.attention_af2(act["msa"], act["msaMask"], dec, 8, False, pb)
+    H.assert_close(out, ref, label="row attention, in-kernel output decode")
+
+
 def test_accumulate_in_place_transposed(ctx, blockw):
     import torch
     from localfold_amd import capi, device as D
