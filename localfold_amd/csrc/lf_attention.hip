@@ -17,6 +17,7 @@
 //           the N^2 x heads logits never leave registers
 //   rowgemm o Wo + bo, + residual, stored through the row map
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <cmath>
 
@@ -30,7 +31,7 @@ constexpr int FA_QPB = 128;     // queries per block (8 / QT waves of QT 16-quer
 // config 3: 155 VGPRs, half the waves)
 constexpr int FA_QT_BIAS = 1, FA_QT_PLAIN = 1;
 constexpr int FA_KC = 64;       // keys per chunk
-constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8;
+constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8, FA_BLD = FA_KC + 8;
 
 
 struct FlashParams {
@@ -243,7 +244,8 @@ __device__ __forceinline__ float bias_add(const h4& v, int i, float c) {
   return (i & 1) ? f16_add<1>(w, c) : f16_add<0>(w, c);
 }
 
-// Pair-bias values of one lane for one key chunk: the 16 keys k0 + 16*g4 .. +15 of each of the
+// (With one query tile per wave the kernel stages the block's bias tile through LDS instead;
+// this per-lane fetch serves QT > 1.)  Pair-bias values of one lane for one key chunk: the 16 keys k0 + 16*g4 .. +15 of each of the
 // lane's queries (rows brow[qt], already offset by 16*g4), as two aligned 16-byte loads;
 // bv[qt][kt][i] is key k0 + 16*g4 + 4*kt + i.  Bias rows are padded to whole chunks; values
 // past Q are never used.
@@ -276,10 +278,15 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], in
 // Key order within a chunk: row 4*g + i of S^T tile kt is key 16*g + 4*kt + i (K rows are
 // stored to LDS in that order), so the 16 scores a lane holds per query are the contiguous
 // keys 16*(lane/16) .. +15: its bias, key bias and V^T pieces are single vector loads.
-template <bool BIAS, int QT>
+template <bool BIAS, int QT, bool BL = BIAS && QT == 1>
 __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
+  static_assert(!BL || (BIAS && QT == 1), "the LDS-staged bias is for one query tile per wave");
+  // (BL, the default with a bias: config 4's row attention 0.30 -> 0.276 ms and triangle
+  // attention 0.106 -> 0.098 ms per launch, config 3 -1%, config 5 unchanged)
   // per buffer: K rows [64][FA_KLD], then V^T rows [32][FA_VLD]
   __shared__ __attribute__((aligned(16))) _Float16 KV[2][FA_KC * FA_KLD + FA_DP * FA_VLD];
+  // BL: the block's pair-bias tile of each chunk, [128 queries][64 keys] at pitch FA_BLD
+  __shared__ __attribute__((aligned(16))) _Float16 Bl[BL ? 2 : 1][BL ? FA_QPB * FA_BLD : 8];
   __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
   __shared__ int Kmasked[2];   // chunk has a masked key or a key past Q
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -337,6 +344,29 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     const int key = t >> 2, krow = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
     loff[j] = isk ? krow * FA_KLD + (t & 3) * 8 : FA_KC * FA_KLD + (tv >> 3) * FA_VLD + (tv & 7) * 8;
   }
+  // BL: thread t stages bias rows t/8 and t/8 + 64 of the block's 128, keys 8 (t % 8) .. +8,
+  // so eight consecutive threads read one row's 128 bytes (coalesced, unlike the per-lane
+  // fetch, where one wave instruction touched 64 rows)
+  const _Float16* bsrc[2];
+  int boff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = (tid >> 3) + 64 * j, q = qb * FA_QPB + r;
+    bsrc[j] = BL ? bias + (size_t)(q < p.Q ? q : p.Q - 1) * Qp + (tid & 7) * 8 : nullptr;
+    boff[j] = r * FA_BLD + (tid & 7) * 8;
+  }
+  // (the bias tile of chunk c + 1 is loaded at the top of chunk c, before chunk c + 2's K/V, and
+  // stored with chunk c + 1's K/V at its end: one chunk of latency, L2 hits)
+  // (two named registers, not an array: an array passed by reference here was promoted to LDS)
+  uint4 bsn0, bsn1;
+  auto bias_load = [&](int c) __attribute__((always_inline)) {
+    bsn0 = *reinterpret_cast<const uint4*>(bsrc[0] + c * FA_KC);
+    bsn1 = *reinterpret_cast<const uint4*>(bsrc[1] + c * FA_KC);
+  };
+  auto bias_store = [&](int buf) __attribute__((always_inline)) {
+    *reinterpret_cast<uint4*>(&Bl[buf][boff[0]]) = bsn0;
+    *reinterpret_cast<uint4*>(&Bl[buf][boff[1]]) = bsn1;
+  };
   auto kv_load = [&](int c, uint4 (&r)[NP], float& kbr) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NP; ++j) r[j] = *reinterpret_cast<const uint4*>(gsrc[j] + (size_t)c * gstep[j]);
@@ -359,13 +389,15 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   float kb0, kb1;
   h4 bq0[QT][4], bq1[QT][4];   // bias of chunk c in set c % 2; chunk c + 2's is fetched once c's is used
   const int c1 = nkc > 1 ? 1 : 0;
+  if (BL) bias_load(0);
   kv_load(0, st0, kb0);
   kv_load(c1, st1, kb1);
-  if (BIAS) {
+  if (BIAS && !BL) {
     bias_fetch<QT>(brow, 0, bq0);
     bias_fetch<QT>(brow, c1 * FA_KC, bq1);
   }
   kv_store(0, st0, kb0);
+  if (BL) bias_store(0);
   __syncthreads();
 
   float m_run[QT];
@@ -382,7 +414,20 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       constexpr int rs = decltype(rs_tag)::value;
       const int buf = rs;
       h4 (&bq)[QT][4] = rs == 0 ? bq0 : bq1;
+      if (BL) {   // this chunk's bias from the block's LDS tile: the lane's query, keys 16 g4 .. +15
+        const _Float16* br = &Bl[buf][(wave * 16 + r16) * FA_BLD + 16 * g4];
+        const h8 lo = *reinterpret_cast<const h8*>(br);
+        const h8 hi = *reinterpret_cast<const h8*>(br + 8);
+        bq[0][0] = h4{lo[0], lo[1], lo[2], lo[3]};
+        bq[0][1] = h4{lo[4], lo[5], lo[6], lo[7]};
+        bq[0][2] = h4{hi[0], hi[1], hi[2], hi[3]};
+        bq[0][3] = h4{hi[4], hi[5], hi[6], hi[7]};
+      }
       const int cn = c + 2 < nkc ? c + 2 : nkc - 1;
+      if (BL) {
+        bias_load(c + 1 < nkc ? c + 1 : nkc - 1);
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads here, a chunk ahead of their store
+      }
       if constexpr (rs == 0) kv_load(cn, st0, kb0);
       else kv_load(cn, st1, kb1);
       const bool general = Kmasked[buf] != 0;   // wave-uniform
@@ -479,7 +524,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         }
       }
       // this chunk's bias values are consumed: fetch chunk c + 2's into the slot
-      if (BIAS) bias_fetch<QT>(brow, cn * FA_KC, bq);
+      if (BIAS && !BL) bias_fetch<QT>(brow, cn * FA_KC, bq);
       // O^T += V^T P^T over two 32-key halves; the ones operand accumulates the row sums
 #pragma unroll
       for (int kh2 = 0; kh2 < 2; ++kh2) {
@@ -502,6 +547,10 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       // branch around the store the compiler's waits on the loads stay exact
       if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1);
       else kv_store(buf ^ 1, st0, kb0);
+      if (BL) {
+        __builtin_amdgcn_sched_barrier(0);
+        bias_store(buf ^ 1);
+      }
       __syncthreads();
   };
   int c0 = 0;
