@@ -322,6 +322,15 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc[qt] * FA_DP + kq);
     brow[qt] = BIAS ? bias + (size_t)qc[qt] * Qp + 16 * g4 : nullptr;
   }
+  // the epilogue's gate (head-major [h][row][d]) is read now, so the block's last step does
+  // not wait a memory round trip for it (QT == 1, d a multiple of 4)
+  const bool gpre = QT == 1 && (p.d & 3) == 0;
+  h4 gp0 = h4{0, 0, 0, 0}, gp1 = h4{0, 0, 0, 0};
+  if (gpre) {
+    const size_t grow = ((size_t)h * p.B * p.Q + (size_t)b * p.Q + qc[0]) * p.d;
+    if (4 * g4 < p.d) gp0 = *reinterpret_cast<const h4*>(p.g + grow + 4 * g4);
+    if (16 + 4 * g4 < p.d) gp1 = *reinterpret_cast<const h4*>(p.g + grow + 16 + 4 * g4);
+  }
   const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
   // identity A operand of a 16x16x16 MFMA: lane supplies I[r16][4*g4 + j]
   const h4 ident = h4{(_Float16)(r16 == 4 * g4), (_Float16)(r16 == 4 * g4 + 1), (_Float16)(r16 == 4 * g4 + 2),
@@ -572,7 +581,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
       const size_t base = row * p.HD + (size_t)h * p.d + d0;
       const size_t gbase = ((size_t)h * p.B * p.Q + row) * p.d + d0;   // gate head-major [h][row][d]
       if (d0 + 4 <= p.d && (p.d & 3) == 0) {
-        const h4 gv = *reinterpret_cast<const h4*>(p.g + gbase);
+        const h4 gv = gpre ? (dt == 0 ? gp0 : gp1) : *reinterpret_cast<const h4*>(p.g + gbase);
         h4 ov;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov[i] = (_Float16)(o[dt][qt][i] * inv * (float)gv[i]);
