@@ -67,6 +67,31 @@ def cpu_info():
     return {"cpu_model": model, "logical_cpus": os.cpu_count(), "physical_cores": physical, "blas_threads": blas}
 
 
+def js_cpu_baseline(n=192):
+    """The library's single-threaded JS restatement of the reference's CPU path
+    (`triangleMultiplicationOutgoingReference`, webgpu/kernels/triangle/cpu-reference.js:55-99)
+    timed under Node on this box's host: one outgoing triangle multiplication at N = n with
+    config 2's channels (c_z = c_hidden = 128), f32 storage and f64 sums as the reference.
+    None when node is not installed."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        return None
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "localfold_amd", "js", "bench_cpu.js")
+    r = subprocess.run([node, script, str(n)], capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"error": r.stderr[-500:]}
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    p_, c = n * n, 128
+    flops = p_ * (8 * c * c + 2 * c * c + 2 * c * c) + 2 * n * c * p_
+    return {"value": round(flops / d["seconds"] / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"outgoing triangle multiplication at N={n} (c_z = c_hidden = 128, deterministic input), "
+                      f"the JS restatement of the reference's CPU path under node {subprocess.run([node, '--version'], capture_output=True, text=True).stdout.strip()}, "
+                      f"single-threaded: {d['seconds']:.2f} s for {flops / 1e9:.2f} GFLOP",
+            "seconds": round(d["seconds"], 3), "finite": d["finite"]}
+
+
 def cpu_baseline(c2, budget_s=30.0):
     """The oracle (numpy: float64 compute, float32 storage, BLAS and host threads) timed on
     this box's host cores: config 2's step (the headline's workload) and config 1 (one AF2
@@ -601,7 +626,12 @@ def main():
     cpu = None
     if not args.no_cpu_baseline and not args.only:
         log("timing the CPU oracle ...")
-        cpu = cpu_baseline(c2)
+        numpy_port = cpu_baseline(c2)
+        log("timing the JS CPU reference (single thread) ...")
+        js = js_cpu_baseline()
+        # the reference's CPU path is single-threaded JS: its restatement is the baseline when
+        # node is present; the multithreaded numpy oracle is reported beside it
+        cpu = dict(js, numpy_port=numpy_port) if js and "value" in js else dict(numpy_port, js_reference=js)
 
     out = {
         "metric": "Evoformer block ms at N_res=384/512 + triangle-op TFLOP/s as % of MFMA peak",
