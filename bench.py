@@ -67,7 +67,7 @@ def cpu_info():
     return {"cpu_model": model, "logical_cpus": os.cpu_count(), "physical_cores": physical, "blas_threads": blas}
 
 
-def js_cpu_baseline(n=192):
+def js_cpu_baseline(n=256):
     """The library's single-threaded JS restatement of the reference's CPU path
     (`triangleMultiplicationOutgoingReference`, webgpu/kernels/triangle/cpu-reference.js:55-99)
     timed under Node on this box's host: one outgoing triangle multiplication at N = n with
