@@ -615,11 +615,21 @@ __device__ __forceinline__ void frag_ln_raw2(FragTile<ACT, KS>& t0, FragTile<ACT
 
 // LayerNorm of one raw tile into MFMA fragments (frag_ln_raw2 for a single tile).
 template <int ACT, int KS>
+__device__ __forceinline__ void frag_ln_given(FragTile<ACT, KS>& t0, h8 (&a0)[KS], const float* gamma,
+                                              const float* beta, float m0, float i0, int lane);
+
+template <int ACT, int KS>
 __device__ __forceinline__ void frag_ln_raw1(FragTile<ACT, KS>& t0, h8 (&a0)[KS], int C, const float* gamma,
                                              const float* beta, float eps, bool fast_var, int lane) {
-  const int g = lane >> 4;
   float m0, i0;
   frag_stats_raw(t0, C, eps, fast_var, m0, i0);
+  frag_ln_given(t0, a0, gamma, beta, m0, i0, lane);
+}
+
+template <int ACT, int KS>
+__device__ __forceinline__ void frag_ln_given(FragTile<ACT, KS>& t0, h8 (&a0)[KS], const float* gamma,
+                                              const float* beta, float m0, float i0, int lane) {
+  const int g = lane >> 4;
 #pragma unroll
   for (int j = 0; j < KS; ++j) {
     const float4 g0 = *reinterpret_cast<const float4*>(gamma + 32 * j + 8 * g);

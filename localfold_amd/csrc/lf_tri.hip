@@ -61,6 +61,7 @@ struct TriProjectParams {
   int kmajor_out;      // store each channel plane transposed: a[h][j][k] for pair (k, j)
   int split;           // AF3 in the resident kernels: wp[0] / wg[0] are the whole interleaved
                        // tensors (even stored columns -> a, odd -> b); wp[1] / wg[1] unused
+  float2* stats;       // when not NULL (128-wide kernel only): LN_in (mean, 1/std) per pair, by z row
 };
 
 struct TriOutputParams {
@@ -74,6 +75,7 @@ struct TriOutputParams {
   int P, C, H;
   WSrc wz, wg;
   const float *bz, *bg;
+  const float2* stats;  // when not NULL: LN_in (mean, 1/std) per pair, written by the project kernel
 };
 
 // ---------------------------------------------------------------------------------------
@@ -1006,7 +1008,7 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v2_kernel(TriProjectPara
 // unrolled, and the next rows are taken into registers (an asm use forces the wait) after the
 // last pass's MFMAs and before its stores: every wait on the in-order vector-memory counter
 // then covers loads issued earlier in the same step, never the stores that follow them.
-template <int ACT, int NWV>
+template <int ACT, int NWV, bool ST>
 __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectParams p) {
   constexpr int NT = 64 * NWV;
   __shared__ __attribute__((aligned(16))) _Float16 Ws[4 * 128 * RS_LD];  // a-proj, a-gate', b-proj, b-gate' [h][k]
@@ -1047,10 +1049,19 @@ __global__ __launch_bounds__(64 * NWV) void tri_project_v3_kernel(TriProjectPara
   __syncthreads();
   if (tile >= ntiles) return;
   for (; tile < ntiles; tile += nw) {
-    const int out0 = tile_geom(p, tile).out0;
+    const TileGeom tg = tile_geom(p, tile);
+    const int out0 = tg.out0;
     const uint32_t lofs = ((uint32_t)r16 * (uint32_t)p.P + (uint32_t)(out0 + q4)) * (uint32_t)sizeof(_Float16);
     h8 xa[4];
-    frag_ln_raw1(tc, xa, 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    if constexpr (ST) {
+      float m0, i0;
+      frag_stats_raw(tc, 128, p.eps, p.fast_var, m0, i0);
+      // the output kernel normalises the same z rows again for its gate: it reads these
+      if (lane < 16) p.stats[tg.src0 + r16 * tg.sstride] = make_float2(m0, i0);
+      frag_ln_given(tc, xa, Gs, Gs + 128, m0, i0, lane);
+    } else {
+      frag_ln_raw1(tc, xa, 128, Gs, Gs + 128, p.eps, p.fast_var, lane);
+    }
     const int nt = tile + nw < ntiles ? tile + nw : tile;   // the last step reloads its own tile
     FragTile<ACT, 4> tn;
     float mn[4];
@@ -1152,7 +1163,7 @@ __device__ __forceinline__ void x_put(_Float16* Xw, const h8 (&xv)[4], int lane)
 // The weights are the MFMA A operand (resident in LDS), so a lane's accumulators hold four
 // consecutive channels of one pair; the gate weights and bias arrive pre-multiplied by
 // -log2(e): sigmoid = rcp(1 + exp2(acc)).
-template <int ACT, int NWV, bool VECX>
+template <int ACT, int NWV, bool VECX, bool ZS>
 __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams p) {
   constexpr int NT = 64 * NWV;
   // X patch buffers per wave: two (the next tile's X is transposed during the current tile's
@@ -1168,11 +1179,14 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   // the first tile's z rows and X columns load while the weights are decoded into LDS
   // (clamped, never skipped)
   int tile = blockIdx.x * NWV + wave;
+  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
   FragTile<ACT, 4> zc;
+  float2 zs = make_float2(0.f, 1.f);
   h8 xv[4];
   {
     const int t0 = tile < nfull ? tile : 0;
     frag_load(zc, p.z, (size_t)t0 * 16, 16, 128, lane);
+    if constexpr (ZS) zs = p.stats[t0 * 16 + r16];
     if constexpr (VECX) x_fetch(xv, p.X, p.P, t0 * 16, lane);
   }
   {
@@ -1190,14 +1204,12 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
   stage_vec(Vs + 640, p.ln_in_o, 128, 0.f, 128, tid, NT);
   __syncthreads();
 
-  const int r16 = lane & 15, g4 = lane >> 4, kq = g4 * 8;
-
   // One tile: LN_out of X (LDS buffer Xc) and LN_in of z (zc), then two passes of 64 output
   // channels.  A pass stages its f32 update in Xc (the X fragments are in registers by then)
   // and each lane writes its own pair r16, channels c0 + 32jj + 8*g4 .. +7: the layout of its
   // z fragment, which holds the residual.  `between` runs after the second pass's MFMAs.
-  auto run_tile = [&](auto full_tag, const FragTile<ACT, 4>& zc, _Float16* Xc, int row0, int nval, auto&& mid,
-                      auto&& between) __attribute__((always_inline)) {
+  auto run_tile = [&](auto full_tag, const FragTile<ACT, 4>& zc, float2 zs, _Float16* Xc, int row0, int nval,
+                      auto&& mid, auto&& between) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full_tag)::value;
     h8 ax[4], az[4];
     {
@@ -1208,7 +1220,8 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     }
     {
       FragTile<ACT, 4> zl = zc;
-      frag_ln_raw1(zl, az, 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
+      if constexpr (ZS) frag_ln_given(zl, az, Vs + 512, Vs + 640, zs.x, zs.y, lane);
+      else frag_ln_raw1(zl, az, 128, Vs + 512, Vs + 640, p.eps, p.fast_var, lane);
     }
     float* Us = reinterpret_cast<float*>(Xc);   // [16 pairs][68] f32 (pitch 68: no bank conflicts)
     auto pass = [&](auto pass_tag) __attribute__((always_inline)) {
@@ -1286,16 +1299,18 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     for (; tile < nfull; tile += nw) {
       const int nt = tile + nw < nfull ? tile + nw : tile;   // the last step reloads its own tile
       FragTile<ACT, 4> zn;
+      float2 zsn = zs;
       h8 xn[4];
       // the next tile's rows load at the top of the step (two X buffers), or between the two
       // passes (one buffer: fewer registers live through the first pass)
       auto fetch_next = [&]() __attribute__((always_inline)) {
         frag_load(zn, p.z, (size_t)nt * 16, 16, 128, lane);
+        if constexpr (ZS) zsn = p.stats[nt * 16 + r16];
         if constexpr (VECX) x_fetch(xn, p.X, p.P, nt * 16, lane);
       };
       if constexpr (XB == 2) fetch_next();
       _Float16* Xn = Xs[wave][XB == 2 ? cur ^ 1 : 0];
-      run_tile(std::true_type{}, zc, Xs[wave][XB == 2 ? cur : 0], tile * 16, 16, [&]() __attribute__((always_inline)) {
+      run_tile(std::true_type{}, zc, zs, Xs[wave][XB == 2 ? cur : 0], tile * 16, 16, [&]() __attribute__((always_inline)) {
         if constexpr (XB == 1) fetch_next();
       }, [&]() __attribute__((always_inline)) {
         if constexpr (VECX) x_put(Xn, xn, lane);
@@ -1304,7 +1319,9 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
       // take the next rows now (an asm use forces the wait here, within this step, where the
       // counter wait cannot cover this step's stores), not at their first use next step
       launder(zn);
+      if constexpr (ZS) asm volatile("" : "+v"(zsn.x), "+v"(zsn.y));
       zc = zn;
+      zs = zsn;
       if constexpr (XB == 2) cur ^= 1;
     }
   }
@@ -1312,8 +1329,9 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     const int row0 = nfull * 16, nval = p.P - row0;
     FragTile<ACT, 4> zc;
     frag_load(zc, p.z, (size_t)row0, nval, 128, lane);
+    const float2 zt = ZS ? p.stats[row0 + (r16 < nval ? r16 : 0)] : make_float2(0.f, 1.f);
     x_transpose<ACT>(Xs[wave][0], p.X, p.P, row0, nval, lane);
-    run_tile(std::false_type{}, zc, Xs[wave][0], row0, nval, []() {}, []() {});
+    run_tile(std::false_type{}, zc, zt, Xs[wave][0], row0, nval, []() {}, []() {});
   }
 }
 
@@ -1324,8 +1342,10 @@ static void launch_project(lf_context* ctx, const TriProjectParams& pp, bool res
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + TRI_P_NWV - 1) / TRI_P_NWV)));
     const bool whole = pp.kmajor_out ? pp.N % 16 == 0 : P % 16 == 0;
-    if (whole && P < (1 << 27))   // 32-bit per-lane store offsets
-      hipLaunchKernelGGL((tri_project_v3_kernel<ACT, TRI_P_NWV>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
+    if (whole && P < (1 << 27) && pp.stats)   // 32-bit per-lane store offsets
+      hipLaunchKernelGGL((tri_project_v3_kernel<ACT, TRI_P_NWV, true>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
+    else if (whole && P < (1 << 27))
+      hipLaunchKernelGGL((tri_project_v3_kernel<ACT, TRI_P_NWV, false>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
     else
       hipLaunchKernelGGL((tri_project_v2_kernel<ACT, TRI_P_NWV, TRI_P_TPW>), g, dim3(64 * TRI_P_NWV), 0, ctx->stream, pp);
     return;
@@ -1349,10 +1369,15 @@ static void launch_output(lf_context* ctx, const TriOutputParams& op, bool resid
     constexpr int NWV = tri_o_nwv<ACT>();
     const int tiles = (P + 15) / 16;
     dim3 g(std::max(1, std::min(ctx->num_cus, (tiles + NWV - 1) / NWV)));
-    if ((P & 7) == 0)
-      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, true>), g, dim3(64 * NWV), 0, ctx->stream, op);
+    // the z statistics come from the project kernel when it stored them (op.stats)
+    if ((P & 7) == 0 && op.stats)
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, true, true>), g, dim3(64 * NWV), 0, ctx->stream, op);
+    else if ((P & 7) == 0)
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, true, false>), g, dim3(64 * NWV), 0, ctx->stream, op);
+    else if (op.stats)
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, false, true>), g, dim3(64 * NWV), 0, ctx->stream, op);
     else
-      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, false>), g, dim3(64 * NWV), 0, ctx->stream, op);
+      hipLaunchKernelGGL((tri_output_v3_kernel<ACT, NWV, false, false>), g, dim3(64 * NWV), 0, ctx->stream, op);
     return;
   }
   if (resident) {
@@ -1430,12 +1455,20 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
   LF_TRY(make_view(w.wz, H, C, "linearZWeight", &views[4]));
   LF_TRY(make_view(w.wg, C, C, "linearGWeight", &views[5]));
 
+  // the 128-wide project kernel for whole 16-pair tiles (32-bit per-lane store offsets) also
+  // stores each pair's LN_in statistics for the output kernel, for 16-bit activations: with
+  // f32 activations that variant computed wrong projections on the GPU (found by the f32
+  // parity tests; cause not identified), so f32 keeps the kernel that recomputes them
+  const bool wide = C == 128 && H == 128 && N >= 16;
+  const bool v3 = wide && a.act_dtype != LF_F32 && (a.direction != LF_OUTGOING ? N % 16 == 0 : P % 16 == 0) &&
+                  P < (1 << 27);
   const size_t plane = (size_t)H * P * sizeof(_Float16);
-  size_t sizes[3] = {plane, plane, plane};
-  void* bufs[3];
+  size_t sizes[4] = {plane, plane, plane, v3 ? (size_t)P * sizeof(float2) : 0};
+  void* bufs[4] = {};
+  const int nbufs = v3 ? 4 : 3;
   if (scratch) {
     size_t total = 0;
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < nbufs; ++i) {
       bufs[i] = static_cast<char*>(scratch) + total;
       total += (sizes[i] + 255) & ~size_t(255);
     }
@@ -1445,8 +1478,9 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
                                            " bytes of scratch; the static scratch holds " +
                                            std::to_string(scratch_cap));
   } else {
-    LF_TRY(workspace(ctx, sizes, bufs, 3));
+    LF_TRY(workspace(ctx, sizes, bufs, nbufs));
   }
+  pp.stats = static_cast<float2*>(bufs[3]);
   pp.out[0] = static_cast<_Float16*>(bufs[0]);
   pp.out[1] = static_cast<_Float16*>(bufs[1]);
   _Float16* X = static_cast<_Float16*>(bufs[2]);
@@ -1517,6 +1551,7 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
   op.H = H;
   op.bz = a.dialect == LF_AF2 ? w.wz_bias : nullptr;
   op.bg = a.dialect == LF_AF2 ? w.wg_bias : nullptr;
+  op.stats = pp.stats;
   {
     LaunchScope ls(ctx, outgoing ? "tri_out.output" : "tri_in.output");
     if (a.act_dtype == LF_F32) launch_output<DT_F32>(ctx, op, resident, kz, kh);
