@@ -134,13 +134,15 @@ int lf_tri_mult(lf_context* ctx, const lf_tri_mult_args* args);
 /* No counterpart in the reference: lf_tri_mult for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as lf_tri_mult, but its scratch (the a, b and X planes,
- * 3 * c_hidden * N^2 f16; weights are decoded while being staged into LDS, so they take no
+ * 3 * c_hidden * N^2 f16, plus 8 * N^2 bytes of LayerNorm statistics with 2-byte activations
+ * at c_z = c_hidden = 128; weights are decoded while being staged into LDS, so they take no
  * scratch) lives in a static per-device array of LF_TRI_NOALLOC_SCRATCH_BYTES (reserved on
  * every device the library loads on, used or not), looked up once per device by
  * lf_context_create; nothing is
  * allocated or freed.  Shapes needing more scratch are rejected with LF_ERR_INVALID (c_hidden
- * 128 fits N <= 417).  Every call on one GPU shares that GPU's array: calls that overlap on one
- * GPU (two streams, two threads, two contexts) race, so serialise them. */
+ * 128 fits N <= 415, or 417 with f32 activations).  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, two threads, two contexts) race, so
+ * serialise them. */
 #define LF_TRI_NOALLOC_SCRATCH_BYTES (128u << 20)
 int lf_tri_mult_noalloc(lf_context* ctx, const lf_tri_mult_args* args);
 
