@@ -8,6 +8,8 @@
 // RangeErrors, webgpu/kernels/triangle/types.js:13-48) and again in the library.
 #include <node_api.h>
 
+#include <dlfcn.h>
+
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -550,6 +552,19 @@ napi_value Version(napi_env env, napi_callback_info) {
   return v;
 }
 
+// The file the dynamic loader resolved liblocalfold.so to for this process (the library whose
+// lf_context_create this addon calls), so a test can check which build ran.
+napi_value NativeLibraryPath(napi_env env, napi_callback_info) {
+  Dl_info info{};
+  napi_value v;
+  if (!dladdr(reinterpret_cast<void*>(&lf_context_create), &info) || !info.dli_fname) {
+    napi_throw_error(env, nullptr, "dladdr(lf_context_create) failed");
+    return nullptr;
+  }
+  napi_create_string_utf8(env, info.dli_fname, NAPI_AUTO_LENGTH, &v);
+  return v;
+}
+
 // ---- ops: op(ctx, args) with args mirroring the C structs (camelCase) -------------------
 
 napi_value TriMult(napi_env env, napi_callback_info info) {
@@ -953,7 +968,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"contextCreate", ContextCreate}, {"contextDestroy", ContextDestroy}, {"upload", Upload},
       {"alloc", Alloc}, {"download", Download}, {"free", Free}, {"synchronize", Synchronize},
       {"memoryStats", MemoryStats}, {"profileEnable", ProfileEnable}, {"profileRead", ProfileRead},
-      {"version", Version}, {"triMult", TriMult}, {"attention", Attention}, {"transition", Transition},
+      {"version", Version}, {"nativeLibraryPath", NativeLibraryPath}, {"triMult", TriMult}, {"attention", Attention}, {"transition", Transition},
       {"outerProductMean", OuterProductMean}, {"evoformerStack", EvoformerStack}, {"evoformerPairStack", EvoformerPairStack},
       {"pairformerBlock", PairformerBlock}, {"globalColumnAttention", GlobalColumnAttention},
       {"extraMsaStack", ExtraMsaStack}, {"msaModuleBlock", MsaModuleBlock}, {"inputEmbedder", InputEmbedder},

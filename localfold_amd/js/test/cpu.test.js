@@ -101,7 +101,8 @@ check('library exports the reference surface', function t() {
 check('addon exports every entry point', function t() {
   const names = ['contextCreate', 'contextDestroy', 'upload', 'alloc', 'download', 'free', 'synchronize', 'memoryStats',
     'profileEnable', 'profileRead', 'triMult', 'attention', 'transition', 'outerProductMean', 'evoformerStack',
-    'evoformerPairStack', 'extraMsaStack', 'pairformerBlock', 'version'];
+    'evoformerPairStack', 'extraMsaStack', 'pairformerBlock', 'globalColumnAttention', 'msaModuleBlock',
+    'inputEmbedder', 'version', 'nativeLibraryPath'];
   const a = lf.addon();
   names.forEach(function each(n) { assert.strictEqual(typeof a[n], 'function', n); });
 });

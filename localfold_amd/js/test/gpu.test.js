@@ -10,6 +10,8 @@ const lf = require('../index.js');
 
 const dir = process.argv[2];
 const device = lf.createDevice(0);
+// the shared library the addon's calls went to (checked by the pytest side)
+console.log('native-library ' + fs.realpathSync(lf.addon().nativeLibraryPath()));
 let failures = 0;
 
 function f32(name) {

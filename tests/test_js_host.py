@@ -1,6 +1,7 @@
 """The Node host (localfold_amd/js): CPU checks here, GPU parity through the JS classes on the
 reference's fixture format and oracle cases (written to a temp directory by this test)."""
 import json
+import os
 import shutil
 import subprocess
 from pathlib import Path
@@ -186,3 +187,7 @@ def test_js_gpu_suite(tmp_path):
     (tmp_path / "cases.json").write_text(json.dumps(cases))
     r = _run_node("gpu.test.js", tmp_path)
     assert r.returncode == 0 and "FAIL" not in r.stdout
+    # the addon's calls went to the in-tree HIP library, not another copy
+    loaded = [l.split(" ", 1)[1] for l in r.stdout.splitlines() if l.startswith("native-library ")]
+    lib = os.path.realpath(os.path.join(os.path.dirname(__file__), "..", "localfold_amd", "lib", "liblocalfold.so"))
+    assert loaded == [lib], (loaded, lib)
