@@ -25,13 +25,13 @@
 
 namespace lf {
 
-constexpr int FA_DP = 32;       // padded head dim (d <= 32)
+constexpr int FA_DP = 32;       // padded head dim (d <= 32); 16 for d <= 16 (the kernel's DP)
 constexpr int FA_QPB = 128;     // queries per block (8 / QT waves of QT 16-query tiles)
 // 16-query tiles per wave, with and without a pair bias: one (two measured 60% slower at
 // config 3: 155 VGPRs, half the waves)
 constexpr int FA_QT_BIAS = 1, FA_QT_PLAIN = 1;
 constexpr int FA_KC = 64;       // keys per chunk
-constexpr int FA_KLD = FA_DP + 8, FA_VLD = FA_KC + 8, FA_BLD = FA_KC + 8;
+constexpr int FA_VLD = FA_KC + 8, FA_BLD = FA_KC + 8;
 
 
 struct FlashParams {
@@ -41,6 +41,10 @@ struct FlashParams {
   long long kb_stride;
   const _Float16* bias;   // [H][Q][Q] or null
   int B, H, Q, d, HD;
+  int dq;                 // head dims q and k hold (d; 0 when every logit is the bias alone)
+  int fix;                // dq < DP or Q not a whole number of chunks: the kernel (the FIX
+                          // instantiation) zeroes the unwritten parts of q, k and v^T as it
+                          // reads them
   int nqb;                // query blocks per (b, h)
   long long nblocks;
 };
@@ -237,6 +241,10 @@ __global__ __launch_bounds__(256) void pwa_average_kernel(PwaParams p) {
   }
 }
 
+// S^T tile += K Q^T over the padded head dims: 16x16x32 for 8 dims a lane, 16x16x16 for 4
+__device__ __forceinline__ f4 qk_mfma(h8 k, h8 q, f4 c) { return mfma16(k, q, c); }
+__device__ __forceinline__ f4 qk_mfma(h4 k, h4 q, f4 c) { return mfma16k16(k, q, c); }
+
 // (float)v[i] + c in one instruction (i is a constant once the caller's loop is unrolled)
 __device__ __forceinline__ float bias_add(const h4& v, int i, float c) {
   const uint2 u = __builtin_bit_cast(uint2, v);
@@ -278,13 +286,18 @@ __device__ __forceinline__ void bias_fetch(const _Float16* const (&brow)[QT], in
 // Key order within a chunk: row 4*g + i of S^T tile kt is key 16*g + 4*kt + i (K rows are
 // stored to LDS in that order), so the 16 scores a lane holds per query are the contiguous
 // keys 16*(lane/16) .. +15: its bias, key bias and V^T pieces are single vector loads.
-template <bool BIAS, int QT, bool BL = BIAS && QT == 1>
+template <bool BIAS, int QT, bool BL = BIAS && QT == 1, int DP = FA_DP, bool FIX = false>
 __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   static_assert(!BL || (BIAS && QT == 1), "the LDS-staged bias is for one query tile per wave");
+  static_assert(DP == 16 || DP == 32, "padded head dim 16 or 32");
+  // DP = 16 (d <= 16): QK^T on 16x16x16 MFMAs (4 head dims a lane), one O tile; DP = 32: QK^T
+  // on 16x16x32 MFMAs (8 a lane), two O tiles.  o[NDT] holds the row sums.
+  constexpr int KLD = DP + 8, NDT = DP / 16, SEGS = DP / 8;
+  using QF = typename std::conditional<DP == 32, h8, h4>::type;
   // (BL, the default with a bias: config 4's row attention 0.30 -> 0.276 ms and triangle
   // attention 0.106 -> 0.098 ms per launch, config 3 -1%, config 5 unchanged)
-  // per buffer: K rows [64][FA_KLD], then V^T rows [32][FA_VLD]
-  __shared__ __attribute__((aligned(16))) _Float16 KV[2][FA_KC * FA_KLD + FA_DP * FA_VLD];
+  // per buffer: K rows [64][KLD], then V^T rows [DP][FA_VLD]
+  __shared__ __attribute__((aligned(16))) _Float16 KV[2][FA_KC * KLD + DP * FA_VLD];
   // BL: the block's pair-bias tile of each chunk, [128 queries][64 keys] at pitch FA_BLD
   __shared__ __attribute__((aligned(16))) _Float16 Bl[BL ? 2 : 1][BL ? FA_QPB * FA_BLD : 8];
   __shared__ __attribute__((aligned(16))) float Kb[2][FA_KC];
@@ -305,21 +318,28 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   const int nkc = (p.Q + FA_KC - 1) / FA_KC;
   const int Qp = nkc * FA_KC;   // keys padded to whole chunks in q, k, v^T, the key bias and bias rows
   const size_t bh = (size_t)b * p.H + h;
-  const _Float16* qh = p.q + bh * Qp * FA_DP;
-  const _Float16* kh = p.k + bh * Qp * FA_DP;
-  const _Float16* vh = p.vt + bh * FA_DP * Qp;
+  const _Float16* qh = p.q + bh * Qp * DP;
+  const _Float16* kh = p.k + bh * Qp * DP;
+  const _Float16* vh = p.vt + bh * DP * Qp;
   const float* kbb = p.kb + b * p.kb_stride;
   const _Float16* bias = BIAS ? p.bias + (size_t)h * p.Q * Qp : nullptr;
 
-  // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims 8*g4 .. +8
+  // Q fragments (B operand of S^T = K Q^T): query r16 of tile qt, dims qd .. +8 (DP 32) or
+  // +4 (DP 16); dims past dq are zeroed here (the buffer's padding is never written)
+  const int qd = DP == 32 ? kq : 4 * g4;
   int qidx[QT], qc[QT];
-  h8 qf[QT];
+  QF qf[QT];
   const _Float16* brow[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     qidx[qt] = qb * FA_QPB + (wave * QT + qt) * 16 + r16;
     qc[qt] = qidx[qt] < p.Q ? qidx[qt] : p.Q - 1;
-    qf[qt] = *reinterpret_cast<const h8*>(qh + (size_t)qc[qt] * FA_DP + kq);
+    qf[qt] = *reinterpret_cast<const QF*>(qh + (size_t)qc[qt] * DP + qd);
+    if (FIX) {
+#pragma unroll
+      for (int e = 0; e < (int)(sizeof(QF) / 2); ++e)
+        if (qd + e >= p.dq) qf[qt][e] = (_Float16)0.f;
+    }
     brow[qt] = BIAS ? bias + (size_t)qc[qt] * Qp + 16 * g4 : nullptr;
   }
   // the epilogue's gate (head-major [h][row][d]) is read now, so the block's last step does
@@ -329,29 +349,39 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   if (gpre) {
     const size_t grow = ((size_t)h * p.B * p.Q + (size_t)b * p.Q + qc[0]) * p.d;
     if (4 * g4 < p.d) gp0 = *reinterpret_cast<const h4*>(p.g + grow + 4 * g4);
-    if (16 + 4 * g4 < p.d) gp1 = *reinterpret_cast<const h4*>(p.g + grow + 16 + 4 * g4);
+    if (DP == 32 && 16 + 4 * g4 < p.d) gp1 = *reinterpret_cast<const h4*>(p.g + grow + 16 + 4 * g4);
   }
   const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
   // identity A operand of a 16x16x16 MFMA: lane supplies I[r16][4*g4 + j]
   const h4 ident = h4{(_Float16)(r16 == 4 * g4), (_Float16)(r16 == 4 * g4 + 1), (_Float16)(r16 == 4 * g4 + 2),
                       (_Float16)(r16 == 4 * g4 + 3)};
 
-  // Staging: a chunk is 512 16-byte pieces: piece t < 256 is K row t/4 (dims 8(t%4) .. +8),
-  // piece t >= 256 V^T row (t-256)/8 (keys 8((t-256)%8) .. +8).  Each thread stages NP pieces
-  // and lane l of every wave loads key bias l (wave 0 stores it).  With whole padded chunks
-  // every load is unconditional, so no branch separates a load from its use and the
-  // prefetched chunks stay in flight until they are needed.
-  constexpr int NT = 64 * (8 / QT), NP = 512 / NT;
+  // Staging: a chunk is 16 DP 16-byte pieces: piece t < 8 DP is K row t / SEGS (dims
+  // 8 (t % SEGS) .. +8), piece t >= 8 DP V^T row (t - 8 DP) / 8 (keys 8 ((t - 8 DP) % 8) .. +8).
+  // Each thread stages NP pieces (DP 16 with 512 threads: threads t and t + 256 load and store
+  // the same piece, so every load and store stays unconditional) and lane l of every wave
+  // loads key bias l (wave 0 stores it).  With whole padded chunks every load is
+  // unconditional, so no branch separates a load from its use and the prefetched chunks stay
+  // in flight until they are needed.
+  constexpr int NT = 64 * (8 / QT), NPC = 16 * DP, NP = NPC > NT ? NPC / NT : 1;
   const _Float16* gsrc[NP];
   int gstep[NP], loff[NP];   // source advance per chunk and LDS offset (elements)
+  // FIX: the piece's first key within a chunk and, for K, how many of its 8 dims are < dq
+  // (V^T dims past d only reach output dims that are never stored)
+  int pkey[NP], pdims[NP];
+  bool pisk[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int t = tid + j * NT, tv = t - 256;
-    const bool isk = t < 256;   // wave-uniform
-    gsrc[j] = isk ? kh + (size_t)(t >> 2) * FA_DP + (t & 3) * 8 : vh + (size_t)(tv >> 3) * Qp + (tv & 7) * 8;
-    gstep[j] = isk ? FA_KC * FA_DP : FA_KC;
-    const int key = t >> 2, krow = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
-    loff[j] = isk ? krow * FA_KLD + (t & 3) * 8 : FA_KC * FA_KLD + (tv >> 3) * FA_VLD + (tv & 7) * 8;
+    const int t = (tid + j * NT) % NPC, tv = t - 8 * DP;
+    const bool isk = t < 8 * DP;   // wave-uniform
+    const int key = t / SEGS, seg = t % SEGS;
+    gsrc[j] = isk ? kh + (size_t)key * DP + seg * 8 : vh + (size_t)(tv >> 3) * Qp + (tv & 7) * 8;
+    gstep[j] = isk ? FA_KC * DP : FA_KC;
+    const int krow = 16 * ((key >> 2) & 3) + 4 * (key >> 4) + (key & 3);
+    loff[j] = isk ? krow * KLD + seg * 8 : FA_KC * KLD + (tv >> 3) * FA_VLD + (tv & 7) * 8;
+    pisk[j] = isk;
+    pkey[j] = isk ? key : (tv & 7) * 8;
+    pdims[j] = isk ? min(max(p.dq - seg * 8, 0), 8) : 8;
   }
   // BL: thread t stages bias rows t/8 and t/8 + 64 of the block's 128, keys 8 (t % 8) .. +8,
   // so eight consecutive threads read one row's 128 bytes (coalesced, unlike the per-lane
@@ -381,7 +411,25 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     for (int j = 0; j < NP; ++j) r[j] = *reinterpret_cast<const uint4*>(gsrc[j] + (size_t)c * gstep[j]);
     kbr = kbb[c * FA_KC + lane];
   };
-  auto kv_store = [&](int buf, const uint4 (&r)[NP], float kbr) __attribute__((always_inline)) {
+  // zeroes what q, k and v^T leave unwritten (head dims past dq in K, keys past Q in K and V^T)
+  // in the registers of chunk c before they are stored: no padding of those buffers is ever
+  // cleared in memory
+  auto kv_fix = [&](int c, uint4 (&r)[NP]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int key0 = c * FA_KC + pkey[j];
+      const int n = pisk[j] ? (key0 < p.Q ? pdims[j] : 0) : min(max(p.Q - key0, 0), 8);
+      uint32_t m[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) m[w] = (2 * w < n ? 0xffffu : 0u) | (2 * w + 1 < n ? 0xffff0000u : 0u);
+      r[j].x &= m[0];
+      r[j].y &= m[1];
+      r[j].z &= m[2];
+      r[j].w &= m[3];
+    }
+  };
+  auto kv_store = [&](int buf, uint4 (&r)[NP], float kbr, int c) __attribute__((always_inline)) {
+    if constexpr (FIX) kv_fix(c, r);
 #pragma unroll
     for (int j = 0; j < NP; ++j) *reinterpret_cast<uint4*>(&KV[buf][loff[j]]) = r[j];
     if (wave == 0) {
@@ -405,17 +453,17 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
     bias_fetch<QT>(brow, 0, bq0);
     bias_fetch<QT>(brow, c1 * FA_KC, bq1);
   }
-  kv_store(0, st0, kb0);
+  kv_store(0, st0, kb0, 0);
   if (BL) bias_store(0);
   __syncthreads();
 
   float m_run[QT];
-  f4 o[3][QT];   // [dt][qt]: O^T[dt*16 + 4*g4 + i][query]; dt = 2: the row sums
+  f4 o[NDT + 1][QT];   // [dt][qt]: O^T[dt*16 + 4*g4 + i][query]; dt = NDT: the row sums
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     m_run[qt] = -1e30f;
 #pragma unroll
-    for (int dt = 0; dt < 3; ++dt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt <= NDT; ++dt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
   }
 
   // one chunk; RS = c % 2 is a compile-time constant so every register-set index is static
@@ -445,9 +493,9 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         f4 s[QT][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const h8 kf = *reinterpret_cast<const h8*>(&KV[buf][(kt * 16 + r16) * FA_KLD + kq]);
+          const QF kf = *reinterpret_cast<const QF*>(&KV[buf][(kt * 16 + r16) * KLD + qd]);
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
+          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = qk_mfma(kf, qf[qt], f4{0.f, 0.f, 0.f, 0.f});
         }
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
@@ -475,7 +523,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
             for (int i = 0; i < 4; ++i) pv[qt][kt][i] = (_Float16)__builtin_amdgcn_exp2f(s[qt][kt][i] - m_new);
           m_run[qt] = m_new;
 #pragma unroll
-          for (int dt = 0; dt < 3; ++dt) o[dt][qt] = o[dt][qt] * corr;
+          for (int dt = 0; dt <= NDT; ++dt) o[dt][qt] = o[dt][qt] * corr;
         }
       } else {
         // S accumulators start at bias - m, so the MFMA yields x - m; the bias lands through an
@@ -492,9 +540,9 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
         }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const h8 kf = *reinterpret_cast<const h8*>(&KV[buf][(kt * 16 + r16) * FA_KLD + kq]);
+          const QF kf = *reinterpret_cast<const QF*>(&KV[buf][(kt * 16 + r16) * KLD + qd]);
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma16(kf, qf[qt], s[qt][kt]);
+          for (int qt = 0; qt < QT; ++qt) s[qt][kt] = qk_mfma(kf, qf[qt], s[qt][kt]);
         }
         float mx[QT];
         bool rose = false;
@@ -528,7 +576,7 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
               for (int i = 0; i < 4; ++i) pv[qt][kt][i] = (_Float16)__builtin_amdgcn_exp2f(s[qt][kt][i] - d);
             m_run[qt] += d;
 #pragma unroll
-            for (int dt = 0; dt < 3; ++dt) o[dt][qt] = o[dt][qt] * corr;
+            for (int dt = 0; dt <= NDT; ++dt) o[dt][qt] = o[dt][qt] * corr;
           }
         }
       }
@@ -538,24 +586,24 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
 #pragma unroll
       for (int kh2 = 0; kh2 < 2; ++kh2) {
         // MFMA k index 8*g4 + j is key 16*g4 + 8*kh2 + j: one 16-byte piece of the V^T row
-        h8 vf[2];
+        h8 vf[NDT];
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-          vf[dt] = *reinterpret_cast<const h8*>(&KV[buf][FA_KC * FA_KLD + (dt * 16 + r16) * FA_VLD + 16 * g4 + 8 * kh2]);
+        for (int dt = 0; dt < NDT; ++dt)
+          vf[dt] = *reinterpret_cast<const h8*>(&KV[buf][FA_KC * KLD + (dt * 16 + r16) * FA_VLD + 16 * g4 + 8 * kh2]);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const h8 pf = h8{pv[qt][2 * kh2][0], pv[qt][2 * kh2][1], pv[qt][2 * kh2][2], pv[qt][2 * kh2][3],
                            pv[qt][2 * kh2 + 1][0], pv[qt][2 * kh2 + 1][1], pv[qt][2 * kh2 + 1][2],
                            pv[qt][2 * kh2 + 1][3]};
 #pragma unroll
-          for (int dt = 0; dt < 2; ++dt) o[dt][qt] = mfma16(vf[dt], pf, o[dt][qt]);
-          o[2][qt] = mfma16(ones, pf, o[2][qt]);
+          for (int dt = 0; dt < NDT; ++dt) o[dt][qt] = mfma16(vf[dt], pf, o[dt][qt]);
+          o[NDT][qt] = mfma16(ones, pf, o[NDT][qt]);
         }
       }
       // unconditional (after the last chunk it stores a repeat that nothing reads): with no
       // branch around the store the compiler's waits on the loads stay exact
-      if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1);
-      else kv_store(buf ^ 1, st0, kb0);
+      if constexpr (rs == 0) kv_store(buf ^ 1, st1, kb1, c + 1 < nkc ? c + 1 : nkc - 1);
+      else kv_store(buf ^ 1, st0, kb0, c + 1 < nkc ? c + 1 : nkc - 1);
       if (BL) {
         __builtin_amdgcn_sched_barrier(0);
         bias_store(buf ^ 1);
@@ -572,10 +620,10 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     if (qidx[qt] >= p.Q) continue;
-    const float inv = 1.0f / o[2][qt][0];
+    const float inv = 1.0f / o[NDT][qt][0];
     const size_t row = (size_t)b * p.Q + qidx[qt];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
       const int d0 = dt * 16 + 4 * g4;
       if (d0 >= p.d) continue;
       const size_t base = row * p.HD + (size_t)h * p.d + d0;
@@ -638,7 +686,10 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
 
   // keys padded to whole 64-key chunks (the flash kernel loads whole chunks)
   const int Qp = (Q + FA_KC - 1) / FA_KC * FA_KC;
-  const size_t qkv = (size_t)B * H * Qp * FA_DP * sizeof(_Float16);
+  // q, k and V^T padded to DP head dims: 16 when d <= 16 (the extra-MSA and MSA-module heads
+  // of 8), else 32
+  const int DP = d <= 16 ? 16 : FA_DP;
+  const size_t qkv = (size_t)B * H * Qp * DP * sizeof(_Float16);
   const size_t hd = (size_t)rows * HD * sizeof(_Float16);
   const size_t biash = (a.bias_mode == LF_BIAS_NONE) ? 0 : (size_t)H * Q * Qp * sizeof(_Float16);
   // buffers: q, k, v, g, o, key bias, f16 pair bias, output weights, packed lnproj weights x 2
@@ -713,15 +764,10 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
                                   : dst_rowmajor(a.out, a.act_dtype, (int)rows, C);
   const bool wo_inkernel = rowgemm_resident(ctx, (int)rows, HD, C, out_dst);
   if (!wo_inkernel) LF_TRY(expand_add_plain(ctx, xl, views[4], bufs[7], &wo, 1.f, "attention.expand"));
-  // head dims past d are zero in q, k and v; V^T keys past Q are zero (their weight is an
-  // exact 0, which must not meet a non-finite value)
-  if (pwa) {
-    if (Qp != Q) LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, vsize, ctx->stream), "attention memset"));
-  } else if (d < FA_DP || no_qk) {
-    for (int i = 0; i < 3; ++i) LF_TRY(check_hip(hipMemsetAsync(bufs[i], 0, qkv, ctx->stream), "attention memset"));
-  } else if (Qp != Q) {
-    LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, qkv, ctx->stream), "attention memset"));
-  }
+  // V^T keys past Q must be zero (their weight is an exact 0, which must not meet a
+  // non-finite value): the averaging GEMM reads them as stored; the flash kernel zeroes them,
+  // and the head dims past d of q and k, as it reads them (FlashParams::fix)
+  if (pwa && Qp != Q) LF_TRY(check_hip(hipMemsetAsync(bufs[2], 0, vsize, ctx->stream), "attention memset"));
   // f16 bias [h][i][j] (row stride Qp) from row (i, j); swapped: [h][j][i]
   const Dst bias_dst = a.swap_bias ? Dst{bias16, DT_F16, Q, 1, Qp, 1, (long long)Q * Qp, 0}
                                    : Dst{bias16, DT_F16, Q, Qp, 1, 1, (long long)Q * Qp, 0};
@@ -730,9 +776,9 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     LF_TRY(lnproj_prepare(ctx, pb, bufs[9], &xl, "attention.pair_bias"));
   }
   {
-    const long long hq = (long long)Qp * FA_DP;
-    if (gq >= 0) pp.g[gq].dst = Dst{qb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
-    if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, FA_DP, d, hq, 1};
+    const long long hq = (long long)Qp * DP;
+    if (gq >= 0) pp.g[gq].dst = Dst{qb, DT_F16, Q, (long long)H * hq, DP, d, hq, 1};
+    if (gk >= 0) pp.g[gk].dst = Dst{kb, DT_F16, Q, (long long)H * hq, DP, d, hq, 1};
     pp.g[gv].dst = pwa ? Dst{vb, DT_F16, Q, (long long)HD * Qp, 1, d, (long long)d * Qp, Qp}
                        : Dst{vb, DT_F16, Q, (long long)H * hq, 1, d, hq, Qp};
     // the gate head-major, g[h][b][q][d]: the consumers read one head's slice of many rows,
@@ -814,15 +860,28 @@ int attention(lf_context* ctx, const lf_attention_args& a, bool no_qk, bool shar
     fp.Q = Q;
     fp.d = d;
     fp.HD = HD;
+    fp.dq = no_qk ? 0 : d;
+    fp.fix = fp.dq < DP || Q != Qp;
     fp.nqb = (Q + FA_QPB - 1) / FA_QPB;
     fp.nblocks = (long long)fp.nqb * B * H;
     LaunchScope ls(ctx, "attention.flash");
-    if (fp.bias)
-      hipLaunchKernelGGL((flash_kernel<true, FA_QT_BIAS>), dim3((unsigned)fp.nblocks), dim3(512 / FA_QT_BIAS), 0,
-                         ctx->stream, fp);
+    const dim3 grid((unsigned)fp.nblocks), bb(512 / FA_QT_BIAS), bp(512 / FA_QT_PLAIN);
+    constexpr bool BLD = FA_QT_BIAS == 1;
+    // d <= 16 always zeroes (dq < 16 or Q ragged, or both: d = 16 with whole chunks is the
+    // exception, and rare); the 32-wide kernel has a variant without the zeroing for the
+    // usual d = 32 with whole chunks
+    if (fp.bias && DP == 16)
+      hipLaunchKernelGGL((flash_kernel<true, FA_QT_BIAS, BLD, 16, true>), grid, bb, 0, ctx->stream, fp);
+    else if (fp.bias && fp.fix)
+      hipLaunchKernelGGL((flash_kernel<true, FA_QT_BIAS, BLD, 32, true>), grid, bb, 0, ctx->stream, fp);
+    else if (fp.bias)
+      hipLaunchKernelGGL((flash_kernel<true, FA_QT_BIAS, BLD, 32, false>), grid, bb, 0, ctx->stream, fp);
+    else if (DP == 16)
+      hipLaunchKernelGGL((flash_kernel<false, FA_QT_PLAIN, false, 16, true>), grid, bp, 0, ctx->stream, fp);
+    else if (fp.fix)
+      hipLaunchKernelGGL((flash_kernel<false, FA_QT_PLAIN, false, 32, true>), grid, bp, 0, ctx->stream, fp);
     else
-      hipLaunchKernelGGL((flash_kernel<false, FA_QT_PLAIN>), dim3((unsigned)fp.nblocks), dim3(512 / FA_QT_PLAIN), 0,
-                         ctx->stream, fp);
+      hipLaunchKernelGGL((flash_kernel<false, FA_QT_PLAIN, false, 32, false>), grid, bp, 0, ctx->stream, fp);
   }
   LF_TRY(check_hip(hipGetLastError(), "flash launch"));
 

@@ -48,6 +48,25 @@ def test_msa_row_attention_pair_bias(ctx, blockw, s, n):
     H.assert_close(out, ref, label=f"row {s}x{n}")
 
 
+@pytest.mark.parametrize("c,heads", [(64, 8), (64, 4), (48, 4), (40, 8), (64, 2)])
+@pytest.mark.parametrize("n", [40, 64])
+def test_row_attention_head_widths(ctx, c, heads, n):
+    """Head dims 8, 16, 12, 5 and 32 over whole (64) and ragged (40) key chunks: the 16-wide
+    (d <= 16) and 32-wide kernels, with and without zeroing the unwritten head dims and keys."""
+    from localfold_amd import capi, device as D
+    w = S.synthetic_block_weights(c_m=c, c_z=32, c_outer=8, heads_msa=heads, heads_pair=2, tri_hidden=32,
+                                  msa_hidden=2 * c, pair_hidden=64, seed=heads + c)
+    act = S.synthetic_activations(3, n, c, 32, seed=n + c)
+    row = w["msaRowAttention"]
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, row["attention"], row["pairBias"])
+    out, _, _ = _run(ctx, act["msa"], act["msaMask"], ws, heads, False, capi.LF_BIAS_SEPARATE, act["pair"])
+    pb = dict(row["pairBias"], source="separate", activations=act["pair"])
+    ref = ops.attention_af2(act["msa"], act["msaMask"], row["attention"], heads, False, pb)
+    assert np.isfinite(out).all()
+    H.assert_close(out, ref, label=f"row c={c} heads={heads} n={n}")
+
+
 def test_row_attention_keys_over_one_stage(ctx, blockw):
     """600 keys (padded to 640): the kernel stages 512 keys in LDS at a time, so the second
     stage (128 keys, the last ones masked) runs after a block-wide reload."""
