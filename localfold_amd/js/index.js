@@ -359,6 +359,11 @@ function resident(device, key, build) {
 
 function finish(device, up, outputs, start) {
   const results = outputs.map(function download(o) {
+    if (o.f16) {
+      const bits = new Uint16Array(o.elements);
+      device.addon.download(device.ctx, o.buffer, bits);
+      return float16BitsToFloat32(bits);
+    }
     const host = new Float32Array(o.elements);
     device.addon.download(device.ctx, o.buffer, host);
     return host;
@@ -421,6 +426,70 @@ function opmWeights(up, w, cM, cOuter, cZ) {
   };
 }
 
+// ---- f16 storage ---------------------------------------------------------------------
+
+// IEEE binary16 bits of each value, rounded to nearest with ties to even; overflow goes to
+// infinity and NaN stays NaN (quiet).  The f32 bits are read through a Uint32Array view of
+// the input's buffer (a Float32Array is always 4-byte aligned).
+function float32ToFloat16Bits(values) {
+  const src = values instanceof Float32Array ? values : Float32Array.from(values);
+  const words = new Uint32Array(src.buffer, src.byteOffset, src.length);
+  const out = new Uint16Array(src.length);
+  for (let i = 0; i < words.length; i += 1) {
+    const bits = words[i];
+    const sign = (bits >>> 16) & 0x8000;
+    const abs = bits & 0x7fffffff;
+    if (abs >= 0x38800000 && abs < 0x477ff000) {
+      // f16 normal range [2^-14, 65520): rebias, drop 13 bits, round up when bit 12 is set and
+      // a lower bit or the kept last bit is (ties to even); a carry moves into the exponent
+      out[i] = sign | (((abs - 0x38000000) >>> 13) + ((abs >>> 12) & ((abs & 0x2fff) !== 0 ? 1 : 0)));
+      continue;
+    }
+    const exponent = (bits >>> 23) & 0xff;
+    let mantissa = bits & 0x7fffff;
+    const e = exponent - 112;   // the f16 exponent field (127 - 15 = 112)
+    if (e > 0 && e < 0x1f) {    // [65520, 65536): rounds to infinity
+      let h = (e << 10) | (mantissa >>> 13);
+      const rest = mantissa & 0x1fff;
+      if (rest > 0x1000 || (rest === 0x1000 && (h & 1))) h += 1;
+      out[i] = sign | h;
+    } else if (exponent === 0xff) {
+      out[i] = sign | 0x7c00 | (mantissa ? 0x200 : 0);
+    } else if (e >= 0x1f) {
+      out[i] = sign | 0x7c00;
+    } else if (e < -10) {
+      out[i] = sign;
+    } else {
+      // subnormal: value = (mantissa | 2^23) * 2^(e - 14) units of 2^-24
+      mantissa |= 0x800000;
+      const shift = 14 - e;
+      let half = mantissa >>> shift;
+      const rest = mantissa & ((1 << shift) - 1), mid = 1 << (shift - 1);
+      if (rest > mid || (rest === mid && (half & 1))) half += 1;
+      out[i] = sign | half;
+    }
+  }
+  return out;
+}
+
+// every binary16 value as f32, built on first use
+let f16Table = null;
+function float16BitsToFloat32(bits) {
+  if (f16Table === null) {
+    f16Table = new Float32Array(65536);
+    for (let h = 0; h < 65536; h += 1) {
+      const sign = (h & 0x8000) ? -1 : 1;
+      const exponent = (h >>> 10) & 0x1f, mantissa = h & 0x3ff;
+      if (exponent === 0) f16Table[h] = sign * mantissa * Math.pow(2, -24);
+      else if (exponent === 0x1f) f16Table[h] = mantissa ? NaN : sign * Infinity;
+      else f16Table[h] = sign * (1 + mantissa / 1024) * Math.pow(2, exponent - 15);
+    }
+  }
+  const out = new Float32Array(bits.length);
+  for (let i = 0; i < bits.length; i += 1) out[i] = f16Table[bits[i]];
+  return out;
+}
+
 // ---- kernels-as-library classes -------------------------------------------------------
 
 // webgpu/kernels/triangle/webgpu.js:38-169
@@ -428,10 +497,21 @@ function TriangleMultiplicationGpu(device, direction) {
   this.device = device;
   this.direction = direction;
 }
+// options.precision (webgpu/kernels/triangle/webgpu.js:40): 'f32' (the default) keeps z and the
+// update in f32 on the device, 'f16' stores them as f16 (z rounded on upload, the update read
+// back from f16); either way the kernels multiply f16 operands with f32 accumulation.
+// options.variance: only the AF2 'two-pass' LayerNorm runs here (AF3's 'fast' form is the
+// AF3 dialect of lf_tri_mult, which this class does not take).
 TriangleMultiplicationGpu.prototype.run = function run(input, options) {
   const self = this;
   return new Promise(function execute(resolve) {
     validateTriangleInput(input);
+    const precision = options && options.precision !== undefined ? options.precision : 'f32';
+    if (precision !== 'f32' && precision !== 'f16') throw new RangeError('precision must be "f32" or "f16"');
+    if (options && options.variance !== undefined && options.variance !== 'two-pass') {
+      throw new RangeError('variance "' + options.variance + '" is not supported: this class runs the AF2 ' +
+        'two-pass LayerNorm');
+    }
     const dev = self.device;
     const shape = input.shape;
     const up = new Uploads(dev);
@@ -441,14 +521,15 @@ TriangleMultiplicationGpu.prototype.run = function run(input, options) {
       return triangleWeights(wu, input.weights, shape.cZ, shape.cHidden);
     });
     const elements = shape.length * shape.length * shape.cZ;
-    const z = up.vec(input.z);
-    const out = up.alloc(elements * 4);
+    const half = precision === 'f16';
+    const z = half ? up.buffer(float32ToFloat16Bits(input.z)) : up.vec(input.z);
+    const out = up.alloc(elements * (half ? 2 : 4));
     dev.addon.triMult(dev.ctx, {
       direction: DIRECTION[self.direction], dialect: 0, length: shape.length, cZ: shape.cZ,
-      cHidden: shape.cHidden, actDtype: ACT.float32, z: z, mask: up.vec(input.mask), out: out,
+      cHidden: shape.cHidden, actDtype: half ? ACT.float16 : ACT.float32, z: z, mask: up.vec(input.mask), out: out,
       accumulate: 0, epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon, weights: weights,
     });
-    const r = finish(dev, up, [{ buffer: out, elements: elements }], start);
+    const r = finish(dev, up, [{ buffer: out, elements: elements, f16: half }], start);
     resolve({ output: r.results[0], elapsedMilliseconds: r.elapsedMilliseconds, memory: r.memory, kernels: r.kernels });
   });
 };
@@ -1054,5 +1135,7 @@ module.exports = {
   triangleMultiplicationOutgoingReference: triangleMultiplicationOutgoingReference,
   generator: generator,
   createDeterministicTriangleInput: createDeterministicTriangleInput,
+  float32ToFloat16Bits: float32ToFloat16Bits,
+  float16BitsToFloat32: float16BitsToFloat32,
   addon: addon,
 };

@@ -8,8 +8,18 @@ const fs = require('fs');
 const lf = require('../index.js');
 
 let failures = 0;
+const pending = [];
+// a check passes when fn returns, or when the promise it returns resolves
 function check(name, fn) {
-  try { fn(); console.log('ok   ' + name); } catch (e) { failures += 1; console.log('FAIL ' + name + ': ' + e.message); }
+  const fail = function fail(e) { failures += 1; console.log('FAIL ' + name + ': ' + e.message); };
+  try {
+    const r = fn();
+    if (r && typeof r.then === 'function') {
+      pending.push(r.then(function ok() { console.log('ok   ' + name); }, fail));
+      return;
+    }
+    console.log('ok   ' + name);
+  } catch (e) { fail(e); }
 }
 
 check('deterministic input has one value per pair channel', function t() {
@@ -107,4 +117,35 @@ check('addon exports every entry point', function t() {
   names.forEach(function each(n) { assert.strictEqual(typeof a[n], 'function', n); });
 });
 
-process.exitCode = failures === 0 ? 0 : 1;
+check('f16 storage conversion: IEEE binary16 with ties to even', function t() {
+  const cases = [[1, 0x3c00], [-2, 0xc000], [65504, 0x7bff], [65519, 0x7bff], [65520, 0x7c00], [0.1, 0x2e66],
+    [Math.pow(2, -24), 0x0001], [Math.pow(2, -25), 0x0000], [3 * Math.pow(2, -26), 0x0001],
+    [1 + Math.pow(2, -11), 0x3c00], [1 + 3 * Math.pow(2, -11), 0x3c02], [Infinity, 0x7c00], [-0, 0x8000],
+    [6.1e-5, 0x03ff], [Math.pow(2, -14), 0x0400]];
+  const bits = lf.float32ToFloat16Bits(Float32Array.from(cases.map(function v(c) { return c[0]; })));
+  cases.forEach(function each(c, i) { assert.strictEqual(bits[i], c[1], String(c[0])); });
+  assert.strictEqual(lf.float32ToFloat16Bits(Float32Array.of(NaN))[0] & 0x7c00, 0x7c00);
+  assert.ok(Number.isNaN(lf.float16BitsToFloat32(Uint16Array.of(0x7e00))[0]));
+  // every non-NaN binary16 value converts to f32 and back to the same bits
+  const all = new Uint16Array(65536);
+  for (let i = 0; i < 65536; i += 1) all[i] = i;
+  const back = lf.float32ToFloat16Bits(lf.float16BitsToFloat32(all));
+  for (let i = 0; i < 65536; i += 1) {
+    if (((i >>> 10) & 31) === 31 && (i & 1023) !== 0) continue;
+    assert.strictEqual(back[i], i, 'bits ' + i);
+  }
+});
+
+check('TriangleMultiplicationGpu rejects an unknown precision or variance before touching a device', function t() {
+  const input = lf.createDeterministicTriangleInput({ length: 2, cZ: 4, cHidden: 4 }, 1);
+  // a stand-in device: the checks throw before any addon call
+  const runner = new lf.TriangleMultiplicationOutgoingGpu({ tail: Promise.resolve() });
+  return Promise.all([
+    runner.run(input, { precision: 'f64' }).then(function no() { throw new Error('accepted f64'); },
+      function yes(e) { assert.ok(e instanceof RangeError && /precision/.test(e.message)); }),
+    runner.run(input, { variance: 'fast' }).then(function no() { throw new Error('accepted fast'); },
+      function yes(e) { assert.ok(e instanceof RangeError && /variance/.test(e.message)); }),
+  ]);
+});
+
+Promise.all(pending).then(function done() { process.exitCode = failures === 0 ? 0 : 1; });

@@ -53,6 +53,9 @@ async function main() {
     const out = await new lf.TriangleMultiplicationOutgoingGpu(device).run(bundle.input, { precision: 'f32' });
     // the reference's f16 bounds for these fixtures
     report('triangle outgoing ' + fixture, lf.errorMetrics(out.output, bundle.expected), { mean: 1e-3, max: 1e-2 });
+    // f16 storage: the reference's bounds for its own f16 runs (test/triangle-multiplication-outgoing.gpu.test.js:50-69)
+    const half = await new lf.TriangleMultiplicationOutgoingGpu(device).run(bundle.input, { precision: 'f16' });
+    report('triangle outgoing f16 ' + fixture, lf.errorMetrics(half.output, bundle.expected), { mean: 1e-3, max: 1e-2 });
   }
   const inc = cases.incoming;
   const bundle = await lf.loadTriangleReferenceBundleFromFiles(path.join(dir, inc.fixture, 'manifest.json'));

@@ -75,6 +75,31 @@ def _dump_tree(node, out: Path, prefix: str):
     return node
 
 
+def test_js_f16_conversion_matches_numpy(tmp_path):
+    """The JS host's f16 storage conversion (float32ToFloat16Bits) against numpy's float32 ->
+    float16 cast (IEEE round to nearest, ties to even) on values over the whole f16 range,
+    subnormals, overflow and exact ties included."""
+    rng = np.random.default_rng(3)
+    mant = rng.integers(0, 1 << 23, 60000, dtype=np.uint32)
+    expo = rng.integers(100, 145, 60000, dtype=np.uint32)     # 2^-27 .. 2^17
+    sign = rng.integers(0, 2, 60000, dtype=np.uint32) << 31
+    vals = ((expo << 23) | mant | sign).view(np.float32)
+    ties = (np.arange(1, 2048, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24)   # halfway cases
+    vals = np.concatenate([vals, ties, ties * 1024, np.float32([65504, 65519.99, 65520, 1e-8, 0, -0.0])])
+    src = tmp_path / "v.f32"
+    vals.astype("<f4").tofile(src)
+    code = ("const lf=require(process.argv[1]);const fs=require('fs');const b=fs.readFileSync(process.argv[2]);"
+            "const v=new Float32Array(b.buffer.slice(b.byteOffset,b.byteOffset+b.byteLength));"
+            "fs.writeFileSync(process.argv[3],Buffer.from(lf.float32ToFloat16Bits(v).buffer));")
+    dst = tmp_path / "h.u16"
+    r = subprocess.run([NODE, "-e", code, str(JS / "index.js"), str(src), str(dst)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = np.fromfile(dst, "<u2")
+    want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+
+
 @pytest.mark.gpu
 def test_js_gpu_suite(tmp_path):
     cases = {"fixtures": H.FIXTURES}
