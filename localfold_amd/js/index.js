@@ -540,7 +540,10 @@ function TriangleMultiplicationIncomingGpu(device) { TriangleMultiplicationGpu.c
 TriangleMultiplicationIncomingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
 
 // webgpu/kernels/attention.js:2580-2739: returns the update in the activation's layout
-function AttentionGpu(device) { this.device = device; }
+// options (webgpu/kernels/attention.js:2586-2622: storage, flashVariant, flashPrecision,
+// projectPrecision) pick among the reference's WGSL variants; there is one HIP path, so they
+// are kept and have no effect
+function AttentionGpu(device, options) { this.device = device; this.options = options || {}; }
 AttentionGpu.prototype.run = function run(input) {
   const self = this;
   return new Promise(function execute(resolve) {
