@@ -11,6 +11,7 @@ A weight value is either a numpy array (float32 values) or a record dict
  block | channel_axis} (the codec records of shared/weights/dtype.js).
 """
 import ctypes as C
+import functools
 
 import numpy as np
 import torch
@@ -27,6 +28,17 @@ def act_code(t: torch.Tensor) -> int:
     if t.dtype not in _TORCH_ACT:
         raise TypeError(f"activation dtype {t.dtype} is not float32/float16/bfloat16")
     return _TORCH_ACT[t.dtype]
+
+
+def _owned(build):
+    """The struct a weight builder returns points into its DeviceWeights' device buffers: it
+    keeps that DeviceWeights alive (weights built from a temporary stay valid)."""
+    @functools.wraps(build)
+    def wrapped(dw, *args, **kwargs):
+        struct = build(dw, *args, **kwargs)
+        struct._owner = dw
+        return struct
+    return wrapped
 
 
 def ptr(t) -> int:
@@ -148,6 +160,7 @@ class DeviceWeights:
 # Triangle multiplication
 # ---------------------------------------------------------------------------------------
 
+@_owned
 def tri_mult_weights(dw: DeviceWeights, w: dict, dialect: int = capi.LF_AF2) -> capi.lf_tri_mult_weights:
     """Struct for the reference's weight names.
 
@@ -211,6 +224,7 @@ def tri_mult(ctx: Context, z: torch.Tensor, mask: torch.Tensor, wstruct: capi.lf
 # Attention
 # ---------------------------------------------------------------------------------------
 
+@_owned
 def attention_weights_af2(dw: DeviceWeights, w: dict, pair_bias: dict = None) -> capi.lf_attention_weights:
     """AF2 gated attention (`webgpu/kernels/attention.js:15-57`): (in,out) weights;
     pair_bias: {layerNormScale, layerNormOffset, projectionWeight} (separate pair tensor) or
@@ -231,6 +245,7 @@ def attention_weights_af2(dw: DeviceWeights, w: dict, pair_bias: dict = None) ->
     return s
 
 
+@_owned
 def attention_weights_af3_grid(dw: DeviceWeights, w: dict) -> capi.lf_attention_weights:
     """AF3 grid attention (`cpu/af3/trunk/pairformer.js:322-431`): q/k/gate (out,in), v/output (in,out)."""
     s = capi.lf_attention_weights()
@@ -246,6 +261,7 @@ def attention_weights_af3_grid(dw: DeviceWeights, w: dict) -> capi.lf_attention_
     return s
 
 
+@_owned
 def attention_weights_af3_single(dw: DeviceWeights, w: dict, norm_scale, norm_offset, projection) -> capi.lf_attention_weights:
     """AF3 single attention (`cpu/af3/trunk/pairformer.js:446-485`) with the pair-logits LN and
     projection of `pairformerBlock` (`:516-537`) as a separate pair bias."""
@@ -297,6 +313,7 @@ def attention(ctx: Context, act: torch.Tensor, mask: torch.Tensor, wstruct: capi
 # Transition and outer product mean
 # ---------------------------------------------------------------------------------------
 
+@_owned
 def transition_weights(dw: DeviceWeights, w: dict, kind: int = capi.LF_TRANSITION_RELU) -> capi.lf_transition_weights:
     """AF2 (`webgpu/kernels/transition.js:445-460`): layerNormScale/Offset, firstWeight [C,H],
     firstBias, secondWeight [H,C], secondBias.  AF3 SwiGLU (`cpu/af3/trunk/pairformer.js:180-201`):
@@ -334,6 +351,7 @@ def transition(ctx: Context, x: torch.Tensor, wstruct: capi.lf_transition_weight
     return out
 
 
+@_owned
 def opm_weights(dw: DeviceWeights, w: dict, dialect: int = capi.LF_AF2) -> capi.lf_opm_weights:
     """AF2 (`webgpu/kernels/outer-product-mean.js:38-85`): layerNormScale/Offset, leftWeight,
     leftBias, rightWeight, rightBias, outputWeight [c*c, cZ], outputBias.  AF3
@@ -375,6 +393,7 @@ def outer_product_mean(ctx: Context, msa: torch.Tensor, mask: torch.Tensor, wstr
     return out
 
 
+@_owned
 def global_attention_weights(dw: DeviceWeights, w: dict) -> capi.lf_global_attention_weights:
     """Global column attention (`encodeGlobalAttention`, `webgpu/af2/evoformer/block.js:963-980`):
     queryNorm, queryWeight [C, H*d], keyWeight / valueWeight [C, d], gatingWeight [C, H*d] +
@@ -412,6 +431,7 @@ def global_column_attention(ctx: Context, msa: torch.Tensor, mask: torch.Tensor,
 # Blocks
 # ---------------------------------------------------------------------------------------
 
+@_owned
 def evoformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_evoformer_weights:
     """lf_evoformer_weights from the `syntheticBlockWeights` / AlphaFoldFixture structure
     (`tools/gpu/af2-synthetic-block.js:36-138`)."""
@@ -488,6 +508,7 @@ def evoformer_pair_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs,
     check(ctx.lib.lf_evoformer_pair_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
 
 
+@_owned
 def extra_msa_weights(dw: DeviceWeights, w: dict) -> capi.lf_extra_msa_weights:
     """An extra-MSA block's weights: the Evoformer structure with `msaColumnGlobalAttention`."""
     s = capi.lf_extra_msa_weights()
@@ -511,6 +532,7 @@ def extra_msa_stack(ctx: Context, msa, pair, msa_mask, pair_mask, wstructs, w0: 
     check(ctx.lib.lf_extra_msa_stack(ctx.handle, C.byref(a), arr, len(wstructs)))
 
 
+@_owned
 def pairformer_weights(dw: DeviceWeights, w: dict) -> capi.lf_pairformer_weights:
     """From the AF3 block structure of `cpu/af3/trunk/pairformer.js:495-541`."""
     s = capi.lf_pairformer_weights()
@@ -546,6 +568,7 @@ def pairformer_block(ctx: Context, pair, single, pair_mask, seq_mask, wstruct, s
     check(ctx.lib.lf_pairformer_block(ctx.handle, C.byref(a)))
 
 
+@_owned
 def pair_averaging_weights(dw: DeviceWeights, w: dict) -> capi.lf_pair_averaging_weights:
     """AF3 `msaAttention1` (`cpu/af3/trunk/msa.js:157-219`): actNorm / pairNorm, pairLogits
     [cZ, H], vProjection / gatingQuery [cM, H*d], outputProjection [H*d, cM], all (in,out)."""
@@ -579,6 +602,7 @@ def msa_pair_weighted_averaging(ctx: Context, msa: torch.Tensor, mask: torch.Ten
     return out
 
 
+@_owned
 def msa_module_weights(dw: DeviceWeights, w: dict) -> capi.lf_msa_module_weights:
     """One AF3 MSA-module block (`msaBlock`, `cpu/af3/trunk/msa.js:233-287`): outerProductMean,
     msaAttention1, msaTransition and the pair weights of a pairformer block."""
@@ -625,6 +649,7 @@ _EMBED_WEIGHTS = {"preprocess_1d_w": "preprocess1dWeight", "preprocess_1d_b": "p
                   "relpos_b": "relativePositionBias", "extra_w": "extraMsaWeight", "extra_b": "extraMsaBias"}
 
 
+@_owned
 def input_embedder_weights(dw: DeviceWeights, w: dict) -> capi.lf_input_embedder_weights:
     """InputEmbedderGpu's weights (`webgpu/af2/evoformer/input-embedder.js:9-26`), f32 (in,out)."""
     s = capi.lf_input_embedder_weights()

@@ -185,3 +185,22 @@ def test_weight_storage_paths(ctx, dtype, mode):
         torch.cuda.synchronize()
         ref = ops.tri_mult_af2(inp["z"], inp["mask"], dec, direction)
         H.assert_close(out.cpu().numpy(), ref, label=f"{dtype}/{mode}/{direction}")
+
+
+def test_weights_from_a_temporary_upload_stay_valid(ctx):
+    """A weight struct built from a DeviceWeights nobody else holds keeps those device buffers
+    alive (the struct points into them)."""
+    import gc
+    import torch
+    from localfold_amd import device as D
+    inp = S.deterministic_triangle_input(40, 128, 128, 9)
+    ws = D.tri_mult_weights(D.DeviceWeights(ctx.device), inp["weights"])
+    gc.collect()
+    # fresh allocations that would reuse freed weight memory
+    junk = [torch.full((1 << 20,), float("nan"), device=ctx.device) for _ in range(8)]
+    z = torch.as_tensor(inp["z"]).to(ctx.device)
+    out = D.tri_mult(ctx, z, torch.as_tensor(np.asarray(inp["mask"], np.float32)).to(ctx.device), ws, "outgoing")
+    torch.cuda.synchronize()
+    del junk
+    H.assert_close(out.cpu().numpy(), ops.tri_mult_af2(inp["z"], inp["mask"], inp["weights"], "outgoing"),
+                   label="temporary DeviceWeights")
