@@ -106,7 +106,8 @@ template <int ACT, int C, int NG>
 __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
   using S = MlpShape<C, NG>;
   constexpr int KS = S::KS, CT = S::CT, P1 = S::P1, P2 = S::P2, NT = S::NT;
-  __shared__ __attribute__((aligned(16))) _Float16 Wb[2][S::BUF];
+  // two buffers of two chunks each: one block barrier per pair of chunks
+  __shared__ __attribute__((aligned(16))) _Float16 Wb[2][2 * S::BUF];
   __shared__ __attribute__((aligned(16))) float Gs[2 * C];   // LN scale, offset
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
@@ -136,12 +137,14 @@ __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
   };
   stage_vec(Gs, p.ln_s, C, 1.f, C, tid, NT);
   stage_vec(Gs + C, p.ln_o, C, 0.f, C, tid, NT);
-  {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {   // chunks 0 and 1 (clamped) into buffer 0
     h8 a1[P1], a2[P2];   // (native vector types: a struct array would be copied through scratch)
-    load_w1(p.w, a1);
-    load_w2(p.w, a2);
-    put_w1(Wb[0], a1);
-    put_w2(Wb[0], a2);
+    const _Float16* src = p.w + (size_t)(c < nch ? c : nch - 1) * S::CE;
+    load_w1(src, a1);
+    load_w2(src, a2);
+    put_w1(&Wb[0][c * S::BUF], a1);
+    put_w2(&Wb[0][c * S::BUF], a2);
   }
   FragTile<ACT, KS> xt[2];
 #pragma unroll
@@ -163,11 +166,13 @@ __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
   }
 
   for (int s = 0; s < nch; ++s) {
-    const _Float16* cur = Wb[s & 1];
-    _Float16* nxt = Wb[(s & 1) ^ 1];
-    // the next chunk's W1^T pieces now, its W2^T pieces after GEMM1 (the last chunk reloads
-    // itself: loads stay unconditional)
-    const _Float16* src = p.w + (size_t)(s + 1 < nch ? s + 1 : s) * S::CE;
+    // chunk s in slot s % 2 of buffer (s / 2) % 2; chunk s + 2 goes to the same slot of the
+    // other buffer, which every wave left at the previous pair's barrier
+    const _Float16* cur = &Wb[(s >> 1) & 1][(s & 1) * S::BUF];
+    _Float16* nxt = &Wb[((s >> 1) & 1) ^ 1][(s & 1) * S::BUF];
+    // chunk s + 2's W1^T pieces now, its W2^T pieces after GEMM1 (the last pair reloads the
+    // last chunk into a buffer nothing reads again: loads stay unconditional)
+    const _Float16* src = p.w + (size_t)(s + 2 < nch ? s + 2 : nch - 1) * S::CE;
     h8 n1[P1];
     load_w1(src, n1);
 
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(64 * MLP_WAVES) void mlp_kernel(MlpParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     put_w2(nxt, n2);
-    __syncthreads();
+    if (s & 1) __syncthreads();   // block-uniform: the pair's reads done, the next pair's writes visible
   }
 
   // residual and store: lane -> row r16 of tile rt, channels 16ct + 4g4 .. +3
