@@ -213,9 +213,12 @@ template <int ACT, int KS>
 __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjParams p) {
   constexpr int KP = KS * 32, LDW = KP + 8;
   constexpr int NREG = (64 * KP / 8 + 511) / 512;
-  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][64 * LDW];
+  // NB chunks per LDS buffer, one block barrier per NB chunks: two at K = 256 (the block is
+  // alone on its CU there, and two buffers of two chunks fit), one elsewhere
+  constexpr int NB = KS == 8 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][NB][64 * LDW];
   __shared__ __attribute__((aligned(16))) float Gs[2 * KP];
-  __shared__ __attribute__((aligned(16))) ChunkTab Tab[2];
+  __shared__ __attribute__((aligned(16))) ChunkTab Tab[2][NB];
   __shared__ int Rp[MAX_GROUPS][LP_ROWS];   // destination row offsets per group and block row
   __shared__ float Rm[LP_ROWS];             // OP_ROWMASK multipliers of the block rows
   __shared__ int Cg[MAX_CHUNKS], Cc[MAX_CHUNKS], Cf[MAX_CHUNKS];   // chunk -> group, first column, fast
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
     const int c0 = __builtin_amdgcn_readfirstlane(p.chunk_c0[ci0]);
     float b0, b1;
     chunk_tab_load(p, g, c0, lane, b0, b1);
-    if (wave == 0) chunk_tab_put(Tab[0], p, g, c0, lane, b0, b1);
+    if (wave == 0) chunk_tab_put(Tab[0][0], p, g, c0, lane, b0, b1);
   }
   const int row_block = blockIdx.x * LP_ROWS;
   for (int i = tid; i < p.ngroups * LP_ROWS; i += 512) {
@@ -255,8 +258,18 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
   const int rbase = row_block + wave * 32;
   auto srow_of = [&](int r) { return p.rmB > 0 ? (r % p.rmQ) * p.rmB + r / p.rmQ : r; };
   h8 xb[2][KS];
-  chunk_store<KP, NREG>(Ws[0], regs, tid);
-  __syncthreads();  // Gs, chunk 0, its table and the row offsets staged
+  chunk_store<KP, NREG>(Ws[0][0], regs, tid);
+  if constexpr (NB == 2) {   // the second chunk of the first pair (clamped)
+    const int c2 = min(ci0 + 1, ci1 - 1);
+    chunk_load<KP, NREG>(p, c2, regs, tid);
+    const int g = __builtin_amdgcn_readfirstlane(p.chunk_group[c2]);
+    const int c0 = __builtin_amdgcn_readfirstlane(p.chunk_c0[c2]);
+    float b0, b1;
+    chunk_tab_load(p, g, c0, lane, b0, b1);
+    chunk_store<KP, NREG>(Ws[0][1], regs, tid);
+    if (wave == 0) chunk_tab_put(Tab[0][1], p, g, c0, lane, b0, b1);
+  }
+  __syncthreads();  // Gs, the first chunks, their tables and the row offsets staged
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int myrow = rbase + tt * 16 + r16;
@@ -270,12 +283,14 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
   }
 
   for (int ci = ci0; ci < ci1; ++ci) {
-    const int kb = (ci - ci0) & 1;   // LDS buffer of this chunk
-    const _Float16* W = Ws[kb];
-    const ChunkTab& T = Tab[kb];
-    // unconditional (the last iteration reloads its own chunk): with no branch around the
+    // chunk ci in slot rel % NB of buffer (rel / NB) % 2; chunk ci + NB goes to the same slot
+    // of the other buffer, which every wave left at the previous barrier
+    const int rel = ci - ci0, kb = (rel / NB) & 1, sl = rel % NB;
+    const _Float16* W = Ws[kb][sl];
+    const ChunkTab& T = Tab[kb][sl];
+    // unconditional (the last chunks reload the last one): with no branch around the
     // prefetch the compiler's wait before the LDS store counts only this iteration's stores
-    const int cn = min(ci + 1, ci1 - 1);
+    const int cn = min(ci + NB, ci1 - 1);
     chunk_load<KP, NREG>(p, cn, regs, tid);
     // wave-uniform by construction; readfirstlane lets the compiler keep them in SGPRs
     const int gn = __builtin_amdgcn_readfirstlane(Cg[cn]), cn0 = __builtin_amdgcn_readfirstlane(Cc[cn]);
@@ -303,8 +318,8 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
       if (tr) lnproj_mma<KS, true>(acc, W, xb, tb, ts, r16, kq);
       else lnproj_mma<KS, false>(acc, W, xb, tb, ts, r16, kq);
       if (th == 0) {
-        chunk_store<KP, NREG>(Ws[kb ^ 1], regs, tid);
-        if (wave == 0) chunk_tab_put(Tab[kb ^ 1], p, gn, cn0, lane, tb0, tb1);
+        chunk_store<KP, NREG>(Ws[kb ^ 1][sl], regs, tid);
+        if (wave == 0) chunk_tab_put(Tab[kb ^ 1][sl], p, gn, cn0, lane, tb0, tb1);
       }
       __builtin_amdgcn_sched_barrier(0);
 #define LF_EPI(OPV)                                                                          \
@@ -321,7 +336,7 @@ __global__ __launch_bounds__(512, KS <= 4 ? 4 : 2) void lnproj_kernel(LnProjPara
       }
 #undef LF_EPI
     }
-    __syncthreads();
+    if (sl == NB - 1) __syncthreads();   // block-uniform
   }
 }
 
