@@ -67,6 +67,26 @@ def test_row_attention_head_widths(ctx, c, heads, n):
     H.assert_close(out, ref, label=f"row c={c} heads={heads} n={n}")
 
 
+@pytest.mark.parametrize("n", [24, 101])
+def test_triangle_attention_256_channels(ctx, n):
+    """256-channel triangle attention, 8 heads of 32: 17 projection chunks of 64 columns (q, k,
+    v, g and the bias), which the 256-wide projection kernel stages two to an LDS buffer, over
+    column ranges of one chunk (N = 24) and of two with an odd remainder (N = 101)."""
+    from localfold_amd import capi, device as D
+    w = S.synthetic_block_weights(c_m=64, c_z=256, c_outer=8, heads_msa=2, heads_pair=8, tri_hidden=32,
+                                  msa_hidden=64, pair_hidden=64, seed=n)
+    tw = w["triangleAttentionStarting"]
+    act = S.synthetic_activations(1, n, 64, 256, seed=n + 1)
+    mask = act["pairMask"].copy()
+    mask[:, -2:] = 0
+    dw = D.DeviceWeights(ctx.device)
+    ws = D.attention_weights_af2(dw, tw["attention"], tw["pairBias"])
+    out, _, _ = _run(ctx, act["pair"], mask, ws, 8, False, capi.LF_BIAS_NORMALIZED_INPUT)
+    ref = ops.attention_af2(act["pair"], mask, tw["attention"], 8, False,
+                            dict(tw["pairBias"], source="normalized-input"))
+    H.assert_close(out, ref, label=f"tri-att c=256 n={n}")
+
+
 def test_row_attention_keys_over_one_stage(ctx, blockw):
     """600 keys (padded to 640): the kernel stages 512 keys in LDS at a time, so the second
     stage (128 keys, the last ones masked) runs after a block-wide reload."""

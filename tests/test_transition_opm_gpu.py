@@ -39,6 +39,24 @@ def test_transition_relu(ctx, blockw, rows_shape, which, chunk):
     H.assert_close(out.cpu().numpy(), ref, label=f"{which} {rows_shape} chunk={chunk}")
 
 
+@pytest.mark.parametrize("c,hidden", [(128, 96), (256, 96), (128, 32)])
+def test_transition_fused_odd_chunk_count(ctx, c, hidden):
+    """Hidden widths of 3 and 1 chunks of 32: the fused kernel stages its weight chunks two to
+    an LDS buffer, so a count that is not a multiple of two ends on a half-used buffer."""
+    import torch
+    from localfold_amd import device as D
+    st = S.Stream(c + hidden)
+    w = {"layerNormScale": st.values(c, 0.2, 1), "layerNormOffset": st.values(c, 0.1),
+         "firstWeight": st.normal(c * hidden, 1 / np.sqrt(c)).reshape(c, hidden), "firstBias": st.values(hidden, 0.1),
+         "secondWeight": st.normal(hidden * c, 1 / np.sqrt(hidden)).reshape(hidden, c),
+         "secondBias": st.values(c, 0.05)}
+    x = st.values(600 * c, 1.5).reshape(600, c)
+    dw = D.DeviceWeights(ctx.device)
+    out = D.transition(ctx, _dev(ctx, x), D.transition_weights(dw, w), hidden)
+    torch.cuda.synchronize()
+    H.assert_close(out.cpu().numpy(), ops.transition_af2(x, w), label=f"c={c} hidden={hidden}")
+
+
 @pytest.mark.parametrize("which,dt", [("pairTransition", "bfloat16"), ("msaTransition", "bfloat16"),
                                       ("msaTransition", "float16")])
 def test_transition_fused_dtypes(ctx, blockw, which, dt):
