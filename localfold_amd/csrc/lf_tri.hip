@@ -1456,9 +1456,9 @@ static int tri_mult_impl(lf_context* ctx, const lf_tri_mult_args& a, void* scrat
   LF_TRY(make_view(w.wg, C, C, "linearGWeight", &views[5]));
 
   // the 128-wide project kernel for whole 16-pair tiles (32-bit per-lane store offsets) also
-  // stores each pair's LN_in statistics for the output kernel, for 16-bit activations: with
-  // f32 activations that variant computed wrong projections on the GPU (found by the f32
-  // parity tests; cause not identified), so f32 keeps the kernel that recomputes them
+  // stores each pair's LN_in statistics for the output kernel, for 16-bit activations; with
+  // f32 activations the hand-over measured neutral (output kernel -3%, project kernel +3%:
+  // its f32 tiles leave less room to hide the extra store), so f32 recomputes them
   const bool wide = C == 128 && H == 128 && N >= 16;
   const bool v3 = wide && a.act_dtype != LF_F32 && (a.direction != LF_OUTGOING ? N % 16 == 0 : P % 16 == 0) &&
                   P < (1 << 27);
