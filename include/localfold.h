@@ -16,9 +16,11 @@
  *    and masks are always float32 (the reference keeps them float32:
  *    tools/quantize_af3.py:57, KEEP_FLOAT32).
  *  - Weights are lf_weight records: float32/float16/bfloat16 values, or the reference's
- *    codecs decoded inside the kernels - int8 symmetric (code*scale) and int5 asymmetric
+ *    codecs decoded on the device - int8 symmetric (code*scale) and int5 asymmetric
  *    (code*scale+zero, LSB-first 5-bit codes, one slack byte), fp16 scale/zero tables
- *    (shared/weights/dtype.js:212-406).  `group` > 0 is the reference's flat group map
+ *    (shared/weights/dtype.js:212-406) - inside the triangle-multiplication kernels and the
+ *    weight-resident output projections as they stage them into LDS, and by one short
+ *    per-call pass for the streaming projections, transitions and OPM.  `group` > 0 is the reference's flat group map
  *    (group index = flat stored index / group: 64 for int8, 32 for int5); `group` == 0
  *    is one group per output channel.
  *  - Return value: LF_OK, or an error code; lf_last_error() holds the message
