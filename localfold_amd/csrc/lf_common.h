@@ -102,8 +102,6 @@ __device__ __forceinline__ float wdecode(const WView& w, int k, int n) {
 }
 
 // True when consecutive k of one logical column are adjacent in storage.
-__device__ __forceinline__ bool wview_k_contiguous(const WView& w) { return w.ld_k == 1; }
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
@@ -613,11 +611,11 @@ __device__ __forceinline__ void frag_ln_raw2(FragTile<ACT, KS>& t0, FragTile<ACT
   }
 }
 
-// LayerNorm of one raw tile into MFMA fragments (frag_ln_raw2 for a single tile).
 template <int ACT, int KS>
 __device__ __forceinline__ void frag_ln_given(FragTile<ACT, KS>& t0, h8 (&a0)[KS], const float* gamma,
                                               const float* beta, float m0, float i0, int lane);
 
+// LayerNorm of one raw tile into MFMA fragments (frag_ln_raw2 for a single tile).
 template <int ACT, int KS>
 __device__ __forceinline__ void frag_ln_raw1(FragTile<ACT, KS>& t0, h8 (&a0)[KS], int C, const float* gamma,
                                              const float* beta, float eps, bool fast_var, int lane) {
@@ -626,6 +624,8 @@ __device__ __forceinline__ void frag_ln_raw1(FragTile<ACT, KS>& t0, h8 (&a0)[KS]
   frag_ln_given(t0, a0, gamma, beta, m0, i0, lane);
 }
 
+// The normalisation of frag_ln_raw1 with a row's mean m0 and 1/std i0 already known (the
+// triangle output kernel reads them from the project kernel).
 template <int ACT, int KS>
 __device__ __forceinline__ void frag_ln_given(FragTile<ACT, KS>& t0, h8 (&a0)[KS], const float* gamma,
                                               const float* beta, float m0, float i0, int lane) {
@@ -642,16 +642,6 @@ __device__ __forceinline__ void frag_ln_given(FragTile<ACT, KS>& t0, h8 (&a0)[KS
     for (int e = 0; e < 8; ++e) a0[j][e] = (_Float16)((t0.get(j, e) - m0) * i0 * gg[e] + bb[e]);
     __builtin_amdgcn_sched_barrier(0);
   }
-}
-
-// Raw tile -> float values (zero past C).
-template <int ACT, int KS>
-__device__ __forceinline__ void frag_values(const FragTile<ACT, KS>& t, float (&x)[KS][8], int C, int lane) {
-  const int g = lane >> 4;
-#pragma unroll
-  for (int j = 0; j < KS; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[j][e] = (32 * j + 8 * g + e < C) ? t.get(j, e) : 0.f;
 }
 
 // dst[i] = v[i] when v is non-null and i < n, else dflt; i < cap (block-cooperative).
