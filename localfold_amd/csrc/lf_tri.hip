@@ -1189,19 +1189,26 @@ __global__ __launch_bounds__(64 * NWV) void tri_output_v3_kernel(TriOutputParams
     if constexpr (ZS) zs = p.stats[t0 * 16 + r16];
     if constexpr (VECX) x_fetch(xv, p.X, p.P, t0 * 16, lane);
   }
+  // the biases and LayerNorm vectors (threads 0-127, one channel each) are loaded before the
+  // weights, so their round trip overlaps the weight stage's instead of following it
+  float vv[6] = {0.f, 0.f, 1.f, 0.f, 1.f, 0.f};
+  if (tid < 128) {   // wave-uniform
+    if (p.bz) vv[0] = p.bz[tid];
+    if (p.bg) vv[1] = TRI_NLOG2E * p.bg[tid];
+    if (p.ln_out_s) vv[2] = p.ln_out_s[tid];
+    if (p.ln_out_o) vv[3] = p.ln_out_o[tid];
+    if (p.ln_in_s) vv[4] = p.ln_in_s[tid];
+    if (p.ln_in_o) vv[5] = p.ln_in_o[tid];
+  }
   {
     _Float16* const dst[2] = {Wz, Wg};
     const WSrc* const src[2] = {&p.wz, &p.wg};
     stage_resident<2, NT>(dst, src, tid);
   }
-  for (int i = tid; i < 128; i += NT) {
-    Vs[i] = p.bz ? p.bz[i] : 0.f;
-    Vs[128 + i] = p.bg ? TRI_NLOG2E * p.bg[i] : 0.f;
+  if (tid < 128) {
+#pragma unroll
+    for (int q = 0; q < 6; ++q) Vs[128 * q + tid] = vv[q];
   }
-  stage_vec(Vs + 256, p.ln_out_s, 128, 1.f, 128, tid, NT);
-  stage_vec(Vs + 384, p.ln_out_o, 128, 0.f, 128, tid, NT);
-  stage_vec(Vs + 512, p.ln_in_s, 128, 1.f, 128, tid, NT);
-  stage_vec(Vs + 640, p.ln_in_o, 128, 0.f, 128, tid, NT);
   __syncthreads();
 
   // One tile: LN_out of X (LDS buffer Xc) and LN_in of z (zc), then two passes of 64 output
