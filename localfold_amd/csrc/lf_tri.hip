@@ -477,12 +477,114 @@ __global__ __launch_bounds__(256, TM == 128 ? 2 : 3) void tri_contract_dma_kerne
   }
 }
 
+// Large N (a multiple of 256, at least 768): 256 x 256 tiles, 8 waves in a 2 x 4 grid, each
+// wave 128 x 64 (32 accumulator tiles), the same direct-to-LDS double buffering as above in
+// two 64 KB stages (one block per CU).  A wave's K step reads 384 bytes of LDS per MFMA
+// instead of the 64 x 64 tile's 512.  Measured at N = 1024 (config-5 shape, same box,
+// alternating runs): 0.373 -> 0.306 ms per contraction.  Four 32-wide stages in the same LDS
+// measured 0.38 ms (twice the barriers).
+
+
+template <int BK>
+__global__ __launch_bounds__(512) void tri_contract_big_kernel(TriContractParams p) {
+  constexpr int TM = 256, NT = 512, FM = 8, FN = 4, WT = 128, WTN = 64, CH = BK / 8, PER = TM * CH / NT,
+                STAGE = TM * BK;
+  static_assert((TM * CH) % NT == 0, "tile rows must split into whole load rounds");
+  __shared__ __attribute__((aligned(16))) _Float16 S[2][2][STAGE];   // [stage][L, R][row][k]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tm = p.N / TM, tiles = tm * tm;
+  const int total = (int)gridDim.x, per = total >> 3;
+  int lin = (int)blockIdx.x;
+  if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
+  const int h = lin / tiles, t = lin - h * tiles;
+  const int m0 = (t / tm) * TM, n0 = (t % tm) * TM;
+  const size_t plane = (size_t)p.N * p.N;
+  const _Float16* L = p.L + h * plane;
+  const _Float16* R = p.R + h * plane;
+  const _Float16* gl[PER];
+  const _Float16* gr[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int q = it * NT + tid, r = q / CH, c = (q % CH) ^ ct_swz<BK>(r);
+    gl[it] = L + (size_t)(m0 + r) * p.N + c * 8;
+    gr[it] = R + (size_t)(n0 + r) * p.N + c * 8;
+  }
+  auto issue = [&](int k0, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int base = (it * NT + wave * 64) * 8;
+#if __HIP_DEVICE_COMPILE__
+      __builtin_amdgcn_global_load_lds(gl[it] + k0, &S[st][0][base], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gr[it] + k0, &S[st][1][base], 16, 0, 0);
+#endif
+    }
+  };
+  f4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int nk = p.N / BK;
+  issue(0, 0);
+  for (int ks = 0; ks < nk; ++ks) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // step ks in LDS for every wave; every wave done with the other stage
+    if (ks + 1 < nk) issue((ks + 1) * BK, (ks + 1) & 1);
+    const _Float16* Ls = S[ks & 1][0];
+    const _Float16* Rs = S[ks & 1][1];
+    // every fragment of the step is read before the first MFMA (the scheduling barrier keeps
+    // the compiler from interleaving them in small groups, each waiting for its reads)
+    constexpr int KK = BK / 32;
+    h8 a[KK][FM], b[KK][FN];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int row = wn * WTN + j * 16 + r16;
+        b[kk][j] = *reinterpret_cast<const h8*>(Rs + row * BK + ((kk * 4 + g4) ^ ct_swz<BK>(row)) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * WT + i * 16 + r16;
+        a[kk][i] = *reinterpret_cast<const h8*>(Ls + row * BK + ((kk * 4 + g4) ^ ct_swz<BK>(row)) * 8);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(b[kk][j], a[kk][i], acc[i][j]);
+  }
+  _Float16* X = p.X + h * plane;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int gm = m0 + wm * WT + i * 16 + r16;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int gn = n0 + wn * WTN + j * 16 + 4 * g4;
+      h4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = (_Float16)(acc[i][j][r] * p.scale);
+      *reinterpret_cast<h4*>(X + (size_t)gm * p.N + gn) = o;
+    }
+  }
+}
+
 template <int TM, int BK = 64, int MINW = 1>
 static void launch_contract(lf_context* ctx, const TriContractParams& cp, int H, bool kmajor) {
   const int tm = (cp.N + TM - 1) / TM;
   const dim3 grid((unsigned)(tm * tm * H));
   const bool vec = (cp.N % 8) == 0;
   if (!kmajor) {
+    if (TM == 128 && cp.N % 256 == 0 && cp.N >= 768) {
+      hipLaunchKernelGGL((tri_contract_big_kernel<64>), dim3((unsigned)((cp.N / 256) * (cp.N / 256) * H)),
+                         dim3(512), 0, ctx->stream, cp);
+      return;
+    }
     if (TM == 128 && cp.N % 64 == 0) {
       // 128-row tiles at two blocks per CU, or, when the grid is only a few waves of blocks
       // and the last one would run mostly empty, 96-row tiles at three per CU.  Measured: at
