@@ -477,7 +477,8 @@ __global__ __launch_bounds__(256, TM == 128 ? 2 : 3) void tri_contract_dma_kerne
   }
 }
 
-// Large N (a multiple of 256, at least 768): 256 x 256 tiles, 8 waves in a 2 x 4 grid, each
+// Large N (a multiple of 64, at least 768, when whole 256-row tiles add at most 10% to the
+// work of 128-row ones; rows past N clamped as above): 256 x 256 tiles, 8 waves in a 2 x 4 grid, each
 // wave 128 x 64 (32 accumulator tiles), the same direct-to-LDS double buffering as above in
 // two 64 KB stages (one block per CU).  A wave's K step reads 384 bytes of LDS per MFMA
 // instead of the 64 x 64 tile's 512.  Measured at N = 1024 (config-5 shape, same box,
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(512) void tri_contract_big_kernel(TriContractParams
   __shared__ __attribute__((aligned(16))) _Float16 S[2][2][STAGE];   // [stage][L, R][row][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
-  const int tm = p.N / TM, tiles = tm * tm;
+  const int tm = (p.N + TM - 1) / TM, tiles = tm * tm;
   const int total = (int)gridDim.x, per = total >> 3;
   int lin = (int)blockIdx.x;
   if (lin < per * 8) lin = (lin & 7) * per + (lin >> 3);
@@ -507,8 +508,8 @@ __global__ __launch_bounds__(512) void tri_contract_big_kernel(TriContractParams
 #pragma unroll
   for (int it = 0; it < PER; ++it) {
     const int q = it * NT + tid, r = q / CH, c = (q % CH) ^ ct_swz<BK>(r);
-    gl[it] = L + (size_t)(m0 + r) * p.N + c * 8;
-    gr[it] = R + (size_t)(n0 + r) * p.N + c * 8;
+    gl[it] = L + (size_t)min(m0 + r, p.N - 1) * p.N + c * 8;
+    gr[it] = R + (size_t)min(n0 + r, p.N - 1) * p.N + c * 8;
   }
   auto issue = [&](int k0, int st) __attribute__((always_inline)) {
 #pragma unroll
@@ -569,7 +570,7 @@ __global__ __launch_bounds__(512) void tri_contract_big_kernel(TriContractParams
       h4 o;
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[r] = (_Float16)(acc[i][j][r] * p.scale);
-      *reinterpret_cast<h4*>(X + (size_t)gm * p.N + gn) = o;
+      if (gm < p.N && gn < p.N) *reinterpret_cast<h4*>(X + (size_t)gm * p.N + gn) = o;
     }
   }
 }
@@ -580,9 +581,10 @@ static void launch_contract(lf_context* ctx, const TriContractParams& cp, int H,
   const dim3 grid((unsigned)(tm * tm * H));
   const bool vec = (cp.N % 8) == 0;
   if (!kmajor) {
-    if (TM == 128 && cp.N % 256 == 0 && cp.N >= 768) {
-      hipLaunchKernelGGL((tri_contract_big_kernel<64>), dim3((unsigned)((cp.N / 256) * (cp.N / 256) * H)),
-                         dim3(512), 0, ctx->stream, cp);
+    const long long t256 = (cp.N + 255) / 256, t128 = (cp.N + 127) / 128;
+    if (TM == 128 && cp.N % 64 == 0 && cp.N >= 768 && t256 * t256 * 65536 * 10 <= t128 * t128 * 16384 * 11) {
+      hipLaunchKernelGGL((tri_contract_big_kernel<64>), dim3((unsigned)(t256 * t256 * H)), dim3(512), 0, ctx->stream,
+                         cp);
       return;
     }
     if (TM == 128 && cp.N % 64 == 0) {

@@ -118,15 +118,15 @@ def test_config2_full_size(ctx):
     assert np.isfinite(out1).all() and np.isfinite(out2).all()
 
 
-@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-def test_large_contraction_tiles(ctx, direction):
-    """N = 768, a multiple of 256: the contraction runs on 256 x 256 tiles (8 waves of
-    128 x 64), every other step as at smaller N; against the oracle."""
+@pytest.mark.parametrize("n,direction", [(768, "outgoing"), (768, "incoming"), (960, "outgoing")])
+def test_large_contraction_tiles(ctx, n, direction):
+    """N = 768 and 960: the contraction runs on 256 x 256 tiles (8 waves of 128 x 64); at 960
+    the last tile row and column are clamped (64 rows past N); against the oracle."""
     import torch
-    inp = S.deterministic_triangle_input(768, 128, 128, 29)
+    inp = S.deterministic_triangle_input(n, 128, 128, 29)
     out, zin = _run(ctx, inp["z"], inp["mask"], inp["weights"], direction, act=torch.bfloat16)
     ref = ops.tri_mult_af2(zin, inp["mask"], inp["weights"], direction)
-    H.assert_close(out, ref, label=f"768/{direction}")
+    H.assert_close(out, ref, label=f"{n}/{direction}")
 
 
 def test_invalid_shapes_rejected(ctx):
