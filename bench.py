@@ -1,4 +1,4 @@
-"""Benchmark: BASELINE config 2 - standalone triangle multiplicative update, outgoing then
+"""Benchmark: the headline workload - standalone triangle multiplicative update, outgoing then
 incoming, N_res = 384, c_z = c_hidden = 128, bf16 pair, int5 weights with per-output-channel
 fp16 scales/zeros, last 16 residues masked.
 
@@ -245,7 +245,7 @@ def timed_restored(fn, restore, reps):
 
 
 def triangle_attention_config3(ctx, D, synthetic, reps):
-    """starting then ending node triangle attention, N=512, fp16."""
+    """Triangle attention workload: starting then ending node, N=512, fp16."""
     import torch
     from localfold_amd import capi
     c3 = synthetic.config3_inputs()
@@ -278,7 +278,7 @@ def triangle_attention_config3(ctx, D, synthetic, reps):
 
 
 def evoformer_block_config4(ctx, D, synthetic, reps, storage="f32"):
-    """BASELINE config 4 at one block: N_res=384, N_seq=512, int8 weights; the residual
+    """The AF2 Evoformer workload at one block: N_res=384, N_seq=512, int8 weights; the residual
     stream (msa, pair) stored in `storage` (f32: the configuration whose parity against the
     oracle is tested within the north-star bound; bf16: the config's storage type, which
     meets the relative bound only)."""
@@ -410,7 +410,7 @@ def input_embedder_n384(ctx, D, synthetic, reps):
 
 
 def evoformer_stack_config4(ctx, D, synthetic, reps, storage="f32"):
-    """BASELINE config 4 in full: the 48-block AF2 Evoformer stack at N_res=384, N_seq=512, one
+    """The AF2 Evoformer workload in full: the 48-block stack at N_res=384, N_seq=512, one
     pass (1 recycle), 48 distinct int8 weight sets, bf16 inputs, the residual stream stored in
     `storage`, through lf_evoformer_stack."""
     import torch
@@ -449,7 +449,7 @@ def evoformer_stack_config4(ctx, D, synthetic, reps, storage="f32"):
 
 
 def pairformer_block_config5(ctx, D, synthetic, reps, storage="f32"):
-    """BASELINE config 5 at one block: an AF3 Pairformer block at N_tokens=1024, c_z=128,
+    """The AF3 Pairformer workload at one block: N_tokens=1024, c_z=128,
     c_s=384, int5 weights (fp16 scale and zero, groups of 32), bf16 activations, the last 32
     tokens padded."""
     import torch

@@ -27,8 +27,8 @@ namespace lf {
 
 constexpr int FA_DP = 32;       // padded head dim (d <= 32); 16 for d <= 16 (the kernel's DP)
 constexpr int FA_QPB = 128;     // queries per block (8 / QT waves of QT 16-query tiles)
-// 16-query tiles per wave, with and without a pair bias: one (two measured 60% slower at
-// config 3: 155 VGPRs, half the waves)
+// 16-query tiles per wave, with and without a pair bias: one (two measured 60% slower for
+// triangle attention at N = 512: 155 VGPRs, half the waves)
 constexpr int FA_QT_BIAS = 1, FA_QT_PLAIN = 1;
 constexpr int FA_KC = 64;       // keys per chunk
 constexpr int FA_VLD = FA_KC + 8, FA_BLD = FA_KC + 8;
@@ -294,8 +294,8 @@ __global__ __launch_bounds__(64 * (8 / QT)) void flash_kernel(FlashParams p) {
   // on 16x16x32 MFMAs (8 a lane), two O tiles.  o[NDT] holds the row sums.
   constexpr int KLD = DP + 8, NDT = DP / 16, SEGS = DP / 8;
   using QF = typename std::conditional<DP == 32, h8, h4>::type;
-  // (BL, the default with a bias: config 4's row attention 0.30 -> 0.276 ms and triangle
-  // attention 0.106 -> 0.098 ms per launch, config 3 -1%, config 5 unchanged)
+  // (BL, the default with a bias: MSA row attention at 512 x 384 0.30 -> 0.276 ms and triangle
+  // attention at N = 384 0.106 -> 0.098 ms per launch, N = 512 -1%, N = 1024 unchanged)
   // per buffer: K rows [64][KLD], then V^T rows [DP][FA_VLD]
   __shared__ __attribute__((aligned(16))) _Float16 KV[2][FA_KC * KLD + DP * FA_VLD];
   // BL: the block's pair-bias tile of each chunk, [128 queries][64 keys] at pitch FA_BLD

@@ -743,7 +743,7 @@ __global__ __launch_bounds__(64 * NWV) void rowgemm_res_kernel(RowGemmParams p) 
 // launched block must be resident together).
 template <int DACT, int KS, int NP>
 static void launch_rowgemm_res(lf_context* ctx, const RowGemmParams& p) {
-  constexpr int NWV = 8;   // 12 measured no faster at config 4, 16 slower
+  constexpr int NWV = 8;   // 12 measured no faster in the N = 384 Evoformer block, 16 slower
   static const int per_cu = [] {
     int n = 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, rowgemm_res_kernel<DACT, KS, NP, NWV>, 64 * NWV, 0) !=

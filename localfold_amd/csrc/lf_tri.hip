@@ -481,7 +481,7 @@ __global__ __launch_bounds__(256, TM == 128 ? 2 : 3) void tri_contract_dma_kerne
 // work of 128-row ones; rows past N clamped as above): 256 x 256 tiles, 8 waves in a 2 x 4 grid, each
 // wave 128 x 64 (32 accumulator tiles), the same direct-to-LDS double buffering as above in
 // two 64 KB stages (one block per CU).  A wave's K step reads 384 bytes of LDS per MFMA
-// instead of the 64 x 64 tile's 512.  Measured at N = 1024 (config-5 shape, same box,
+// instead of the 64 x 64 tile's 512.  Measured at N = 1024 (same box,
 // alternating runs): 0.373 -> 0.306 ms per contraction.  Four 32-wide stages in the same LDS
 // measured 0.38 ms (twice the barriers).
 
@@ -960,7 +960,7 @@ constexpr float TRI_NLOG2E = -1.4426950408889634f;
 constexpr int TRI_P_NWV = 12, TRI_P_TPW = 1;
 // waves per block of the output kernel: 12 (three per SIMD, one X buffer each) for 2-byte
 // activations; f32 rows need more registers than three waves per SIMD leave, so 8 (two X
-// buffers each).  Measured at config 2: 43.9 -> 39.9 us with 12 waves for bf16, while f32 at
+// buffers each).  Measured at N = 384: 43.9 -> 39.9 us with 12 waves for bf16, while f32 at
 // 12 waves spills and is 4-7% slower than at 8.
 template <int ACT>
 constexpr int tri_o_nwv() { return ACT == DT_F32 ? 8 : 12; }

@@ -1,5 +1,5 @@
 """Synthetic inputs: the reference's deterministic generator, its synthetic weight builders,
-its weight quantisers, and the BASELINE workload definitions.
+its weight quantisers, and the benchmark workload definitions.
 
 This is the equivalent of the reference's testing/tooling surface
 (`webgpu/testing/deterministic-input.js`, `tools/gpu/af2-synthetic-block.js`,
@@ -53,7 +53,7 @@ class Stream:
     def normal(self, count: int, std: float = 1.0) -> np.ndarray:
         """Box-Muller over consecutive draw pairs: z = sqrt(-2 ln(1-u1)) cos(2 pi u2).
 
-        The reference has no normal sampler; this is the transform the BASELINE configs
+        The reference has no normal sampler; this is the transform the benchmark workloads
         (`~N(0, s)`) are generated with here, stated so a fixture can be reproduced.
         """
         pairs = self.uniform(2 * count).reshape(count, 2)
@@ -276,7 +276,7 @@ def pack_bits(codes: np.ndarray, bits: int = 5) -> np.ndarray:
     return np.concatenate([packed, np.zeros(1, np.uint8)])
 
 def quantise_per_channel(values: np.ndarray, out_axis: int, bits: int, symmetric: bool):
-    """Per-output-channel quantisation: one group per output column.
+    """Per-output-channel quantisation (the headline triangle workload's): one group per output column.
 
     Same rounding rules as the flat quantisers (scale/zero rounded to f16 before the codes
     are chosen).  Returns codes in the stored (flattened) order and per-channel tables.
@@ -365,7 +365,7 @@ def af3_tri_weights(c, seed):
 
 
 def config2_inputs(n=384, c=128, seed=2, masked_tail=16):
-    """z ~N(0,1), weights N(0,1/fan_in) masters quantised int5 per output channel,
+    """Headline triangle workload: z ~N(0,1), weights N(0,1/fan_in) masters quantised int5 per output channel,
     mask ones except the last `masked_tail` residues (rows and columns)."""
     s = Stream(seed)
     z = s.normal(n * n * c).reshape(n, n, c)
@@ -475,7 +475,7 @@ def synthetic_msa_module_weights(c_m: int = 64, c_z: int = 128, heads: int = 8, 
 
 
 def config3_attention_weights(c: int, heads: int, seed: int) -> dict:
-    """BASELINE config 3 triangle-attention weights: N(0, 1/fan_in) masters, LN scale ~1."""
+    """Triangle-attention workload weights: N(0, 1/fan_in) masters, LN scale ~1."""
     s = Stream(seed)
     r = 1.0 / np.sqrt(c)
     att = {"queryNormScale": s.values(c, 0.2, 1), "queryNormOffset": s.values(c, 0.1),
@@ -488,7 +488,7 @@ def config3_attention_weights(c: int, heads: int, seed: int) -> dict:
 
 
 def config1_inputs(seed: int = 0, n: int = 64, c_m: int = 256, c_z: int = 128):
-    """one AF2 Evoformer block, N_res=64, N_seq=1, fp32 weights ~N(0,1/fan_in)
+    """CPU-path workload: one AF2 Evoformer block, N_res=64, N_seq=1, fp32 weights ~N(0,1/fan_in)
     (LN scales/offsets as `syntheticBlockWeights`), msa/pair ~N(0,1).  Returns (weights, msa, pair)."""
     w = synthetic_block_weights(c_m=c_m, c_z=c_z, c_outer=32, heads_msa=8, heads_pair=4, tri_hidden=128,
                                 msa_hidden=4 * c_m, pair_hidden=4 * c_z, seed=seed + 1)
@@ -521,7 +521,7 @@ def quantise_tree(w: dict, dtype: str, block: int = 64) -> dict:
 
 
 def config3_inputs(n: int = 512, c: int = 128, heads: int = 4, seed: int = 33):
-    """fp16 pair ~N(0,1), fp16 weights ~N(0,1/fan_in) for starting and ending
+    """Triangle-attention workload: fp16 pair ~N(0,1), fp16 weights ~N(0,1/fan_in) for starting and ending
     node attention, key padding with the last 5% of residues masked (rows and columns)."""
     s = Stream(seed)
     pair = s.normal(n * n * c).reshape(n, n, c)
@@ -540,7 +540,7 @@ def config3_inputs(n: int = 512, c: int = 128, heads: int = 4, seed: int = 33):
 
 def config4_inputs(n: int = 384, sequences: int = 512, c_m: int = 256, c_z: int = 128, seed: int = 4,
                    block: int = 64):
-    """BASELINE config 4, one block's inputs: an MSA of random tokens over 21 classes (gap
+    """AF2 Evoformer workload, one block's inputs: an MSA of random tokens over 21 classes (gap
     probability 0.2, the first row the gap-free query) embedded through a random N(0,1) table,
     pair ~N(0,1), block weights ~N(0,1/fan_in) quantised to int8 with fp16 scales (flat groups
     of `block`).  Masks are all ones (no padding)."""

@@ -13,7 +13,7 @@ localfold_amd/synthetic.py; this module only reads records back, independently.
 * float16: `shared/weights/dtype.js:391-395`.
 
 Besides the reference's flat-group map (group = flat_index // block) this module also
-builds the per-output-channel map that BASELINE config 2 names ("per-output-channel fp16
+builds the per-output-channel map that the headline triangle workload uses ("per-output-channel fp16
 scales"): group = output column.  Both decode with the same `code*scale(+zero)`.
 
 The decoder computes `code*scale + zero` exactly and rounds once to float32, as the

@@ -1,7 +1,7 @@
 """Gated attention on the GPU through the C ABI against the oracle: MSA row attention with a
 separate pair bias, column attention, triangle attention (starting / ending, bias from the
 normalised input), AF3 grid and single attention; activation and weight dtypes; full-size
-BASELINE config 3 (checked on a sample of batch rows)."""
+N = 512 workload (checked on a sample of batch rows)."""
 import numpy as np
 import pytest
 
@@ -288,7 +288,7 @@ def test_fully_masked_row_is_finite(ctx, blockw):
 
 
 def test_config3_full_size_sampled(ctx):
-    """N=512, c_z=128, 4x32 heads, fp16 pair ~N(0,1), fp16 weights, last 26
+    """The triangle-attention workload: N=512, c_z=128, 4x32 heads, fp16 pair ~N(0,1), fp16 weights, last 26
     residues masked; starting then ending node, checked on 3 batch rows each."""
     import torch
     from localfold_amd import capi, device as D

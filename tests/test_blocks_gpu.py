@@ -1,5 +1,5 @@
 """AF2 Evoformer block / stack and AF3 Pairformer block on the GPU through the C ABI, against
-the oracle's block composition; BASELINE config 1 at full size."""
+the oracle's block composition; the CPU-path block (N_res = 64, N_seq = 1) at full size."""
 import numpy as np
 import pytest
 
@@ -122,7 +122,7 @@ def test_evoformer_stack_mask_tables_follow_the_masks(ctx):
 
 
 def test_config1_af2_block_full_size(ctx):
-    """one AF2 block, N_res=64, N_seq=1, c_m 256, c_z 128, fp32 weights
+    """The CPU-path workload: one AF2 block, N_res=64, N_seq=1, c_m 256, c_z 128, fp32 weights
     ~N(0, 1/fan_in), activations ~N(0, 1), seed 0."""
     import torch
     from localfold_amd import device as D

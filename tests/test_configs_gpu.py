@@ -1,4 +1,5 @@
-"""BASELINE configs 4 and 5 on the GPU through the C ABI, against the oracle.
+"""The Evoformer (N_res = 384, N_seq = 512) and Pairformer (N = 1024) workloads on the GPU through
+the C ABI, against the oracle.
 
 Config 4: one AF2 Evoformer block at full size (N_res = 384, N_seq = 512, int8 weights in
 groups of 64), and the 48-block stack at a reduced shape (48 distinct int8 weight sets).

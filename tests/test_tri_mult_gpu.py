@@ -105,7 +105,7 @@ def test_accumulate_in_place(ctx):
 
 
 def test_config2_full_size(ctx):
-    """BASELINE config 2 at full size: N=384, int5 per-output-channel weights, bf16 pair,
+    """The headline workload at full size: N=384, int5 per-output-channel weights, bf16 pair,
     last 16 residues masked; outgoing then incoming, each against the oracle."""
     import torch
     c2 = H.config2_inputs()
