@@ -90,6 +90,21 @@ def test_af3_dialect(ctx, direction, divide, n):
     H.assert_close(out, ref, label=f"af3/{direction}/{divide}")
 
 
+def test_af3_dialect_large_contraction_tiles(ctx):
+    """AF3 at N = 768 (incoming, divided by the length, bf16 pair): the split projection of
+    the interleaved tensors feeding the 256 x 256-tile contraction; against the oracle."""
+    import torch
+    n, c = 768, 128
+    w = H.af3_tri_weights(c, 23)
+    z = S.Stream(79).normal(n * n * c).reshape(n, n, c)
+    mask = np.ones((n, n), np.float32)
+    mask[-8:, :] = 0
+    mask[:, -8:] = 0
+    out, zin = _run(ctx, z, mask, w, "incoming", dialect=1, act=torch.bfloat16, divide=True)
+    ref = ops.tri_mult_af3(zin, mask, w, "incoming", divide_by_length=True)
+    H.assert_close(out, ref, max_abs=2e-2, label="af3/768/incoming")
+
+
 def test_accumulate_in_place(ctx):
     import torch
     from localfold_amd import device as D
